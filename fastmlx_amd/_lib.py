@@ -1,0 +1,79 @@
+"""Loader for libfmxq.so, the HIP library behind every op in this package.
+
+There is no CPU fallback: if the library is missing or a call fails, the
+caller gets an exception.  ``load()`` resolves every symbol the C headers
+declare, so a stale or partial build fails at load time, not mid-run.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libfmxq.so")
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_bool = ctypes.c_bool
+
+# name -> (restype, argtypes); the raw kernel ABI of include/fmxq.h
+FMXQ_SYMBOLS = {
+    "fmxq_version": (_int, []),
+    "fmxq_last_error": (ctypes.c_char_p, []),
+    "fmxq_dequantize": (_int, [_p, _p, _p, _p, _i64, _i64, _int, _int, _p]),
+    "fmxq_quantized_matmul": (_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _bool, _int, _int, _p]),
+    "fmxq_quantized_matmul_bias": (_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _bool, _int,
+                                          _int, _p]),
+    "fmxq_gather_qmm": (_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
+                               _i64, _bool, _int, _int, _bool, _p]),
+    "fmxq_device_error": (_int, [_p]),
+}
+
+STATUS = {
+    0: "FMXQ_OK",
+    1: "FMXQ_ERR_INVALID_ARGUMENT",
+    2: "FMXQ_ERR_UNSUPPORTED",
+    3: "FMXQ_ERR_SHAPE",
+    4: "FMXQ_ERR_INDEX",
+    5: "FMXQ_ERR_DEVICE",
+}
+
+_lib = None
+
+
+class FmxqError(RuntimeError):
+    """A libfmxq call returned a nonzero status."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"{STATUS.get(code, code)}: {message}")
+        self.code = code
+
+
+def all_symbols() -> dict:
+    return dict(FMXQ_SYMBOLS)
+
+
+def load(path: str | None = None):
+    """Load libfmxq.so and bind every declared symbol (raises if any is missing)."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = path or LIB_PATH
+    if not os.path.exists(p):
+        raise FileNotFoundError(
+            f"{p} is missing: build it with `python -m fastmlx_amd.build` (no CPU fallback exists)")
+    lib = ctypes.CDLL(p)
+    for name, (res, args) in all_symbols().items():
+        fn = getattr(lib, name)  # AttributeError if the build lacks the symbol
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        msg = load().fmxq_last_error()
+        raise FmxqError(rc, msg.decode() if msg else "")

@@ -1,0 +1,50 @@
+// fmxq_internal.hpp -- launchers shared between the kernel files and the C ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fmxq {
+
+// Arguments common to every dense quantized product y = x . deq(W)^T.
+struct QmmArgs {
+  const uint16_t* x;        // [M, K] bf16 (row stride ldx elements)
+  const uint32_t* w;        // [N, K*bits/32]
+  const uint16_t* scales;   // [N, K/group]
+  const uint16_t* biases;   // [N, K/group]
+  const uint16_t* bias;     // optional additive bias [N] (qlinearBias), may be null
+  uint16_t* y;              // [M, N] bf16 (row stride ldy elements)
+  int64_t M, N, K;
+  int64_t ldx, ldy;
+  int group_size, bits;
+};
+
+// Gathered product over `batch` items of Mx rows:
+//   y[i] = x[xi(i)] . deq(W[rhs[i]])^T,  xi(i) = lhs ? lhs[i] : i / lhs_div.
+// A slot is one (item, row) pair; slot s = item * Mx + row is output row s.
+struct GatherArgs {
+  const uint16_t* x;        // [x_batch, Mx, K]
+  const uint32_t* w;        // [E, N, K*bits/32]
+  const uint16_t* scales;   // [E, N, K/group]
+  const uint16_t* biases;   // [E, N, K/group]
+  const uint32_t* lhs;      // [batch] or null
+  const uint32_t* rhs;      // [batch]
+  uint16_t* y;              // [batch, Mx, N]
+  int64_t batch, x_batch, lhs_div, Mx, N, K, E;
+  int group_size, bits;
+  uint32_t* err_flag;       // set to 1 by a kernel that meets an out-of-range index
+};
+
+hipError_t launch_dequantize(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                             uint16_t* out, int64_t rows, int64_t K, int group_size, int bits,
+                             hipStream_t stream);
+
+// Bandwidth-bound decode GEMV, M <= kQmvMaxM.
+constexpr int kQmvMaxM = 4;
+hipError_t launch_qmv(const QmmArgs& a, hipStream_t stream);
+
+// MFMA GEMM for larger M.
+hipError_t launch_qmm(const QmmArgs& a, hipStream_t stream);
+
+hipError_t launch_gather_qmv(const GatherArgs& a, hipStream_t stream);
+
+}  // namespace fmxq

@@ -1,0 +1,97 @@
+"""torch-facing wrappers over the raw C ABI (include/fmxq.h).
+
+Tensors are device buffers only: bf16 values travel as ``torch.bfloat16`` or
+``torch.int16``/``torch.uint16`` bit patterns, packed weights as ``torch.int32``
+or ``torch.uint32``, indices as ``torch.int32``/``torch.uint32``.  Every call
+is enqueued on torch's current HIP stream.  Nothing here computes on the CPU.
+"""
+from __future__ import annotations
+
+import torch
+
+from ._lib import check, load
+
+_BF16_LIKE = (torch.bfloat16, torch.int16, torch.uint16)
+_U32_LIKE = (torch.int32, torch.uint32)
+
+
+def _dev(t: torch.Tensor, name: str, dtypes) -> int:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must live on the GPU (got {t.device})")
+    if t.dtype not in dtypes:
+        raise TypeError(f"{name} has dtype {t.dtype}, expected one of {dtypes}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t.data_ptr()
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def dequantize(w, scales, biases, group_size: int = 64, bits: int = 4, out=None):
+    """MLX dequantize: [..., K*bits/32] packed -> [..., K] bf16."""
+    K = w.shape[-1] * 32 // bits
+    rows = w.numel() // max(w.shape[-1], 1)
+    if out is None:
+        out = torch.empty(*w.shape[:-1], K, dtype=torch.bfloat16, device=w.device)
+    check(load().fmxq_dequantize(_dev(w, "w", _U32_LIKE), _dev(scales, "scales", _BF16_LIKE),
+                                 _dev(biases, "biases", _BF16_LIKE), _dev(out, "out", _BF16_LIKE),
+                                 rows, K, group_size, bits, _stream(w)))
+    return out
+
+
+def quantized_matmul(x, w, scales, biases, transpose: bool = True, group_size: int = 64,
+                     bits: int = 4, bias=None, out=None):
+    """y = x @ deq(W)^T over x [..., K]; W [N, K*bits/32]; y [..., N] bf16."""
+    K = x.shape[-1]
+    N = w.shape[0]
+    M = x.numel() // max(K, 1)
+    if w.shape[-1] * 32 // bits != K:
+        raise ValueError(f"x has K={K} but w packs {w.shape[-1] * 32 // bits} values per row")
+    if out is None:
+        out = torch.empty(*x.shape[:-1], N, dtype=torch.bfloat16, device=x.device)
+    lib = load()
+    args = (_dev(x, "x", _BF16_LIKE), _dev(w, "w", _U32_LIKE),
+            _dev(scales, "scales", _BF16_LIKE), _dev(biases, "biases", _BF16_LIKE))
+    if bias is None:
+        check(lib.fmxq_quantized_matmul(*args, _dev(out, "out", _BF16_LIKE), M, N, K, transpose,
+                                        group_size, bits, _stream(x)))
+    else:
+        check(lib.fmxq_quantized_matmul_bias(*args, _dev(bias, "bias", _BF16_LIKE),
+                                             _dev(out, "out", _BF16_LIKE), M, N, K, transpose,
+                                             group_size, bits, _stream(x)))
+    return out
+
+
+def gather_qmm(x, w, scales, biases, rhs_indices, lhs_indices=None, lhs_div: int = 1,
+               transpose: bool = True, group_size: int = 64, bits: int = 4,
+               sorted_indices: bool = False, out=None):
+    """Flat-index gather_qmm (raw ABI form).
+
+    x [x_batch, Mx, K]; w [E, N, K*bits/32]; rhs_indices [batch];
+    lhs_indices [batch] or None (then item i reads x[i // lhs_div]).
+    Returns y [batch, Mx, N]."""
+    if x.dim() != 3:
+        raise ValueError("x must be [x_batch, Mx, K] in the flat form")
+    x_batch, Mx, K = x.shape
+    E, N = w.shape[0], w.shape[1]
+    batch = rhs_indices.numel()
+    if out is None:
+        out = torch.empty(batch, Mx, N, dtype=torch.bfloat16, device=x.device)
+    lhs_ptr = None if lhs_indices is None else _dev(lhs_indices, "lhs_indices", _U32_LIKE)
+    check(load().fmxq_gather_qmm(_dev(x, "x", _BF16_LIKE), _dev(w, "w", _U32_LIKE),
+                                 _dev(scales, "scales", _BF16_LIKE),
+                                 _dev(biases, "biases", _BF16_LIKE), lhs_ptr,
+                                 _dev(rhs_indices, "rhs_indices", _U32_LIKE),
+                                 _dev(out, "out", _BF16_LIKE), batch, x_batch, lhs_div, Mx, N, K,
+                                 E, transpose, group_size, bits, sorted_indices, _stream(x)))
+    return out
+
+
+def device_error(device=None) -> None:
+    """Raise FmxqError(FMXQ_ERR_INDEX) if a gather met an out-of-range index."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else device
+    check(load().fmxq_device_error(torch.cuda.current_stream(dev).cuda_stream))

@@ -1,0 +1,102 @@
+/*
+ * fmxq.h -- C ABI of the MI355X quantized-linear library (libfmxq.so).
+ *
+ * Kernel-level entry points: plain device pointers, element counts and a HIP
+ * stream (hipStream_t passed as void*, NULL = the null stream).  Every call is
+ * asynchronous on that stream and returns an fmxq_status; a nonzero status
+ * means nothing was enqueued, and fmxq_last_error() describes why.
+ *
+ * Each entry replaces one mlx-c call the reference binds through cgo:
+ *   fmxq_quantized_matmul  <- mlx_quantized_matmul  (mlxgo/binding_cgo.go:636-643)
+ *   fmxq_gather_qmm        <- mlx_gather_qmm        (mlxgo/binding_cgo.go:645-673)
+ *   fmxq_dequantize        <- mlx_dequantize        (mlxgo/binding_cgo.go:675-682)
+ * The array-handle layer with mlx-c's exact argument lists is in fmx.h.
+ *
+ * Data layout (MLX affine quantization):
+ *   x       [M, K] bf16 (uint16 bit patterns), row-major
+ *   w       [N, K*bits/32] uint32, LSB-first packing (32/bits values per word)
+ *   scales  [N, K/group_size] bf16;  biases [N, K/group_size] bf16
+ *   y       [M, N] bf16
+ * Supported: bits in {4, 8}, group_size in {32, 64, 128}, K a multiple of
+ * group_size, transpose = true.  Anything else returns FMXQ_ERR_UNSUPPORTED
+ * rather than a wrong answer (the oQ policy in quant/oq.go:21-27 can emit 2/3/5/6
+ * bits; those are rejected).
+ * All pointers must be 16-byte aligned, and rows of x must be 16-byte aligned
+ * (K % 8 == 0 holds for every supported K).
+ */
+#ifndef FMXQ_H
+#define FMXQ_H
+
+#include <stdbool.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  FMXQ_OK = 0,
+  FMXQ_ERR_INVALID_ARGUMENT = 1, /* null pointer, negative size, misalignment */
+  FMXQ_ERR_UNSUPPORTED = 2,      /* bits / group_size / transpose combination */
+  FMXQ_ERR_SHAPE = 3,            /* sizes that do not fit together */
+  FMXQ_ERR_INDEX = 4,            /* an index out of range (reported by fmxq_device_error) */
+  FMXQ_ERR_DEVICE = 5            /* a HIP runtime error */
+} fmxq_status;
+
+/* Library version, major*10000 + minor*100 + patch. */
+int fmxq_version(void);
+
+/* Text of the most recent failure in this process (any thread).  The pointer
+ * stays valid until the next failing call. */
+const char* fmxq_last_error(void);
+
+/* w = scale * q + bias per group of group_size along K, written as bf16:
+ * out [rows, K].  Rounding: bf16(bf16(q * s) + b), both to nearest-even --
+ * MLX's CPU composition multiply(q, scales) then add(., biases).
+ * Replaces mlx_dequantize (mlxgo/binding_cgo.go:675-682). */
+int fmxq_dequantize(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                    uint16_t* out, int64_t rows, int64_t K, int group_size, int bits,
+                    void* stream);
+
+/* y [M, N] = x [M, K] . deq(W)^T, fp32 accumulation, bf16 output.
+ * transpose must be true (the only value the reference passes, quant.go:98).
+ * Replaces mlx_quantized_matmul (mlxgo/binding_cgo.go:636-643). */
+int fmxq_quantized_matmul(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
+                          const uint16_t* biases, uint16_t* y, int64_t M, int64_t N,
+                          int64_t K, bool transpose, int group_size, int bits, void* stream);
+
+/* qlinearBias (compute/models/quant.go:105-111): quantized_matmul followed by a
+ * broadcast add of the additive bias [N] (bf16), fused into the epilogue with
+ * the op chain's rounding: bf16(bf16(x . deq(W)^T) + bias).  bias may be NULL. */
+int fmxq_quantized_matmul_bias(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
+                               const uint16_t* biases, const uint16_t* bias, uint16_t* y,
+                               int64_t M, int64_t N, int64_t K, bool transpose,
+                               int group_size, int bits, void* stream);
+
+/* gather_qmm over a stacked expert weight W [E, N, K*bits/32] (scales/biases
+ * [E, N, K/group_size]).  The output has `batch` items of Mx rows each:
+ *     y[i] (Mx x N) = x[xi] (Mx x K) . deq(W[rhs_indices[i]])^T
+ * with xi = lhs_indices[i] when lhs_indices is non-NULL, else xi = i / lhs_div
+ * (lhs_div = 1 is the identity; lhs_div = top_k is SwitchGLU's broadcast of one
+ * token row against its top_k experts, switch_glu.go:122-130).  x holds x_batch
+ * items.  Index arrays are uint32 (int32 bit patterns are accepted; negative
+ * values count as out of range).  sorted_indices is a locality hint and never
+ * changes the result.  An out-of-range index writes zeros for that item and
+ * raises the device error flag read by fmxq_device_error.
+ * Replaces mlx_gather_qmm (mlxgo/binding_cgo.go:645-673). */
+int fmxq_gather_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
+                    const uint16_t* biases, const uint32_t* lhs_indices,
+                    const uint32_t* rhs_indices, uint16_t* y, int64_t batch, int64_t x_batch,
+                    int64_t lhs_div, int64_t Mx, int64_t N, int64_t K, int64_t E,
+                    bool transpose, int group_size, int bits, bool sorted_indices,
+                    void* stream);
+
+/* Synchronizes `stream`, then reports (and clears) the device-side error flag
+ * that gather kernels raise on an out-of-range index: returns FMXQ_OK or
+ * FMXQ_ERR_INDEX. */
+int fmxq_device_error(void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FMXQ_H */

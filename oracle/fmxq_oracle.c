@@ -1,0 +1,304 @@
+/*
+ * fmxq_oracle.c -- CPU restatement of the quantized-linear path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see fmxq_oracle.h): imported by tests/, by
+ * __graft_entry__.smoke() and by the cpu_baseline leg of bench.py, never by the
+ * product library.
+ *
+ * The arithmetic lives in MLX/mlx-c, which the reference binds but does not
+ * vendor (mlxgo/binding_cgo.go:19-23 links -lmlxc -lmlx; no third_party/ and
+ * no version pin in go.mod:1-3).  The semantics restated here are the ones the
+ * reference's call sites and stub documentation fix:
+ *   - packing: 32/bits values per uint32, LSB first; [out, in*bits/32] words
+ *     (compute/models/switch_glu_test.go:123-163, "8 int4 values per uint32")
+ *   - dequantize: w = scale * q + bias per group along the input axis
+ *     (mlxgo/binding_stub.go:312-318, compute/models/quant.go:117-142)
+ *   - quantized_matmul with transpose=true: y = x . deq(W)^T
+ *     (compute/models/quant.go:91-101, mlxgo/binding_cgo.go:636-643)
+ *   - gather_qmm: per-row expert selection by rhs indices
+ *     (compute/models/switch_glu.go:179-186, mlxgo/binding_cgo.go:645-673)
+ *   - SwitchGLU: silu(gate) * up then down, silu = x * sigmoid(x)
+ *     (compute/models/switch_glu.go:107-153, qwen3_forward.go:229-239)
+ * Build with -ffp-contract=off so every a*b+c below rounds the way it reads.
+ */
+#include "fmxq_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+float oracle_bf16_to_f32(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+/* Round to nearest, ties to even; NaN stays a quiet NaN. */
+uint16_t oracle_f32_to_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+static inline float r16(float f) { return oracle_bf16_to_f32(oracle_f32_to_bf16(f)); }
+
+uint32_t oracle_unpack(const uint32_t *row_words, int64_t k, int bits) {
+  const int per = 32 / bits;
+  const uint32_t word = row_words[k / per];
+  return (word >> ((k % per) * bits)) & ((1u << bits) - 1u);
+}
+
+static int supported(int group_size, int bits, int64_t K) {
+  if (bits != 4 && bits != 8) return 0;
+  if (group_size != 32 && group_size != 64 && group_size != 128) return 0;
+  if (K <= 0 || K % group_size != 0) return 0;
+  return 1;
+}
+
+/* One dequantized element as fp32 (exactly a bf16 value). */
+static inline float deq_elem(uint32_t q, uint16_t s16, uint16_t b16, int mode) {
+  const float s = oracle_bf16_to_f32(s16), b = oracle_bf16_to_f32(b16);
+  if (mode == ORACLE_DEQ_MLX) {
+    /* multiply(q, scales) -> bf16, then add(., biases) -> bf16 */
+    return r16(r16((float)q * s) + b);
+  }
+  return r16((float)q * s + b);
+}
+
+static void deq_row(const uint32_t *wrow, const uint16_t *srow,
+                    const uint16_t *brow, float *out, int64_t K, int group_size,
+                    int bits, int mode) {
+  for (int64_t k = 0; k < K; ++k) {
+    const int64_t g = k / group_size;
+    out[k] = deq_elem(oracle_unpack(wrow, k, bits), srow[g], brow[g], mode);
+  }
+}
+
+int oracle_dequantize(const uint32_t *w, const uint16_t *scales,
+                      const uint16_t *biases, uint16_t *out, int64_t rows,
+                      int64_t K, int group_size, int bits, int mode) {
+  if (!supported(group_size, bits, K) || rows < 0) return -1;
+  const int64_t wpr = K * bits / 32, gpr = K / group_size;
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int64_t k = 0; k < K; ++k) {
+      const int64_t g = k / group_size;
+      out[r * K + k] = oracle_f32_to_bf16(
+          deq_elem(oracle_unpack(w + r * wpr, k, bits), scales[r * gpr + g],
+                   biases[r * gpr + g], mode));
+    }
+  }
+  return 0;
+}
+
+int oracle_qmm_f32(const uint16_t *x, const uint32_t *w, const uint16_t *scales,
+                   const uint16_t *biases, uint16_t *y, float *y_f32,
+                   int64_t M, int64_t N, int64_t K, int group_size, int bits,
+                   int mode) {
+  if (!supported(group_size, bits, K) || M < 0 || N < 0) return -1;
+  const int64_t wpr = K * bits / 32, gpr = K / group_size;
+#pragma omp parallel
+  {
+    float *wf = (float *)malloc(sizeof(float) * (size_t)K);
+#pragma omp for schedule(static)
+    for (int64_t n = 0; n < N; ++n) {
+      deq_row(w + n * wpr, scales + n * gpr, biases + n * gpr, wf, K,
+              group_size, bits, mode);
+      for (int64_t m = 0; m < M; ++m) {
+        const uint16_t *xr = x + m * K;
+        float acc = 0.0f;
+        for (int64_t k = 0; k < K; ++k) acc += oracle_bf16_to_f32(xr[k]) * wf[k];
+        if (y) y[m * N + n] = oracle_f32_to_bf16(acc);
+        if (y_f32) y_f32[m * N + n] = acc;
+      }
+    }
+    free(wf);
+  }
+  return 0;
+}
+
+int oracle_qmm_f64(const uint16_t *x, const uint32_t *w, const uint16_t *scales,
+                   const uint16_t *biases, double *y, int64_t M, int64_t N,
+                   int64_t K, int group_size, int bits, int mode) {
+  if (!supported(group_size, bits, K) || M < 0 || N < 0) return -1;
+  const int64_t wpr = K * bits / 32, gpr = K / group_size;
+#pragma omp parallel
+  {
+    float *wf = (float *)malloc(sizeof(float) * (size_t)K);
+#pragma omp for schedule(static)
+    for (int64_t n = 0; n < N; ++n) {
+      deq_row(w + n * wpr, scales + n * gpr, biases + n * gpr, wf, K,
+              group_size, bits, mode);
+      for (int64_t m = 0; m < M; ++m) {
+        const uint16_t *xr = x + m * K;
+        double acc = 0.0;
+        for (int64_t k = 0; k < K; ++k)
+          acc += (double)oracle_bf16_to_f32(xr[k]) * (double)wf[k];
+        y[m * N + n] = acc;
+      }
+    }
+    free(wf);
+  }
+  return 0;
+}
+
+int oracle_gather_qmm(const uint16_t *x, const uint32_t *w,
+                      const uint16_t *scales, const uint16_t *biases,
+                      const int32_t *xrow, const int32_t *expert, uint16_t *y,
+                      int64_t S, int64_t E, int64_t N, int64_t K,
+                      int group_size, int bits, int mode) {
+  if (!supported(group_size, bits, K) || S < 0 || N < 0) return -1;
+  for (int64_t i = 0; i < S; ++i)
+    if (expert[i] < 0 || expert[i] >= E) return -2;
+  const int64_t wpr = K * bits / 32, gpr = K / group_size;
+#pragma omp parallel
+  {
+    float *wf = (float *)malloc(sizeof(float) * (size_t)K);
+#pragma omp for schedule(static)
+    for (int64_t t = 0; t < S * N; ++t) {
+      const int64_t i = t / N, n = t % N;
+      const int64_t e = expert[i];
+      const int64_t row = e * N + n;
+      deq_row(w + row * wpr, scales + row * gpr, biases + row * gpr, wf, K,
+              group_size, bits, mode);
+      const uint16_t *xr = x + (int64_t)xrow[i] * K;
+      float acc = 0.0f;
+      for (int64_t k = 0; k < K; ++k) acc += oracle_bf16_to_f32(xr[k]) * wf[k];
+      y[i * N + n] = oracle_f32_to_bf16(acc);
+    }
+    free(wf);
+  }
+  return 0;
+}
+
+/* One quantized GEMV row against expert e of a stacked projection. */
+static float gemv_row(const float *xv, const uint32_t *w, const uint16_t *s,
+                      const uint16_t *b, int64_t e, int64_t N, int64_t n,
+                      int64_t K, int group_size, int bits, float *wf) {
+  const int64_t wpr = K * bits / 32, gpr = K / group_size;
+  const int64_t row = e * N + n;
+  deq_row(w + row * wpr, s + row * gpr, b + row * gpr, wf, K, group_size, bits,
+          ORACLE_DEQ_MLX);
+  float acc = 0.0f;
+  for (int64_t k = 0; k < K; ++k) acc += xv[k] * wf[k];
+  return acc;
+}
+
+int oracle_switch_glu(const uint16_t *x, const int32_t *inds,
+                      const uint32_t *wg, const uint16_t *sg, const uint16_t *bg,
+                      const uint32_t *wu, const uint16_t *su, const uint16_t *bu,
+                      const uint32_t *wd, const uint16_t *sd, const uint16_t *bd,
+                      uint16_t *out, int64_t T, int64_t topk, int64_t E,
+                      int64_t D, int64_t I, int group_size, int bits,
+                      const int32_t *token_sel, int64_t n_sel) {
+  if (!supported(group_size, bits, D) || !supported(group_size, bits, I)) return -1;
+  const int64_t nt = token_sel ? n_sel : T;
+  for (int64_t j = 0; j < nt; ++j) {
+    const int64_t t = token_sel ? token_sel[j] : j;
+    if (t < 0 || t >= T) return -2;
+    for (int64_t q = 0; q < topk; ++q)
+      if (inds[t * topk + q] < 0 || inds[t * topk + q] >= E) return -2;
+  }
+  const int64_t maxk = D > I ? D : I;
+  for (int64_t j = 0; j < nt; ++j) {
+    const int64_t t = token_sel ? token_sel[j] : j;
+    float *xv = (float *)malloc(sizeof(float) * (size_t)D);
+    float *hv = (float *)malloc(sizeof(float) * (size_t)I);
+    for (int64_t k = 0; k < D; ++k) xv[k] = oracle_bf16_to_f32(x[t * D + k]);
+    for (int64_t q = 0; q < topk; ++q) {
+      const int64_t e = inds[t * topk + q];
+#pragma omp parallel
+      {
+        float *wf = (float *)malloc(sizeof(float) * (size_t)maxk);
+#pragma omp for schedule(static)
+        for (int64_t n = 0; n < I; ++n) {
+          const float g = r16(gemv_row(xv, wg, sg, bg, e, I, n, D, group_size, bits, wf));
+          const float u = r16(gemv_row(xv, wu, su, bu, e, I, n, D, group_size, bits, wf));
+          const float sig = r16(1.0f / (1.0f + expf(-g)));
+          const float silu = r16(g * sig);
+          hv[n] = r16(silu * u);
+        }
+#pragma omp for schedule(static)
+        for (int64_t n = 0; n < D; ++n) {
+          const float d = gemv_row(hv, wd, sd, bd, e, D, n, I, group_size, bits, wf);
+          out[(j * topk + q) * D + n] = oracle_f32_to_bf16(d);
+        }
+        free(wf);
+      }
+    }
+    free(xv);
+    free(hv);
+  }
+  return 0;
+}
+
+/* CPU baseline.  Per row n and group g the product is
+ *   sum_k x_k (s q_k + b) = s * sum_k x_k q_k + b * sum_k x_k,
+ * which is exact algebra; the fp32 sums round differently from the
+ * element-wise form, well inside the parity tolerance.  x is converted to fp32
+ * once and its per-group sums are computed once per row of x. */
+int oracle_qmm_cpu_fast(const uint16_t *x, const uint32_t *w,
+                        const uint16_t *scales, const uint16_t *biases,
+                        uint16_t *y, int64_t M, int64_t N, int64_t K,
+                        int group_size, int bits) {
+  if (!supported(group_size, bits, K) || M < 0 || N < 0) return -1;
+  const int64_t wpr = K * bits / 32, gpr = K / group_size;
+  const int per = 32 / bits;
+  const uint32_t mask = (1u << bits) - 1u;
+  float *xf = (float *)malloc(sizeof(float) * (size_t)(M * K));
+  float *xs = (float *)malloc(sizeof(float) * (size_t)(M * gpr));
+  for (int64_t i = 0; i < M * K; ++i) xf[i] = oracle_bf16_to_f32(x[i]);
+  for (int64_t m = 0; m < M; ++m)
+    for (int64_t g = 0; g < gpr; ++g) {
+      float a = 0.0f;
+      for (int64_t k = 0; k < group_size; ++k) a += xf[m * K + g * group_size + k];
+      xs[m * gpr + g] = a;
+    }
+#pragma omp parallel
+  {
+    float *qf = (float *)malloc(sizeof(float) * (size_t)K);
+#pragma omp for schedule(static)
+    for (int64_t n = 0; n < N; ++n) {
+      const uint32_t *wr = w + n * wpr;
+      for (int64_t i = 0; i < wpr; ++i) {
+        const uint32_t word = wr[i];
+        for (int p = 0; p < per; ++p) qf[i * per + p] = (float)((word >> (p * bits)) & mask);
+      }
+      for (int64_t m = 0; m < M; ++m) {
+        const float *xr = xf + m * K;
+        float acc = 0.0f;
+        for (int64_t g = 0; g < gpr; ++g) {
+          const float *xq = xr + g * group_size;
+          const float *qq = qf + g * group_size;
+          float part[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+          for (int64_t k = 0; k < group_size; k += 8)
+            for (int j = 0; j < 8; ++j) part[j] = fmaf(xq[k + j], qq[k + j], part[j]);
+          const float dot = ((part[0] + part[1]) + (part[2] + part[3])) +
+                            ((part[4] + part[5]) + (part[6] + part[7]));
+          const float s = oracle_bf16_to_f32(scales[n * gpr + g]);
+          const float b = oracle_bf16_to_f32(biases[n * gpr + g]);
+          acc = fmaf(s, dot, fmaf(b, xs[m * gpr + g], acc));
+        }
+        y[m * N + n] = oracle_f32_to_bf16(acc);
+      }
+    }
+    free(qf);
+  }
+  free(xf);
+  free(xs);
+  return 0;
+}
+
+int oracle_num_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}

@@ -1,0 +1,27 @@
+"""Copy the reference's own fixture rows for this path into tests/golden/.
+
+Run here (where /root/reference exists); the GPU box only reads the committed
+JSON.  Source: quant/testdata/oq.json "tensor_bytes", the fixture of
+TestTensorQuantizedBytesParity (quant/oq_test.go:158-165).
+"""
+import json
+import os
+import sys
+
+REF = os.environ.get("FMXQ_REFERENCE", "/root/reference")
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def main() -> int:
+    src = os.path.join(REF, "quant", "testdata", "oq.json")
+    with open(src) as f:
+        data = json.load(f)
+    out = {"source": "quant/testdata/oq.json#tensor_bytes", "tensor_bytes": data["tensor_bytes"]}
+    with open(os.path.join(HERE, "oq_tensor_bytes.json"), "w") as f:
+        json.dump(out, f, indent=1)
+        f.write("\n")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,146 @@
+"""GPU parity: dequantize (bit-exact) and quantized_matmul (tolerance) vs the oracle.
+
+Inputs are seeded numpy tensors shared byte-for-byte by the HIP path and the
+CPU oracle.  Parity metric: max|y - y_ref| / max|y_ref| <= 2e-2 on bf16
+outputs (north star), reported also against the fp64 oracle.
+"""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import announce, to_dev, to_np
+from synth import TOL, make_quant, make_x, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("group", [32, 64, 128])
+def test_dequantize_bit_exact(gpu, oracle, bits, group):
+    rng = np.random.default_rng(100 + bits * 10 + group)
+    N, K = 96, 512
+    w, s, b = make_quant(rng, (N,), K, bits, group)
+    announce(f"dequantize bits={bits} group={group} N={N} K={K}")
+    from fastmlx_amd import ops
+
+    out = ops.dequantize(to_dev(w, gpu), to_dev(s, gpu), to_dev(b, gpu), group, bits)
+    torch.cuda.synchronize()
+    got = to_np(out)
+    ref = oracle.dequantize(w, s, b, group, bits)
+    assert got.shape == ref.shape
+    assert np.array_equal(got, ref), f"{np.count_nonzero(got != ref)} mismatching elements"
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_dequantize_exhaustive_q_and_bf16_sweep(gpu, oracle, bits):
+    """Every q value against a sweep of bf16 scale/bias bit patterns (incl. subnormal,
+    negative, large and tie-producing values): bit-exact with the oracle."""
+    rng = np.random.default_rng(7 + bits)
+    group = 64
+    nq = 1 << bits
+    # bf16 patterns: random over all finite exponents plus specials
+    pats = rng.integers(0, 0x7F80, size=2048, dtype=np.uint32).astype(np.uint16)
+    pats = np.concatenate([pats, pats | 0x8000,
+                           np.array([0x0000, 0x8000, 0x0001, 0x007F, 0x3F80, 0xBF80, 0x4300,
+                                     0x3C00, 0x7F7F, 0xFF7F], dtype=np.uint16)])
+    rows = len(pats)
+    K = group * 4  # four groups per row
+    q = np.tile(np.arange(K, dtype=np.uint32) % nq, (rows, 1))
+    from synth import pack
+
+    w = pack(q, bits)
+    s = np.stack([pats, np.roll(pats, 1), np.roll(pats, 7), pats[::-1]], axis=1).astype(np.uint16)
+    bb = np.stack([np.roll(pats, 3), pats, pats[::-1], np.roll(pats, 11)], axis=1).astype(np.uint16)
+    s = np.ascontiguousarray(s)
+    bb = np.ascontiguousarray(bb)
+    announce(f"dequantize sweep bits={bits} rows={rows}")
+    from fastmlx_amd import ops
+
+    out = ops.dequantize(to_dev(w, gpu), to_dev(s, gpu), to_dev(bb, gpu), group, bits)
+    torch.cuda.synchronize()
+    got = to_np(out)
+    ref = oracle.dequantize(w, s, bb, group, bits)
+    nan_ref = (ref & 0x7FFF) > 0x7F80
+    assert np.array_equal(got[~nan_ref], ref[~nan_ref])
+    assert np.all((got[nan_ref] & 0x7FFF) > 0x7F80)
+
+
+def _qmm_case(gpu, oracle, M, N, K, bits, group, seed, rows_checked=None, bias=False):
+    rng = np.random.default_rng(seed)
+    w, s, b = make_quant(rng, (N,), K, bits, group)
+    x = make_x(rng, M, K)
+    bvec = make_x(rng, N) if bias else None
+    announce(f"quantized_matmul M={M} N={N} K={K} bits={bits} group={group} bias={bias}")
+    from fastmlx_amd import ops
+
+    y = ops.quantized_matmul(to_dev(x, gpu), to_dev(w, gpu), to_dev(s, gpu), to_dev(b, gpu),
+                             True, group, bits, bias=None if bvec is None else to_dev(bvec, gpu))
+    torch.cuda.synchronize()
+    got = to_np(y)
+    sel = np.arange(M) if rows_checked is None else rows_checked
+    xs = np.ascontiguousarray(x[sel])
+    ref16 = oracle.qmm(xs, w, s, b, group, bits)
+    ref64 = oracle.qmm_f64(xs, w, s, b, group, bits)
+    g = oracle.bf16_to_f32(got[sel])
+    r = oracle.bf16_to_f32(ref16)
+    if bvec is not None:
+        bf = oracle.bf16_to_f32(bvec)
+        r = oracle.bf16_to_f32(oracle.f32_to_bf16(r + bf[None, :]))
+        ref64 = ref64 + bf[None, :]
+    e16 = rel_err(g, r)
+    e64 = rel_err(g, ref64)
+    print(f"  rel_err vs fp32 oracle {e16:.3e}, vs fp64 {e64:.3e}")
+    assert e16 <= TOL and e64 <= TOL
+    return e16
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_qmv_config0_shape(gpu, oracle, M, bits):
+    # config 0: 2048x2048, group 64
+    # the decode GEMV works on the exact affine value s*q + b (no bf16 rounding of
+    # the dequantized weight) and sums in another order; it must still meet 2e-2
+    _qmm_case(gpu, oracle, M, 2048, 2048, bits, 64, seed=1000 + M + bits)
+
+
+@pytest.mark.parametrize("group", [32, 128])
+def test_qmv_other_groups(gpu, oracle, group):
+    _qmm_case(gpu, oracle, 1, 384, 1024, 4, group, seed=31 + group)
+    _qmm_case(gpu, oracle, 7, 384, 1024, 8, group, seed=37 + group)
+
+
+@pytest.mark.parametrize("M", [5, 8, 16, 32, 64, 100, 128, 300])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_qmm_mfma_shapes(gpu, oracle, M, bits):
+    _qmm_case(gpu, oracle, M, 1024 + 64, 2048, bits, 64, seed=2000 + M + bits)
+
+
+def test_qmm_ragged_n(gpu, oracle):
+    # N not a multiple of any tile, K a multiple of 32 only
+    _qmm_case(gpu, oracle, 1, 333, 96, 4, 32, seed=5)
+    _qmm_case(gpu, oracle, 37, 333, 96, 4, 32, seed=6)
+    _qmm_case(gpu, oracle, 130, 77, 160, 8, 32, seed=7)
+
+
+@pytest.mark.parametrize("M", [1, 9, 70])
+def test_qlinear_bias_epilogue(gpu, oracle, M):
+    _qmm_case(gpu, oracle, M, 512, 1024, 4, 64, seed=300 + M, bias=True)
+
+
+@pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 14336)])
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M", [1, 5, 64, 512, 2048])
+def test_config2_full_shapes(gpu, oracle, N, K, bits, M):
+    """Config 2 (verify/prefill) at full size; the oracle evaluates a sample of rows."""
+    rows = None if M <= 8 else np.random.default_rng(M).choice(M, size=6, replace=False)
+    if rows is not None:
+        rows = np.sort(np.append(rows, [0, M - 1]))
+    _qmm_case(gpu, oracle, M, N, K, bits, 64, seed=4000 + M + bits + K, rows_checked=rows)
+
+
+def test_zero_sizes_enqueue_nothing(gpu):
+    from fastmlx_amd import _lib
+
+    lib = _lib.load()
+    assert lib.fmxq_quantized_matmul(None, None, None, None, None, 0, 16, 64, True, 64, 4,
+                                     None) == 0

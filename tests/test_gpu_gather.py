@@ -1,0 +1,99 @@
+"""GPU parity: gather_qmm (flat ABI form) vs the oracle."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import announce, to_dev, to_np
+from synth import TOL, make_quant, make_x, rel_err, topk_uniform
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(gpu, x, w, s, b, rhs, lhs=None, lhs_div=1, group=64, bits=4, sorted_indices=False):
+    from fastmlx_amd import ops
+
+    y = ops.gather_qmm(to_dev(x, gpu), to_dev(w, gpu), to_dev(s, gpu), to_dev(b, gpu),
+                       to_dev(rhs.astype(np.uint32), gpu),
+                       None if lhs is None else to_dev(lhs.astype(np.uint32), gpu), lhs_div,
+                       True, group, bits, sorted_indices)
+    torch.cuda.synchronize()
+    return to_np(y)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_switchglu_broadcast_form(gpu, oracle, bits):
+    """x [T,1,K] against top_k experts per token (lhs_div = top_k)."""
+    rng = np.random.default_rng(11 + bits)
+    T, k, E, N, K = 6, 3, 9, 192, 256
+    w, s, b = make_quant(rng, (E, N), K, bits, 64)
+    x = make_x(rng, T, 1, K)
+    inds = topk_uniform(rng, T, E, k)
+    announce(f"gather broadcast bits={bits}")
+    got = _run(gpu, x, w, s, b, inds.reshape(-1), lhs_div=k, bits=bits)
+    ref = oracle.gather_qmm(x.reshape(T, K), w, s, b, np.repeat(np.arange(T), k),
+                            inds.reshape(-1), 64, bits)
+    assert got.shape == (T * k, 1, N)
+    assert rel_err(oracle.bf16_to_f32(got.reshape(T * k, N)), oracle.bf16_to_f32(ref)) <= TOL
+
+
+def test_sorted_hint_does_not_change_result(gpu, oracle):
+    rng = np.random.default_rng(3)
+    S, E, N, K = 80, 8, 128, 512
+    w, s, b = make_quant(rng, (E, N), K, 4, 64)
+    x = make_x(rng, S, 1, K)
+    rhs = np.sort(rng.integers(0, E, size=S)).astype(np.uint32)
+    announce("gather sorted vs unsorted")
+    a = _run(gpu, x, w, s, b, rhs, sorted_indices=True)
+    c = _run(gpu, x, w, s, b, rhs, sorted_indices=False)
+    assert np.array_equal(a, c)
+    ref = oracle.gather_qmm(x.reshape(S, K), w, s, b, np.arange(S), rhs.astype(np.int32))
+    assert rel_err(oracle.bf16_to_f32(a.reshape(S, N)), oracle.bf16_to_f32(ref)) <= TOL
+
+
+def test_explicit_lhs_and_multi_row_items(gpu, oracle):
+    rng = np.random.default_rng(4)
+    xb, Mx, E, N, K = 5, 3, 4, 64, 128
+    w, s, b = make_quant(rng, (E, N), K, 8, 32)
+    x = make_x(rng, xb, Mx, K)
+    lhs = np.array([4, 0, 0, 2, 3, 1, 4], dtype=np.uint32)
+    rhs = np.array([1, 3, 0, 0, 2, 1, 3], dtype=np.uint32)
+    announce("gather explicit lhs, Mx=3")
+    got = _run(gpu, x, w, s, b, rhs, lhs=lhs, group=32, bits=8)
+    xrow = (lhs[:, None].astype(np.int64) * Mx + np.arange(Mx)[None, :]).reshape(-1)
+    ref = oracle.gather_qmm(x.reshape(xb * Mx, K), w, s, b, xrow,
+                            np.repeat(rhs, Mx).astype(np.int32), 32, 8)
+    assert rel_err(oracle.bf16_to_f32(got.reshape(-1, N)), oracle.bf16_to_f32(ref)) <= TOL
+
+
+def test_out_of_range_expert_zeroes_and_flags(gpu):
+    """An expert id >= E never reads outside the stack: zeros plus a device error."""
+    from fastmlx_amd import FmxqError, ops
+
+    rng = np.random.default_rng(5)
+    E, N, K = 4, 64, 128
+    w, s, b = make_quant(rng, (E, N), K, 4, 64)
+    x = make_x(rng, 3, 1, K)
+    rhs = np.array([1, 7, 2], dtype=np.uint32)  # 7 is out of range
+    announce("gather out-of-range id")
+    got = _run(gpu, x, w, s, b, rhs)
+    assert np.all(got[1] == 0)
+    assert np.any(got[0] != 0)
+    with pytest.raises(FmxqError) as ei:
+        ops.device_error()
+    assert ei.value.code == 4
+    ops.device_error()  # cleared
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_config3_expert_projection(gpu, oracle, M):
+    """Config 3 gate projection: 512 experts, 2048 -> 512, top-10 per token."""
+    rng = np.random.default_rng(600 + M)
+    E, N, K, k = 512, 512, 2048, 10
+    w, s, b = make_quant(rng, (E, N), K, 4, 64)
+    x = make_x(rng, M, 1, K)
+    inds = topk_uniform(rng, M, E, k)
+    announce(f"config3 gather M={M}")
+    got = _run(gpu, x, w, s, b, inds.reshape(-1), lhs_div=k)
+    ref = oracle.gather_qmm(x.reshape(M, K), w, s, b, np.repeat(np.arange(M), k),
+                            inds.reshape(-1))
+    assert rel_err(oracle.bf16_to_f32(got.reshape(-1, N)), oracle.bf16_to_f32(ref)) <= TOL

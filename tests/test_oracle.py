@@ -1,0 +1,262 @@
+"""CPU checks that pin the oracle before anything is compared against it.
+
+Each check is chosen so a plausible mistake in the restatement fails it:
+hand-packed words catch a wrong nibble order, closed forms catch a dropped
+scale or bias, exact integer cases catch rounding slips, the independent numpy
+and fp64 restatements catch accumulation or indexing errors, and reductions
+(one-hot x, E=1 gather, linearity) catch transposed operands.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from synth import deq_numpy, make_quant, make_x, pack, rel_err, unpack
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+# ---------------------------------------------------------------- bf16 / packing
+
+def test_bf16_round_to_nearest_even(oracle):
+    f = np.array([1.0, 1.00390625, 1.005859375, 1.0078125, 1.01171875, -2.5, 3.0e38, 1e-40],
+                 dtype=np.float32)
+    # 1 + 2^-8 is a tie -> even (1.0); 1 + 1.5*2^-8 rounds up to 1 + 2^-7
+    want = [0x3F80, 0x3F80, 0x3F81, 0x3F81, 0x3F82, 0xC020, 0x7F62, 0x0001]
+    got = oracle.f32_to_bf16(f)
+    assert [int(v) for v in got] == want
+    for v, w in zip(f, want):
+        assert oracle.lib().oracle_f32_to_bf16(float(v)) == w
+    assert oracle.f32_to_bf16(np.array([np.nan], dtype=np.float32))[0] & 0x7FFF > 0x7F80
+
+
+def test_pack_order_lsb_first(oracle):
+    # element k of a row sits at bit (k % 8) * 4 of word k / 8
+    w = np.array([[0x76543210, 0xFEDCBA98]], dtype=np.uint32)
+    assert unpack(w, 4).tolist() == [list(range(16))]
+    assert [oracle.lib().oracle_unpack(w.ctypes.data_as(__import__("ctypes").c_void_p), k, 4)
+            for k in range(16)] == list(range(16))
+    w8 = np.array([[0x03020100, 0xFFFEFDFC]], dtype=np.uint32)
+    assert unpack(w8, 8).tolist() == [[0, 1, 2, 3, 0xFC, 0xFD, 0xFE, 0xFF]]
+    q = np.arange(64, dtype=np.uint32).reshape(1, 64) % 16
+    assert np.array_equal(unpack(pack(q, 4), 4), q)
+
+
+def _lib_unpack_sig(oracle):
+    import ctypes
+    L = oracle.lib()
+    L.oracle_unpack.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int]
+    L.oracle_unpack.restype = ctypes.c_uint32
+
+
+@pytest.fixture(autouse=True)
+def _sig(oracle):
+    _lib_unpack_sig(oracle)
+
+
+# ---------------------------------------------------------------- dequantize
+
+def test_dequant_closed_forms(oracle):
+    # s = 1, b = 0: dequant returns q exactly
+    K = 64
+    q = (np.arange(K, dtype=np.uint32) % 16).reshape(1, K)
+    w = pack(q, 4)
+    one = np.array([[0x3F80]], dtype=np.uint16)
+    zero = np.array([[0x0000]], dtype=np.uint16)
+    out = oracle.bf16_to_f32(oracle.dequantize(w, one, zero, 64, 4))
+    assert out.tolist() == [q[0].astype(np.float32).tolist()]
+    # s = 0.5, b = -4: q/2 - 4, exact in bf16
+    half = np.array([[0x3F00]], dtype=np.uint16)
+    m4 = np.array([[0xC080]], dtype=np.uint16)
+    out = oracle.bf16_to_f32(oracle.dequantize(w, half, m4, 64, 4))
+    assert out.tolist() == [(q[0] * 0.5 - 4).astype(np.float32).tolist()]
+    # q = 0 -> b; s = 0 -> b
+    rng = np.random.default_rng(0)
+    w0, s0, b0 = make_quant(rng, (8,), 128, 4, 64)
+    zq = np.zeros_like(w0)
+    out = oracle.dequantize(zq, s0, b0, 64, 4)
+    assert np.array_equal(out, np.repeat(b0, 64, axis=1))
+    out = oracle.dequantize(w0, np.zeros_like(s0), b0, 64, 4)
+    assert np.array_equal(out, np.repeat(b0, 64, axis=1))
+
+
+def test_dequant_double_rounding_is_observable(oracle):
+    """The two rounding sequences differ on a hand-built case, so the choice matters.
+
+    s = 1 + 2^-7 (bf16 0x3F81), q = 3: q*s = 3.0234375 -> bf16 3.03125 (tie to even up);
+    b = 2^-6: bf16(3.03125 + 0.015625) = 3.046875, while one rounding of
+    3.0234375 + 0.015625 = 3.0390625 gives 3.03125 (tie to even down)."""
+    w = pack(np.array([[3] + [0] * 63], dtype=np.uint32), 4)
+    s = np.array([[0x3F81]], dtype=np.uint16)
+    b = np.array([[0x3C80]], dtype=np.uint16)
+    mlx = oracle.bf16_to_f32(oracle.dequantize(w, s, b, 64, 4, oracle.DEQ_MLX))[0, 0]
+    fused = oracle.bf16_to_f32(oracle.dequantize(w, s, b, 64, 4, oracle.DEQ_FUSED))[0, 0]
+    assert mlx == np.float32(3.046875)
+    assert fused == np.float32(3.03125)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("group", [32, 64, 128])
+def test_dequant_matches_independent_numpy(oracle, bits, group):
+    rng = np.random.default_rng(bits * group)
+    w, s, b = make_quant(rng, (33,), 512, bits, group)
+    for fused, mode in ((False, oracle.DEQ_MLX), (True, oracle.DEQ_FUSED)):
+        ref = deq_numpy(w, s, b, bits, group, fused=fused)
+        got = oracle.bf16_to_f32(oracle.dequantize(w, s, b, group, bits, mode))
+        assert np.array_equal(got, ref)
+
+
+def test_dequant_vs_fp64_brute_force(oracle):
+    """All q against a sweep of bf16 scales/biases: the MLX sequence is within two
+    half-ulps of the exact value s*q + b -- one relative to q*s (first rounding),
+    one relative to the result (second rounding)."""
+    rng = np.random.default_rng(9)
+    pats = rng.integers(0x3000, 0x4200, size=512).astype(np.uint16)  # moderate magnitudes
+    rows = len(pats)
+    q = np.tile(np.arange(64, dtype=np.uint32) % 16, (rows, 1))
+    w = pack(q, 4)
+    s = pats.reshape(rows, 1)
+    b = np.roll(pats, 5).reshape(rows, 1) ^ np.uint16(0x8000)
+    got = oracle.bf16_to_f32(oracle.dequantize(w, s, b, 64, 4)).astype(np.float64)
+    qs = q * oracle.bf16_to_f32(s).astype(np.float64)
+    exact = qs + oracle.bf16_to_f32(b).astype(np.float64)
+    bound = (np.abs(qs) + np.abs(exact)) * 2.0 ** -8
+    assert np.all(np.abs(got - exact) <= bound * 1.0001 + 1e-38)
+    # and the bound is tight enough to catch a dropped bias or scale
+    assert not np.all(np.abs(qs - exact) <= bound)
+
+
+# ---------------------------------------------------------------- quantized_matmul
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_qmm_vs_fp64_and_numpy(oracle, bits):
+    rng = np.random.default_rng(21 + bits)
+    M, N, K = 3, 40, 256
+    w, s, b = make_quant(rng, (N,), K, bits, 64)
+    x = make_x(rng, M, K)
+    y, yf = oracle.qmm(x, w, s, b, 64, bits, want_f32=True)
+    y64 = oracle.qmm_f64(x, w, s, b, 64, bits)
+    W = deq_numpy(w, s, b, bits, 64).astype(np.float64)
+    ref = oracle.bf16_to_f32(x).astype(np.float64) @ W.T
+    assert np.allclose(y64, ref, rtol=0, atol=1e-9)
+    assert rel_err(yf, ref) < 1e-5
+    assert np.array_equal(y, oracle.f32_to_bf16(yf))
+
+
+def test_qmm_one_hot_selects_a_column(oracle):
+    rng = np.random.default_rng(2)
+    N, K = 16, 128
+    w, s, b = make_quant(rng, (N,), K, 4, 64)
+    W = oracle.dequantize(w, s, b, 64, 4)
+    for k in (0, 5, 63, 64, 127):
+        x = np.zeros((1, K), dtype=np.uint16)
+        x[0, k] = 0x3F80  # 1.0
+        y = oracle.qmm(x, w, s, b, 64, 4)
+        assert np.array_equal(y[0], W[:, k])
+
+
+def test_qmm_matches_torch_matmul(oracle):
+    import torch
+
+    rng = np.random.default_rng(8)
+    M, N, K = 4, 64, 512
+    w, s, b = make_quant(rng, (N,), K, 4, 64)
+    x = make_x(rng, M, K)
+    W = torch.from_numpy(oracle.bf16_to_f32(oracle.dequantize(w, s, b, 64, 4))).double()
+    X = torch.from_numpy(oracle.bf16_to_f32(x)).double()
+    ref = (X @ W.T).numpy()
+    y = oracle.bf16_to_f32(oracle.qmm(x, w, s, b, 64, 4))
+    assert rel_err(y, ref) < 4e-3
+
+
+def test_qmm_linearity(oracle):
+    rng = np.random.default_rng(13)
+    N, K = 24, 256
+    w, s, b = make_quant(rng, (N,), K, 8, 64)
+    x1 = make_x(rng, 1, K)
+    x2 = make_x(rng, 1, K)
+    xs = oracle.f32_to_bf16(oracle.bf16_to_f32(x1) * 2)  # exact doubling
+    _, y1 = oracle.qmm(x1, w, s, b, 64, 8, want_f32=True)
+    _, y2 = oracle.qmm(xs, w, s, b, 64, 8, want_f32=True)
+    assert np.array_equal(y2, y1 * 2)
+    both = np.concatenate([x1, x2])
+    _, yb = oracle.qmm(both, w, s, b, 64, 8, want_f32=True)
+    _, y22 = oracle.qmm(x2, w, s, b, 64, 8, want_f32=True)
+    assert np.array_equal(yb[0], y1[0]) and np.array_equal(yb[1], y22[0])
+
+
+def test_cpu_fast_baseline_within_tolerance(oracle):
+    rng = np.random.default_rng(17)
+    for bits in (4, 8):
+        w, s, b = make_quant(rng, (96,), 1024, bits, 64)
+        x = make_x(rng, 5, 1024)
+        ref = oracle.qmm_f64(x, w, s, b, 64, bits)
+        fast = oracle.bf16_to_f32(oracle.qmm_cpu_fast(x, w, s, b, 64, bits))
+        # the baseline uses the exact affine value s*q + b (no bf16 rounding of the
+        # dequantized weight), so it sits a few 1e-3 away from the bf16-weight product
+        assert rel_err(fast, ref) < 2e-2
+
+
+# ---------------------------------------------------------------- gather / SwitchGLU
+
+def test_gather_single_expert_reduces_to_qmm(oracle):
+    rng = np.random.default_rng(31)
+    N, K = 32, 128
+    w, s, b = make_quant(rng, (1, N), K, 4, 64)
+    x = make_x(rng, 5, K)
+    g = oracle.gather_qmm(x, w, s, b, np.arange(5), np.zeros(5, dtype=np.int32))
+    q = oracle.qmm(x, w[0], s[0], b[0])
+    assert np.array_equal(g, q)
+
+
+def test_gather_picks_expert_slices(oracle):
+    rng = np.random.default_rng(32)
+    E, N, K = 5, 16, 128
+    w, s, b = make_quant(rng, (E, N), K, 4, 64)
+    x = make_x(rng, 3, K)
+    xrow = np.array([2, 0, 1, 2])
+    ex = np.array([4, 1, 1, 0])
+    g = oracle.gather_qmm(x, w, s, b, xrow, ex)
+    for i in range(4):
+        q = oracle.qmm(np.ascontiguousarray(x[xrow[i]:xrow[i] + 1]), w[ex[i]], s[ex[i]], b[ex[i]])
+        assert np.array_equal(g[i], q[0])
+    with pytest.raises(ValueError):
+        oracle.gather_qmm(x, w, s, b, xrow, np.array([0, 1, 5, 0]))
+
+
+def test_switch_glu_is_the_op_chain(oracle):
+    """switch_glu == gather(down, bf16(silu(gate)) * up) with each op rounded."""
+    rng = np.random.default_rng(41)
+    T, k, E, D, I = 3, 2, 4, 128, 64
+    gate = make_quant(rng, (E, I), D, 4, 64)
+    up = make_quant(rng, (E, I), D, 4, 64)
+    down = make_quant(rng, (E, D), I, 4, 64)
+    x = make_x(rng, T, D)
+    inds = np.array([[0, 3], [2, 2 - 1], [3, 0]], dtype=np.int32)
+    out = oracle.switch_glu(x, inds, gate, up, down)
+    xr = np.repeat(np.arange(T), k)
+    ex = inds.reshape(-1)
+    g = oracle.bf16_to_f32(oracle.gather_qmm(x, *gate, xr, ex))
+    u = oracle.bf16_to_f32(oracle.gather_qmm(x, *up, xr, ex))
+    r = lambda v: oracle.bf16_to_f32(oracle.f32_to_bf16(v.astype(np.float32)))
+    sig = r(1.0 / (1.0 + np.exp(-g.astype(np.float64))))
+    h = oracle.f32_to_bf16(r(g * sig) * u)
+    d = oracle.gather_qmm(h, *down, np.arange(T * k), ex)
+    assert rel_err(oracle.bf16_to_f32(out.reshape(T * k, D)), oracle.bf16_to_f32(d)) < 1e-2
+    sel = oracle.switch_glu(x, inds, gate, up, down, token_sel=np.array([2]))
+    assert np.array_equal(sel[0], out[2])
+
+
+# ---------------------------------------------------------------- reference fixture
+
+def test_tensor_bytes_formula_matches_reference_fixture():
+    """The algorithmic byte count used for the roofline equals the reference's
+    TensorQuantizedBytes (quant/oq.go:315-332) on its own fixture rows."""
+    from fastmlx_amd.roofline import quantized_tensor_bytes
+
+    with open(os.path.join(GOLDEN, "oq_tensor_bytes.json")) as f:
+        rows = json.load(f)["tensor_bytes"]
+    assert rows
+    for r in rows:
+        assert quantized_tensor_bytes(r["shape"], r["bits"], r["gs"], r["mode"]) == r["bytes"], r
