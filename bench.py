@@ -68,7 +68,8 @@ def capture(torch, fn):
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    # capture on the warmed stream: the split-K workspace is kept per stream
+    with torch.cuda.graph(g, stream=side):
         fn()
     torch.cuda.synchronize()
     return g

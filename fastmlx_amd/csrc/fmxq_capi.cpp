@@ -11,6 +11,8 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <algorithm>
+#include <map>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -21,7 +23,6 @@
 namespace {
 
 std::mutex g_err_mu;
-std::string g_err_msg = "";
 // The returned pointer must survive until the next failure; keep two buffers
 // and alternate so a reader of the previous message is not overwritten mid-read.
 char g_err_buf[2][512];
@@ -82,6 +83,60 @@ int device_flag(uint32_t** out) {
   return FMXQ_OK;
 }
 
+// Split-K workspace of the MFMA GEMM, one per (device, stream) so that calls on
+// different streams never share it.  Both arrays are zero between calls: the
+// kernel's last split per tile restores them.  Growth needs hipMalloc, which is
+// refused while the stream is being captured into a graph.
+struct SplitWs {
+  float* ws = nullptr;
+  int64_t ws_floats = 0;
+  uint32_t* counters = nullptr;
+  int64_t n_counters = 0;
+};
+std::mutex g_ws_mu;
+std::map<std::pair<int, hipStream_t>, SplitWs> g_ws;
+std::vector<void*> g_retired;
+
+int split_workspace(hipStream_t s, const fmxq::QmmPlan& plan, float** ws, uint32_t** cnt) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(FMXQ_ERR_DEVICE, "hipGetDevice failed");
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  SplitWs& w = g_ws[{dev, s}];
+  if (w.ws_floats < plan.ws_floats || w.n_counters < plan.tile_counters) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
+      return fail(FMXQ_ERR_INVALID_ARGUMENT,
+                  "quantized_matmul: split-K workspace must grow to %lld floats during graph "
+                  "capture; run the same shape once outside capture first",
+                  (long long)plan.ws_floats);
+    if (int rc = hip_status(hipStreamSynchronize(s), "split-K workspace: synchronize")) return rc;
+    const int64_t nf = std::max(plan.ws_floats, w.ws_floats);
+    const int64_t nc = std::max(plan.tile_counters, w.n_counters);
+    float* nws = nullptr;
+    uint32_t* ncnt = nullptr;
+    if (int rc = hip_status(hipMalloc(&nws, nf * sizeof(float)), "split-K workspace: hipMalloc"))
+      return rc;
+    if (int rc = hip_status(hipMalloc(&ncnt, nc * sizeof(uint32_t)), "split-K counters: hipMalloc")) {
+      (void)hipFree(nws);
+      return rc;
+    }
+    if (int rc = hip_status(hipMemset(nws, 0, nf * sizeof(float)), "split-K workspace: clear")) return rc;
+    if (int rc = hip_status(hipMemset(ncnt, 0, nc * sizeof(uint32_t)), "split-K counters: clear"))
+      return rc;
+    // A graph captured earlier may still hold the old buffers, so they are kept
+    // alive (growth is monotonic, at most doubling the footprint) rather than freed.
+    if (w.ws) g_retired.push_back(w.ws);
+    if (w.counters) g_retired.push_back(w.counters);
+    w.ws = nws;
+    w.ws_floats = nf;
+    w.counters = ncnt;
+    w.n_counters = nc;
+  }
+  *ws = w.ws;
+  *cnt = w.counters;
+  return FMXQ_OK;
+}
+
 int qmm_common(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
                const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M, int64_t N,
                int64_t K, bool transpose, int group_size, int bits, void* stream,
@@ -96,8 +151,15 @@ int qmm_common(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
     return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: x and w must be 16-byte aligned", op);
   fmxq::QmmArgs a{x, w, scales, biases, bias, y, M, N, K, K, N, group_size, bits};
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e = (M <= fmxq::kQmvMaxM) ? fmxq::launch_qmv(a, s) : fmxq::launch_qmm(a, s);
-  return hip_status(e, op);
+  if (M <= fmxq::kQmvMaxM) return hip_status(fmxq::launch_qmv(a, s), op);
+  if (M <= fmxq::kSkinnyMaxM && fmxq::qmv_mfma_supported(a))
+    return hip_status(fmxq::launch_qmv_mfma(a, s), op);
+  const fmxq::QmmPlan plan = fmxq::qmm_plan(M, N, K);
+  if (plan.splits > 1) {
+    if (int rc = split_workspace(s, plan, &a.ws, &a.tile_count)) return rc;
+    a.splits = plan.splits;
+  }
+  return hip_status(fmxq::launch_qmm(a, s), op);
 }
 
 }  // namespace

@@ -51,6 +51,15 @@ __device__ __forceinline__ uint32_t perm_b32(uint32_t hi_src, uint32_t lo_src, u
   return __builtin_amdgcn_perm(hi_src, lo_src, sel);
 }
 
+// Epilogue rounding of one output: bf16(acc), then, when an additive bias is
+// present, bf16(bf16(acc) + bias) -- the qlinear then add op chain
+// (compute/models/quant.go:105-111).
+__device__ __forceinline__ uint16_t finish_out(float acc, const uint16_t* bias, int64_t n) {
+  uint32_t v = f32_to_bf16_rne(acc);
+  if (bias) v = f32_to_bf16_rne(bf16_bits_to_f32(v) + bf16_bits_to_f32(bias[n]));
+  return (uint16_t)v;
+}
+
 // Wave64 butterfly sum.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -16,6 +16,13 @@ struct QmmArgs {
   int64_t M, N, K;
   int64_t ldx, ldy;
   int group_size, bits;
+  // Split-K state (MFMA GEMM only): splits > 1 adds fp32 partial tiles into ws
+  // [M, N] (all zero between calls) and counts finished splits per output tile
+  // in tile_count (all zero between calls); the last split of a tile writes y
+  // and restores both to zero.
+  float* ws = nullptr;
+  uint32_t* tile_count = nullptr;
+  int splits = 1;
 };
 
 // Gathered product over `batch` items of Mx rows:
@@ -42,7 +49,19 @@ hipError_t launch_dequantize(const uint32_t* w, const uint16_t* scales, const ui
 constexpr int kQmvMaxM = 4;
 hipError_t launch_qmv(const QmmArgs& a, hipStream_t stream);
 
-// MFMA GEMM for larger M.
+// MFMA GEMV for 5 <= M <= 32 (int4 with group_size >= 64, int8 with >= 32).
+constexpr int kSkinnyMaxM = 32;
+bool qmv_mfma_supported(const QmmArgs& a);
+hipError_t launch_qmv_mfma(const QmmArgs& a, hipStream_t stream);
+
+// MFMA GEMM for larger M.  qmm_plan() reports the split-K factor and the
+// workspace launch_qmm() will need for these sizes.
+struct QmmPlan {
+  int splits;
+  int64_t ws_floats;     // M * N when splits > 1
+  int64_t tile_counters; // output tiles when splits > 1
+};
+QmmPlan qmm_plan(int64_t M, int64_t N, int64_t K);
 hipError_t launch_qmm(const QmmArgs& a, hipStream_t stream);
 
 hipError_t launch_gather_qmv(const GatherArgs& a, hipStream_t stream);

@@ -151,13 +151,17 @@ __global__ __launch_bounds__(256) void qmm_kernel(QmmArgs a) {
 #pragma unroll
     for (int j = 0; j < T::TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  load_step(0);
+  // This block's share of the K steps (the whole axis unless split-K).
+  const int64_t kt0 = (int64_t)blockIdx.z * nk / a.splits;
+  const int64_t kt1 = (int64_t)(blockIdx.z + 1) * nk / a.splits;
+
+  load_step(kt0);
   store_step(0);
   __syncthreads();
 
   int buf = 0;
-  for (int64_t kt = 0; kt < nk; ++kt) {
-    const bool more = kt + 1 < nk;
+  for (int64_t kt = kt0; kt < kt1; ++kt) {
+    const bool more = kt + 1 < kt1;
     if (more) load_step(kt + 1);
 #pragma unroll
     for (int ks = 0; ks < kBK / 32; ++ks) {
@@ -181,6 +185,24 @@ __global__ __launch_bounds__(256) void qmm_kernel(QmmArgs a) {
   }
 
   // Epilogue: lane l, register r of tile (i, j) holds row 4*(l/16)+r, column l%16.
+  if (a.splits == 1) {
+#pragma unroll
+    for (int i = 0; i < T::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < T::TN; ++j) {
+        const int64_t n = n0 + wn * T::WTN + j * 16 + (lane & 15);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t m = m0 + wm * T::WTM + i * 16 + (lane >> 4) * 4 + r;
+          if (m < a.M && n < a.N) a.y[m * a.ldy + n] = finish_out(acc[i][j][r], a.bias, n);
+        }
+      }
+    return;
+  }
+
+  // Split-K: add the partial tile into the fp32 workspace, then the last split
+  // to arrive at this tile converts it, writes y and zeroes the workspace tile
+  // and the tile counter for the next call on this stream.
 #pragma unroll
   for (int i = 0; i < T::TM; ++i)
 #pragma unroll
@@ -189,14 +211,57 @@ __global__ __launch_bounds__(256) void qmm_kernel(QmmArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int64_t m = m0 + wm * T::WTM + i * 16 + (lane >> 4) * 4 + r;
-        if (m < a.M && n < a.N) a.y[m * a.ldy + n] = finish_out(acc[i][j][r], a.bias, n);
+        if (m < a.M && n < a.N) atomicAdd(a.ws + m * a.N + n, acc[i][j][r]);
       }
     }
+  __threadfence();
+  __syncthreads();
+  __shared__ uint32_t last;
+  const int64_t tile = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
+  if (tid == 0) last = atomicAdd(a.tile_count + tile, 1u) == (uint32_t)(a.splits - 1);
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  for (int e = tid; e < BM * BN; e += 256) {
+    const int64_t m = m0 + e / BN, n = n0 + e % BN;
+    if (m < a.M && n < a.N) {
+      float* p = a.ws + m * a.N + n;
+      const float v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      a.y[m * a.ldy + n] = finish_out(v, a.bias, n);
+      *p = 0.f;
+    }
+  }
+  if (tid == 0) a.tile_count[tile] = 0u;
+}
+
+// Tile shape by M: skinny tiles for verify-sized M, 128x128 for prefill.
+struct TileCfg {
+  int bm, bn;
+};
+static TileCfg tile_for(int64_t M) {
+  if (M <= 16) return {16, 64};
+  if (M <= 32) return {32, 64};
+  if (M <= 64) return {64, 128};
+  return {128, 128};
+}
+
+// Split K until there are enough blocks to cover the chip a few times over,
+// keeping at least 4 K steps per split.
+QmmPlan qmm_plan(int64_t M, int64_t N, int64_t K) {
+  const TileCfg t = tile_for(M);
+  const int64_t tiles = ((N + t.bn - 1) / t.bn) * ((M + t.bm - 1) / t.bm);
+  const int64_t nk = (K + kBK - 1) / kBK;
+  int64_t s = (1024 + tiles - 1) / tiles;
+  const int64_t smax = nk / 4;
+  if (s > smax) s = smax;
+  if (s > 32) s = 32;
+  if (s < 2) return {1, 0, 0};
+  return {(int)s, M * N, tiles};
 }
 
 template <int BITS, int BM, int BN, int WM, int WN>
 static hipError_t launch_tile(const QmmArgs& a, hipStream_t stream) {
-  dim3 grid((unsigned)((a.N + BN - 1) / BN), (unsigned)((a.M + BM - 1) / BM));
+  dim3 grid((unsigned)((a.N + BN - 1) / BN), (unsigned)((a.M + BM - 1) / BM), (unsigned)a.splits);
   qmm_kernel<BITS, BM, BN, WM, WN><<<grid, 256, 0, stream>>>(a);
   return hipGetLastError();
 }
@@ -211,6 +276,7 @@ static hipError_t launch_qmm_bits(const QmmArgs& a, hipStream_t stream) {
 
 hipError_t launch_qmm(const QmmArgs& a, hipStream_t stream) {
   if (a.M <= 0 || a.N <= 0) return hipSuccess;
+  if (a.splits > 1 && (!a.ws || !a.tile_count)) return hipErrorInvalidValue;
   return a.bits == 4 ? launch_qmm_bits<4>(a, stream) : launch_qmm_bits<8>(a, stream);
 }
 

@@ -4,23 +4,108 @@
 // Replaces the decode side of mlx_quantized_matmul (mlxgo/binding_cgo.go:636-643,
 // reached from compute/models/quant.go:91-101 on every decode step) and the
 // short-routing gather of mlx_gather_qmm (switch_glu.go:124-130 -> :179-186).
-// The kernel body is in fmxq_qmv_impl.hpp.
+//
+// Dense GEMV layout of work: a block is 4 waves.  The K axis is split into KS
+// slices (KS in {1, 2, 4}) so that every wave owns at most CPL 16-byte chunks
+// per row; the 4/KS row groups of a block each take R rows, and the KS waves
+// of a row group split its K axis and meet in LDS at the end.  Every weight
+// load of a wave is issued before any arithmetic, so a wave keeps
+// R*CPL*64*16 bytes in flight; the wave-wide sum is a DPP reduction.
+// The arithmetic per chunk is chunk_dot() (fmxq_qmv_impl.hpp): bf16(128+q)
+// operands from the exponent trick against x pairs, v_dot2_f32_bf16.
 #include "fmxq_internal.hpp"
 #include "fmxq_qmv_impl.hpp"
 
 namespace fmxq {
 
-template <int BITS, int MM, int R>
+template <int CTRL, int RMASK>
+__device__ __forceinline__ float dpp_add(float a) {
+  const int b = __builtin_amdgcn_update_dpp(0, __float_as_int(a), CTRL, RMASK, 0xf, false);
+  return a + __int_as_float(b);
+}
+
+// Sum over the 64 lanes; the result is returned in every lane.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v = dpp_add<0xb1, 0xf>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add<0x4e, 0xf>(v);   // quad_perm [2,3,0,1]
+  v = dpp_add<0x141, 0xf>(v);  // row_half_mirror
+  v = dpp_add<0x140, 0xf>(v);  // row_mirror
+  v = dpp_add<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+  v = dpp_add<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+template <int BITS, int MM, int R, int CPL, int KS>
 __global__ __launch_bounds__(256) void qmv_kernel(QmmArgs a) {
-  const int wave = threadIdx.x >> 6;
-  const int64_t n0 = ((int64_t)blockIdx.x * 4 + wave) * R;
-  if (n0 >= a.N) return;  // uniform per wave
-  const uint16_t* xrows[MM];
+  constexpr int CH = 128 / BITS;
+  constexpr int RG = 4 / KS;  // row groups per block
+  __shared__ float part[KS > 1 ? RG : 1][KS > 1 ? KS - 1 : 1][R][MM];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rg = wave / KS, ks = wave % KS;
+  const int64_t n0 = ((int64_t)blockIdx.x * RG + rg) * R;
+  const int64_t nch = a.K / CH;
+  const int64_t c0 = ks * nch / KS, c1 = (ks + 1) * nch / KS;
+  const int64_t wpr = a.K * BITS / 32, gpr = a.K / a.group_size;
+
+  // Issue every weight and scale/bias load of this wave first.  Rows past N and
+  // chunks past the slice are clamped to valid addresses and masked below.
+  u32x4 wv[R][CPL];
+  float sv[R][CPL], bv[R][CPL];
 #pragma unroll
-  for (int m = 0; m < MM; ++m) xrows[m] = a.x + (int64_t)m * a.ldx;
+  for (int r = 0; r < R; ++r) {
+    const int64_t n = n0 + r < a.N ? n0 + r : a.N - 1;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      int64_t c = c0 + lane + 64 * i;
+      c = c < c1 ? c : c1 - 1;
+      wv[r][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.w + n * wpr) + c);
+      const int64_t g = c * CH / a.group_size;
+      sv[r][i] = bf16_bits_to_f32(a.scales[n * gpr + g]);
+      bv[r][i] = bf16_bits_to_f32(a.biases[n * gpr + g]);
+    }
+  }
   float acc[R][MM];
-  qmv_wave<BITS, MM, R>(xrows, a.w, a.scales, a.biases, n0, a.N, a.K, a.group_size, acc);
-  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < MM; ++m) acc[r][m] = 0.f;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int64_t c = c0 + lane + 64 * i;
+    if (c < c1) {
+#pragma unroll
+      for (int m = 0; m < MM; ++m) {
+        XChunk<BITS> xc;
+        xc.load(a.x + (int64_t)m * a.ldx, c * CH);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const float d = chunk_dot<BITS>(wv[r][i], xc);
+          const float boff = __builtin_fmaf(-magic_offset<BITS>(), sv[r][i], bv[r][i]);
+          acc[r][m] = __builtin_fmaf(sv[r][i], d, __builtin_fmaf(boff, xc.sum, acc[r][m]));
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < MM; ++m) acc[r][m] = wave_sum_dpp(acc[r][m]);
+  if constexpr (KS > 1) {
+    if (ks > 0 && lane == 0) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MM; ++m) part[rg][ks - 1][r][m] = acc[r][m];
+    }
+    __syncthreads();
+    if (ks > 0) return;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int m = 0; m < MM; ++m)
+#pragma unroll
+        for (int s = 0; s < KS - 1; ++s) acc[r][m] += part[rg][s][r][m];
+  }
   if (lane == 0) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -33,26 +118,43 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmmArgs a) {
   }
 }
 
-// Rows per wave: enough waves to cover the chip (about 8 per CU on 256 CUs)
-// before a wave takes several rows and shares its x chunk across them.
-static int pick_rows_per_wave(int64_t N) {
-  if (N >= 4 * 2048) return 4;
-  if (N >= 2 * 2048) return 2;
-  return 1;
+// K split and chunks per lane: the fewest K slices that keep a wave at no more
+// than 2 chunks per row (4 for the longest rows).
+struct QmvShape {
+  int ks, cpl;
+};
+static QmvShape pick_qmv_shape(int64_t nch) {
+  if (nch <= 64) return {1, 1};
+  if (nch <= 128) return {1, 2};
+  if (nch <= 256) return {2, 2};
+  if (nch <= 512) return {4, 2};
+  return {4, (int)((nch + 255) / 256)};
+}
+
+template <int BITS, int MM, int R, int CPL, int KS>
+static hipError_t launch_qmv_cfg(const QmmArgs& a, hipStream_t stream) {
+  constexpr int rows_per_block = (4 / KS) * R;
+  const unsigned blocks = (unsigned)((a.N + rows_per_block - 1) / rows_per_block);
+  qmv_kernel<BITS, MM, R, CPL, KS><<<blocks, 256, 0, stream>>>(a);
+  return hipGetLastError();
+}
+
+template <int BITS, int MM, int R>
+static hipError_t launch_qmv_r(const QmmArgs& a, const QmvShape& sh, hipStream_t stream) {
+  if (sh.ks == 1 && sh.cpl == 1) return launch_qmv_cfg<BITS, MM, R, 1, 1>(a, stream);
+  if (sh.ks == 1) return launch_qmv_cfg<BITS, MM, R, 2, 1>(a, stream);
+  if (sh.ks == 2) return launch_qmv_cfg<BITS, MM, R, 2, 2>(a, stream);
+  if (sh.cpl <= 2) return launch_qmv_cfg<BITS, MM, R, 2, 4>(a, stream);
+  if (sh.cpl <= 4) return launch_qmv_cfg<BITS, MM, R, 4, 4>(a, stream);
+  return launch_qmv_cfg<BITS, MM, R, 8, 4>(a, stream);
 }
 
 template <int BITS, int MM>
 static hipError_t launch_qmv_m(const QmmArgs& a, hipStream_t stream) {
-  const int R = pick_rows_per_wave(a.N);
-  const int64_t rows_per_block = 4 * (int64_t)R;
-  const unsigned blocks = (unsigned)((a.N + rows_per_block - 1) / rows_per_block);
-  if (R == 4)
-    qmv_kernel<BITS, MM, 4><<<blocks, 256, 0, stream>>>(a);
-  else if (R == 2)
-    qmv_kernel<BITS, MM, 2><<<blocks, 256, 0, stream>>>(a);
-  else
-    qmv_kernel<BITS, MM, 1><<<blocks, 256, 0, stream>>>(a);
-  return hipGetLastError();
+  const QmvShape sh = pick_qmv_shape(a.K / (128 / BITS));
+  // Two rows per wave share each x chunk; worth it once there are rows to spare.
+  const bool two = sh.ks == 1 && a.N >= 8192;
+  return two ? launch_qmv_r<BITS, MM, 2>(a, sh, stream) : launch_qmv_r<BITS, MM, 1>(a, sh, stream);
 }
 
 template <int BITS>
@@ -71,9 +173,9 @@ hipError_t launch_qmv(const QmmArgs& a, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------------------
-// Gathered GEMV: grid (row blocks, slots).  Each slot reads its own x row and
-// the weight slice of its expert.  An out-of-range expert id writes zeros for
-// that slot and raises err_flag instead of reading outside the stack.
+// Gathered GEMV: grid (slots, row blocks).  Each slot reads its own x row and
+// the weight slice of its expert.  An out-of-range index writes zeros for that
+// slot and raises err_flag instead of reading outside the stacks.
 
 template <int BITS, int R>
 __global__ __launch_bounds__(256) void gather_qmv_kernel(GatherArgs a) {

@@ -110,14 +110,6 @@ __device__ __forceinline__ constexpr float magic_offset() {
   return BITS == 4 ? 128.f : 2176.f;
 }
 
-// Epilogue rounding of one output: bf16(acc), then, when an additive bias is
-// present, bf16(bf16(acc) + bias) -- the qlinear then add op chain.
-__device__ __forceinline__ uint16_t finish_out(float acc, const uint16_t* bias, int64_t n) {
-  uint32_t v = f32_to_bf16_rne(acc);
-  if (bias) v = f32_to_bf16_rne(bf16_bits_to_f32(v) + bf16_bits_to_f32(bias[n]));
-  return (uint16_t)v;
-}
-
 // One wave computes rows [n0, n0+R) x MM rows of x over the whole K axis.
 // xrows[m] points at row m of x; wbase/sbase/bbase at row 0 of the weight
 // matrix being read (an expert slice for gather_qmm).

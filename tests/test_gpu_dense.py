@@ -122,6 +122,15 @@ def test_qmm_ragged_n(gpu, oracle):
     _qmm_case(gpu, oracle, 130, 77, 160, 8, 32, seed=7)
 
 
+@pytest.mark.parametrize("M", [5, 7, 8, 9, 13, 16, 17, 24, 25, 31, 32])
+@pytest.mark.parametrize("bits,group,K", [(4, 64, 192), (4, 128, 1024), (8, 32, 96),
+                                          (8, 64, 2048)])
+def test_skinny_mfma_rows_and_groups(gpu, oracle, M, bits, group, K):
+    """The 5 <= M <= 32 MFMA GEMV: every count of live accumulator rows, ragged N,
+    both bit widths and the group sizes it accepts."""
+    _qmm_case(gpu, oracle, M, 333, K, bits, group, seed=900 + M * 3 + bits + group)
+
+
 @pytest.mark.parametrize("M", [1, 9, 70])
 def test_qlinear_bias_epilogue(gpu, oracle, M):
     _qmm_case(gpu, oracle, M, 512, 1024, 4, 64, seed=300 + M, bias=True)
@@ -136,6 +145,79 @@ def test_config2_full_shapes(gpu, oracle, N, K, bits, M):
     if rows is not None:
         rows = np.sort(np.append(rows, [0, M - 1]))
     _qmm_case(gpu, oracle, M, N, K, bits, 64, seed=4000 + M + bits + K, rows_checked=rows)
+
+
+@pytest.mark.parametrize("M,N,K", [(5, 1024, 4096), (16, 1024, 4096), (32, 512, 14336),
+                                   (64, 4096, 2048), (200, 256, 4096)])
+def test_split_k_shapes_repeat(gpu, oracle, M, N, K):
+    """Shapes with few output tiles take the split-K path; the per-stream workspace
+    must come back to zero after every call, so two calls in a row agree exactly."""
+    from fastmlx_amd import ops
+
+    rng = np.random.default_rng(M * 7 + N)
+    w, s, b = make_quant(rng, (N,), K, 4, 64)
+    x = make_x(rng, M, K)
+    dx, dw, ds, db = (to_dev(t, gpu) for t in (x, w, s, b))
+    announce(f"split-K M={M} N={N} K={K}")
+    y1 = to_np(ops.quantized_matmul(dx, dw, ds, db, True, 64, 4))
+    y2 = to_np(ops.quantized_matmul(dx, dw, ds, db, True, 64, 4))
+    torch.cuda.synchronize()
+    rows = np.unique(np.array([0, M // 2, M - 1]))
+    ref = oracle.qmm(np.ascontiguousarray(x[rows]), w, s, b, 64, 4)
+    assert rel_err(oracle.bf16_to_f32(y1[rows]), oracle.bf16_to_f32(ref)) <= TOL
+    g = oracle.bf16_to_f32(y1).astype(np.float64)
+    h = oracle.bf16_to_f32(y2).astype(np.float64)
+    # fp32 atomics may add partials in another order: allow one bf16 ulp
+    assert np.max(np.abs(g - h) / (np.abs(g) + 1e-3)) <= 2 ** -7
+
+
+def test_graph_replay_matches_eager(gpu):
+    """The decode stack runs from a captured HIP graph in bench.py: replays, with
+    eager work in between, must reproduce the eager result every time."""
+    from fastmlx_amd import ops
+
+    rng = np.random.default_rng(77)
+    shapes = [(1, 4096, 4096), (4, 1024, 4096), (16, 2048, 2048), (96, 512, 1024)]
+    tensors = []
+    for M, N, K in shapes:
+        w, s, b = make_quant(rng, (N,), K, 4, 64)
+        x = make_x(rng, M, K)
+        tensors.append(tuple(to_dev(t, gpu) for t in (x, w, s, b)) +
+                       (torch.empty(M, N, dtype=torch.bfloat16, device=gpu),))
+
+    def step():
+        for x, w, s, b, y in tensors:
+            ops.quantized_matmul(x, w, s, b, True, 64, 4, out=y)
+
+    announce("graph capture of quantized_matmul calls")
+    step()
+    torch.cuda.synchronize()
+    eager = [to_np(t[-1]).copy() for t in tensors]
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()  # warm the split-K workspace of the capture stream
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=side):
+        step()
+    for rep in range(4):
+        for t in tensors:
+            t[-1].zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for t, e in zip(tensors, eager):
+            got = oracle_free_close(to_np(t[-1]), e)
+            assert got, f"replay {rep} differs from eager"
+        step()  # eager work between replays
+        torch.cuda.synchronize()
+
+
+def oracle_free_close(a, b):
+    fa = (a.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    fb = (b.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    return bool(np.all(np.abs(fa - fb) <= 2 ** -7 * (np.abs(fb) + 1e-3)))
 
 
 def test_zero_sizes_enqueue_nothing(gpu):
