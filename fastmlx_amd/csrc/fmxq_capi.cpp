@@ -209,7 +209,8 @@ int fmxq_gather_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* scales
                     int64_t lhs_div, int64_t Mx, int64_t N, int64_t K, int64_t E,
                     bool transpose, int group_size, int bits, bool sorted_indices,
                     void* stream) {
-  (void)sorted_indices;  // a locality hint only; results never depend on it
+  // sorted_indices only picks the kernel: the grouped MFMA kernel for sorted
+  // batches, the per-slot GEMV otherwise.  Both give the same values for a slot.
   const char* op = "gather_qmm";
   if (int rc = check_quant(group_size, bits, K, transpose, op)) return rc;
   if (batch < 0 || x_batch < 0 || Mx < 0 || N < 0 || E < 0)
@@ -234,7 +235,10 @@ int fmxq_gather_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* scales
   fmxq::GatherArgs a{x,      w,     scales,  biases, lhs_indices, rhs_indices, y,
                      batch,  x_batch, lhs_div, Mx,   N,           K,           E,
                      group_size, bits, flag};
-  return hip_status(fmxq::launch_gather_qmv(a, static_cast<hipStream_t>(stream)), op);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (sorted_indices && batch * Mx >= fmxq::kGroupedMinSlots && fmxq::gather_mfma_supported(a))
+    return hip_status(fmxq::launch_gather_mfma(a, s), op);
+  return hip_status(fmxq::launch_gather_qmv(a, s), op);
 }
 
 int fmxq_device_error(void* stream) {

@@ -66,4 +66,9 @@ hipError_t launch_qmm(const QmmArgs& a, hipStream_t stream);
 
 hipError_t launch_gather_qmv(const GatherArgs& a, hipStream_t stream);
 
+// Grouped MFMA gather for expert-sorted batches (int4 group_size >= 64, int8 >= 32).
+constexpr int64_t kGroupedMinSlots = 32;
+bool gather_mfma_supported(const GatherArgs& a);
+hipError_t launch_gather_mfma(const GatherArgs& a, hipStream_t stream);
+
 }  // namespace fmxq

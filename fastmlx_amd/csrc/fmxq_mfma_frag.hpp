@@ -1,0 +1,61 @@
+// fmxq_mfma_frag.hpp -- MFMA operand fragments built straight from packed
+// weights (exponent trick) and from bf16 x, shared by the skinny GEMV and the
+// grouped gather kernel.
+//
+// For v_mfma_f32_32x32x16_bf16 a lane supplies 8 bf16 values per operand.
+// wfrag<4>(w): one int4 word (values q0..q7) -> pairs (q0,q4) (q1,q5) (q2,q6)
+//   (q3,q7), each value as bf16(128 + q) = 0x4300 | q.
+// wfrag<8>(w): one int8 word (values e0..e3) -> (lo e0, lo e2) (hi e0, hi e2)
+//   (lo e1, lo e3) (hi e1, hi e3) with lo as bf16(128 + lo) and hi as
+//   bf16(2048 + 16 hi) = 0x4500 | hi, so the pair sums to 2176 + q.
+// xfrag4 / xfrag8 put x in the same order, so A . B sums x * (offset + q).
+#pragma once
+#include "fmxq_common.hpp"
+
+namespace fmxq {
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  const u32x4 v = {a, b, c, d};
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// 16 bytes of x (x0..x7) -> (x0,x4) (x1,x5) (x2,x6) (x3,x7).
+__device__ __forceinline__ bf16x8 xfrag4(const u32x4 a) {
+  return as_bf16x8(__builtin_amdgcn_perm(a[2], a[0], 0x05040100u),
+                   __builtin_amdgcn_perm(a[2], a[0], 0x07060302u),
+                   __builtin_amdgcn_perm(a[3], a[1], 0x05040100u),
+                   __builtin_amdgcn_perm(a[3], a[1], 0x07060302u));
+}
+// 8 bytes of x (x0..x3) -> (x0,x2) (x0,x2) (x1,x3) (x1,x3).
+__device__ __forceinline__ bf16x8 xfrag8(uint32_t a01, uint32_t a23) {
+  const uint32_t e = __builtin_amdgcn_perm(a23, a01, 0x05040100u);
+  const uint32_t o = __builtin_amdgcn_perm(a23, a01, 0x07060302u);
+  return as_bf16x8(e, e, o, o);
+}
+
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t magic) {
+  return (a & mask) | magic;
+}
+
+template <int BITS>
+__device__ __forceinline__ bf16x8 wfrag(uint32_t w) {
+  constexpr uint32_t K = 0x000F000Fu;
+  if constexpr (BITS == 4) {
+    constexpr uint32_t M = 0x43004300u;
+    return as_bf16x8(and_or(w, K, M), and_or(w >> 4, K, M), and_or(w >> 8, K, M),
+                     and_or(w >> 12, K, M));
+  } else {
+    constexpr uint32_t LO = 0x43004300u, HI = 0x45004500u;
+    return as_bf16x8(and_or(w, K, LO), and_or(w >> 4, K, HI), and_or(w >> 8, K, LO),
+                     and_or(w >> 12, K, HI));
+  }
+}
+
+// Exponent-trick offset per value and the factor that turns the ones-MFMA sum of
+// the A operand back into sum x (int8 A carries every x value twice).
+template <int BITS>
+__device__ __forceinline__ constexpr float frag_offset() { return BITS == 4 ? 128.f : 2176.f; }
+template <int BITS>
+__device__ __forceinline__ constexpr float frag_xscale() { return BITS == 4 ? 1.f : 0.5f; }
+
+}  // namespace fmxq

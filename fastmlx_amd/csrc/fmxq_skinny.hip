@@ -22,47 +22,9 @@
 // The K axis is split over the KS waves of a block, which meet in LDS.
 #include "fmxq_common.hpp"
 #include "fmxq_internal.hpp"
+#include "fmxq_mfma_frag.hpp"
 
 namespace fmxq {
-
-__device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-  const u32x4 v = {a, b, c, d};
-  return __builtin_bit_cast(bf16x8, v);
-}
-
-// x pairs for one int4 word of weights: 16 bytes of x (x0..x7) ->
-// (x0,x4) (x1,x5) (x2,x6) (x3,x7).
-__device__ __forceinline__ bf16x8 xfrag4(const u32x4 a) {
-  return as_bf16x8(__builtin_amdgcn_perm(a[2], a[0], 0x05040100u),
-                   __builtin_amdgcn_perm(a[2], a[0], 0x07060302u),
-                   __builtin_amdgcn_perm(a[3], a[1], 0x05040100u),
-                   __builtin_amdgcn_perm(a[3], a[1], 0x07060302u));
-}
-// x pairs for one int8 word: 8 bytes of x (x0..x3) -> (x0,x2) (x0,x2) (x1,x3) (x1,x3).
-__device__ __forceinline__ bf16x8 xfrag8(uint32_t a01, uint32_t a23) {
-  const uint32_t e = __builtin_amdgcn_perm(a23, a01, 0x05040100u);
-  const uint32_t o = __builtin_amdgcn_perm(a23, a01, 0x07060302u);
-  return as_bf16x8(e, e, o, o);
-}
-
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t magic) {
-  return (a & mask) | magic;
-}
-
-// One packed word -> bf16 B operand in the order xfrag4 / xfrag8 expect.
-template <int BITS>
-__device__ __forceinline__ bf16x8 wfrag(uint32_t w) {
-  constexpr uint32_t K = 0x000F000Fu;
-  if constexpr (BITS == 4) {
-    constexpr uint32_t M = 0x43004300u;
-    return as_bf16x8(and_or(w, K, M), and_or(w >> 4, K, M), and_or(w >> 8, K, M),
-                     and_or(w >> 12, K, M));
-  } else {
-    constexpr uint32_t LO = 0x43004300u, HI = 0x45004500u;
-    return as_bf16x8(and_or(w, K, LO), and_or(w >> 4, K, HI), and_or(w >> 8, K, LO),
-                     and_or(w >> 12, K, HI));
-  }
-}
 
 template <int NT>
 struct SkStage {

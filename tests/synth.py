@@ -37,8 +37,8 @@ def make_x(rng: np.random.Generator, *shape) -> np.ndarray:
 def make_quant(rng: np.random.Generator, lead: tuple, K: int, bits: int = 4, group: int = 64):
     """Quantized weight triple with leading shape `lead` (e.g. (N,) or (E, N))."""
     G = K // group
-    q = rng.integers(0, 1 << bits, size=lead + (K,), dtype=np.uint32)
-    w = pack(q, bits)
+    # uniform random words are uniform, independent q values in every nibble/byte
+    w = rng.integers(0, 1 << 32, size=lead + (K * bits // 32,), dtype=np.uint64).astype(np.uint32)
     if bits == 4:
         s = rng.uniform(0.002, 0.02, size=lead + (G,)).astype(np.float32)
         s16 = f32_to_bf16(s)

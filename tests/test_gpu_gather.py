@@ -36,7 +36,16 @@ def test_switchglu_broadcast_form(gpu, oracle, bits):
     assert rel_err(oracle.bf16_to_f32(got.reshape(T * k, N)), oracle.bf16_to_f32(ref)) <= TOL
 
 
+def _close_ulps(a, b, ulps=2):
+    fa = (a.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    fb = (b.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    return float(np.max(np.abs(fa - fb) / (np.abs(fb) * 2.0 ** -8 + 1e-6)))
+
+
 def test_sorted_hint_does_not_change_result(gpu, oracle):
+    """sorted_indices selects the grouped kernel; the values it produces agree with
+    the per-slot kernel to within bf16 rounding (switch_glu.go:28-30: the sort is
+    only a memory-access win) and both meet the oracle tolerance."""
     rng = np.random.default_rng(3)
     S, E, N, K = 80, 8, 128, 512
     w, s, b = make_quant(rng, (E, N), K, 4, 64)
@@ -45,9 +54,52 @@ def test_sorted_hint_does_not_change_result(gpu, oracle):
     announce("gather sorted vs unsorted")
     a = _run(gpu, x, w, s, b, rhs, sorted_indices=True)
     c = _run(gpu, x, w, s, b, rhs, sorted_indices=False)
-    assert np.array_equal(a, c)
+    assert _close_ulps(a, c) <= 2.0
     ref = oracle.gather_qmm(x.reshape(S, K), w, s, b, np.arange(S), rhs.astype(np.int32))
-    assert rel_err(oracle.bf16_to_f32(a.reshape(S, N)), oracle.bf16_to_f32(ref)) <= TOL
+    for got in (a, c):
+        assert rel_err(oracle.bf16_to_f32(got.reshape(S, N)), oracle.bf16_to_f32(ref)) <= TOL
+
+
+@pytest.mark.parametrize("bits,group", [(4, 64), (4, 128), (8, 32), (8, 64)])
+@pytest.mark.parametrize("runs", [[1] * 40, [5, 3, 32, 1, 40, 7], [100], [31, 33, 2]])
+def test_grouped_kernel_runs(gpu, oracle, bits, group, runs):
+    """Expert-sorted batches whose runs start and end inside and across 32-slot
+    tiles, with ragged N; each slot must equal its own per-slot product."""
+    rng = np.random.default_rng(sum(runs) * 13 + bits + group)
+    E, N, K = len(runs) + 3, 72, 256
+    w, s, b = make_quant(rng, (E, N), K, bits, group)
+    experts = np.sort(rng.choice(E, size=len(runs), replace=False))
+    rhs = np.concatenate([np.full(r, e) for r, e in zip(runs, experts)]).astype(np.uint32)
+    S = len(rhs)
+    x = make_x(rng, S, 1, K)
+    announce(f"grouped gather bits={bits} group={group} runs={runs[:6]}")
+    got = _run(gpu, x, w, s, b, rhs, group=group, bits=bits, sorted_indices=True)
+    ref = oracle.gather_qmm(x.reshape(S, K), w, s, b, np.arange(S), rhs.astype(np.int32), group,
+                            bits)
+    assert rel_err(oracle.bf16_to_f32(got.reshape(S, N)), oracle.bf16_to_f32(ref)) <= TOL
+
+
+def test_grouped_kernel_lhs_multirow_and_bad_ids(gpu, oracle):
+    """Grouped path with explicit lhs, Mx = 2 rows per item and an out-of-range id
+    inside the sorted run: that item's rows are zero and the flag is raised."""
+    from fastmlx_amd import FmxqError, ops
+
+    rng = np.random.default_rng(21)
+    E, N, K, xb, Mx = 6, 64, 128, 9, 2
+    w, s, b = make_quant(rng, (E, N), K, 4, 64)
+    x = make_x(rng, xb, Mx, K)
+    rhs = np.array([0, 0, 1, 1, 1, 2, 4, 4, 4, 4, 4, 5, 5, 9, 9, 5, 0, 1, 1, 3], dtype=np.uint32)
+    lhs = rng.integers(0, xb, size=len(rhs)).astype(np.uint32)
+    announce("grouped gather with lhs, Mx=2, bad ids")
+    got = _run(gpu, x, w, s, b, rhs, lhs=lhs, sorted_indices=True)
+    good = rhs < E
+    assert np.all(got[~good] == 0)
+    xrow = (lhs[:, None].astype(np.int64) * Mx + np.arange(Mx)[None, :])[good].reshape(-1)
+    ref = oracle.gather_qmm(x.reshape(xb * Mx, K), w, s, b, xrow,
+                            np.repeat(rhs[good], Mx).astype(np.int32))
+    assert rel_err(oracle.bf16_to_f32(got[good].reshape(-1, N)), oracle.bf16_to_f32(ref)) <= TOL
+    with pytest.raises(FmxqError):
+        ops.device_error()
 
 
 def test_explicit_lhs_and_multi_row_items(gpu, oracle):
@@ -97,3 +149,32 @@ def test_config3_expert_projection(gpu, oracle, M):
     ref = oracle.gather_qmm(x.reshape(M, K), w, s, b, np.repeat(np.arange(M), k),
                             inds.reshape(-1))
     assert rel_err(oracle.bf16_to_f32(got.reshape(-1, N)), oracle.bf16_to_f32(ref)) <= TOL
+
+
+@pytest.mark.parametrize("cfg,M", [("c3", 128), ("c3", 512), ("c4", 32), ("c4", 256)])
+def test_sorted_switch_projection_full_size(gpu, oracle, cfg, M):
+    """The sorted branch of switchGLUCore (switch_glu.go:135-148) at config 3/4 sizes:
+    slots sorted by expert, x rows gathered by order // top_k.  The oracle checks a
+    sample of slots."""
+    from synth import topk_zipf
+
+    rng = np.random.default_rng(700 + M)
+    if cfg == "c3":
+        E, N, K, k = 512, 512, 2048, 10
+        inds = topk_uniform(rng, M, E, k)
+    else:
+        E, N, K, k = 256, 2048, 7168, 8
+        inds = topk_zipf(rng, M, E, k)
+    w, s, b = make_quant(rng, (E, N), K, 4, 64)
+    x = make_x(rng, M, 1, K)
+    flat = inds.reshape(-1)
+    order = np.argsort(flat, kind="stable")
+    rhs = flat[order].astype(np.uint32)
+    lhs = (order // k).astype(np.uint32)
+    announce(f"sorted switch projection {cfg} M={M}")
+    got = _run(gpu, x, w, s, b, rhs, lhs=lhs, sorted_indices=True).reshape(-1, N)
+    sel = np.unique(np.concatenate([[0, len(rhs) - 1],
+                                    rng.choice(len(rhs), size=24, replace=False)]))
+    ref = oracle.gather_qmm(x.reshape(M, K), w, s, b, lhs[sel].astype(np.int32),
+                            rhs[sel].astype(np.int32))
+    assert rel_err(oracle.bf16_to_f32(got[sel]), oracle.bf16_to_f32(ref)) <= TOL
