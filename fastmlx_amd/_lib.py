@@ -28,6 +28,8 @@ FMXQ_SYMBOLS = {
     "fmxq_gather_qmm": (_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
                                _i64, _bool, _int, _int, _bool, _p]),
     "fmxq_device_error": (_int, [_p]),
+    "fmxq_switch_glu": (_int, [_p] * 12 + [_i64] * 5 + [_int, _int, _p]),
+    "fmxq_moe_combine": (_int, [_p] * 5 + [_i64] * 3 + [_p]),
 }
 
 STATUS = {

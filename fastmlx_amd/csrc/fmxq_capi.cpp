@@ -137,6 +137,32 @@ int split_workspace(hipStream_t s, const fmxq::QmmPlan& plan, float** ws, uint32
   return FMXQ_OK;
 }
 
+// Per-(device, stream) scratch for the SwitchGLU intermediates, grown on demand
+// (never while the stream is being captured) and, like the split-K workspace,
+// never freed while a captured graph may still point at it.
+std::mutex g_arena_mu;
+std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> g_arena;
+
+int stream_arena(hipStream_t s, size_t bytes, void** out, const char* op) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(FMXQ_ERR_DEVICE, "hipGetDevice failed");
+  std::lock_guard<std::mutex> lk(g_arena_mu);
+  auto& a = g_arena[{dev, s}];
+  if (a.second < bytes) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
+      return fail(FMXQ_ERR_INVALID_ARGUMENT,
+                  "%s: scratch must grow to %zu bytes during graph capture; run the same shape "
+                  "once outside capture first", op, bytes);
+    void* p = nullptr;
+    if (int rc = hip_status(hipMalloc(&p, bytes), "switch_glu scratch: hipMalloc")) return rc;
+    if (a.first) g_retired.push_back(a.first);
+    a = {p, bytes};
+  }
+  *out = a.first;
+  return FMXQ_OK;
+}
+
 int qmm_common(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
                const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M, int64_t N,
                int64_t K, bool transpose, int group_size, int bits, void* stream,
@@ -257,3 +283,95 @@ int fmxq_device_error(void* stream) {
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// SwitchGLU MoE expert MLP and its combine.
+
+namespace {
+
+int gather_dispatch(const fmxq::GatherArgs& a, bool sorted, hipStream_t s) {
+  if (sorted && a.batch * a.Mx >= fmxq::kGroupedMinSlots && fmxq::gather_mfma_supported(a))
+    return hip_status(fmxq::launch_gather_mfma(a, s), "switch_glu: gather");
+  return hip_status(fmxq::launch_gather_qmv(a, s), "switch_glu: gather");
+}
+
+size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
+
+}  // namespace
+
+extern "C" int fmxq_switch_glu(const uint16_t* x, const uint32_t* inds, const uint32_t* w_gate,
+                               const uint16_t* s_gate, const uint16_t* b_gate,
+                               const uint32_t* w_up, const uint16_t* s_up, const uint16_t* b_up,
+                               const uint32_t* w_down, const uint16_t* s_down,
+                               const uint16_t* b_down, uint16_t* out, int64_t T, int64_t topk,
+                               int64_t E, int64_t D, int64_t I, int group_size, int bits,
+                               void* stream) {
+  const char* op = "switch_glu";
+  if (int rc = check_quant(group_size, bits, D, true, op)) return rc;
+  if (int rc = check_quant(group_size, bits, I, true, op)) return rc;
+  if (T < 0 || topk < 1 || E < 1)
+    return fail(FMXQ_ERR_SHAPE, "%s: need T >= 0, top_k >= 1, E >= 1 (got %lld %lld %lld)", op,
+                (long long)T, (long long)topk, (long long)E);
+  const int64_t S = T * topk;
+  if (S == 0) return FMXQ_OK;
+  if (!x || !inds || !w_gate || !s_gate || !b_gate || !w_up || !s_up || !b_up || !w_down ||
+      !s_down || !b_down || !out)
+    return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: null operand", op);
+  if (!aligned16(x) || !aligned16(w_gate) || !aligned16(w_up) || !aligned16(w_down) ||
+      !aligned16(out))
+    return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: x, weights and out must be 16-byte aligned", op);
+  if (S > 0x7fffffffLL) return fail(FMXQ_ERR_SHAPE, "%s: too many slots", op);
+  // The reference sorts once routing reaches 64 slots (switch_glu.go:119-124).
+  const bool sort = S >= 64 && E <= 16384;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint32_t* flag = nullptr;
+  if (int rc = device_flag(&flag)) return rc;
+  const size_t hbytes = align_up((size_t)S * I * sizeof(uint16_t));
+  const size_t ibytes = align_up((size_t)S * sizeof(uint32_t));
+  void* arena = nullptr;
+  if (int rc = stream_arena(s, 2 * hbytes + (sort ? 3 * ibytes : 0), &arena, op)) return rc;
+  uint16_t* gbuf = static_cast<uint16_t*>(arena);
+  uint16_t* ubuf = reinterpret_cast<uint16_t*>(static_cast<char*>(arena) + hbytes);
+  uint32_t* order = reinterpret_cast<uint32_t*>(static_cast<char*>(arena) + 2 * hbytes);
+  uint32_t* rhs_s = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(order) + ibytes);
+  uint32_t* lhs_s = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(rhs_s) + ibytes);
+
+  fmxq::GatherArgs g{x, w_gate, s_gate, b_gate, nullptr, inds, gbuf, S, T, topk, 1, I, D, E,
+                     group_size, bits, flag};
+  if (sort) {
+    if (int rc = hip_status(fmxq::launch_sort_slots(inds, S, topk, E, order, rhs_s, lhs_s, s),
+                            "switch_glu: sort"))
+      return rc;
+    g.lhs = lhs_s;
+    g.rhs = rhs_s;
+    g.lhs_div = 1;
+  }
+  if (int rc = gather_dispatch(g, sort, s)) return rc;
+  fmxq::GatherArgs u = g;
+  u.w = w_up;
+  u.scales = s_up;
+  u.biases = b_up;
+  u.y = ubuf;
+  if (int rc = gather_dispatch(u, sort, s)) return rc;
+  if (int rc = hip_status(fmxq::launch_silu_mul(gbuf, ubuf, gbuf, S * I, s), "switch_glu: silu"))
+    return rc;
+  fmxq::GatherArgs d{gbuf, w_down, s_down, b_down, nullptr, sort ? rhs_s : inds, out, S, S, 1,
+                     1, D, I, E, group_size, bits, flag};
+  if (sort) d.yrow = order;
+  return gather_dispatch(d, sort, s);
+}
+
+extern "C" int fmxq_moe_combine(const uint16_t* y, const uint16_t* weights,
+                                const uint16_t* shared, const uint16_t* shared_gate,
+                                uint16_t* out, int64_t T, int64_t topk, int64_t D, void* stream) {
+  const char* op = "moe_combine";
+  if (T < 0 || topk < 1 || D < 0 || D % 2 != 0)
+    return fail(FMXQ_ERR_SHAPE, "%s: need T >= 0, top_k >= 1 and an even D", op);
+  if (T == 0 || D == 0) return FMXQ_OK;
+  if (!y || !weights || !out) return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: null operand", op);
+  if (shared_gate && !shared)
+    return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: shared_gate without shared", op);
+  return hip_status(fmxq::launch_moe_combine(y, weights, shared, shared_gate, out, T, topk, D,
+                                             static_cast<hipStream_t>(stream)),
+                    op);
+}

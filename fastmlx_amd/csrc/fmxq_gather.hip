@@ -64,7 +64,8 @@ __global__ __launch_bounds__(256) void gather_mfma_kernel(GatherArgs a) {
     const uint64_t tail = ~(same >> done);
     const int len = (int)__builtin_ctzll(tail);
     const int end = done + len;
-    uint16_t* yslot = a.y + (s0 + ml) * a.N;
+    const int64_t yr = a.yrow ? (int64_t)a.yrow[s0 + (ml < nslots ? ml : 0)] : s0 + ml;
+    uint16_t* yslot = a.y + yr * a.N;
     if (er == 0xffffffffu) {
       if (ks == 0 && half == 0 && ml >= done && ml < end) {
         for (int c = 0; c < 32; ++c)
@@ -143,7 +144,10 @@ __global__ __launch_bounds__(256) void gather_mfma_kernel(GatherArgs a) {
         const float v = acc[r] + red[0][r][lane] + red[1][r][lane] + red[2][r][lane];
         // C layout: register r of lane l is row 8*(r/4) + 4*(l/32) + r%4, column l%32.
         const int m = (r / 4) * 8 + half * 4 + (r % 4);
-        if (m >= done && m < end && nb + ml < a.N) a.y[(s0 + m) * a.N + nb + ml] = finish_out(v, nullptr, 0);
+        if (m >= done && m < end && nb + ml < a.N) {
+          const int64_t orow = a.yrow ? (int64_t)a.yrow[s0 + m] : s0 + m;
+          a.y[orow * a.N + nb + ml] = finish_out(v, nullptr, 0);
+        }
       }
     }
     __syncthreads();

@@ -39,6 +39,8 @@ struct GatherArgs {
   int64_t batch, x_batch, lhs_div, Mx, N, K, E;
   int group_size, bits;
   uint32_t* err_flag;       // set to 1 by a kernel that meets an out-of-range index
+  const uint32_t* yrow = nullptr;  // optional output row of each slot (Mx == 1): the
+                                   // unsort of switchGLUCore fused into the store
 };
 
 hipError_t launch_dequantize(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
@@ -65,6 +67,16 @@ QmmPlan qmm_plan(int64_t M, int64_t N, int64_t K);
 hipError_t launch_qmm(const QmmArgs& a, hipStream_t stream);
 
 hipError_t launch_gather_qmv(const GatherArgs& a, hipStream_t stream);
+
+// MoE pieces around gather_qmm (fmxq_moe.hip).
+hipError_t launch_sort_slots(const uint32_t* inds, int64_t S, int64_t topk, int64_t E,
+                             uint32_t* order, uint32_t* rhs_sorted, uint32_t* lhs_sorted,
+                             hipStream_t stream);
+hipError_t launch_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* h, int64_t n,
+                           hipStream_t stream);
+hipError_t launch_moe_combine(const uint16_t* y, const uint16_t* w, const uint16_t* shared,
+                              const uint16_t* sgate, uint16_t* out, int64_t T, int64_t topk,
+                              int64_t D, hipStream_t stream);
 
 // Grouped MFMA gather for expert-sorted batches (int4 group_size >= 64, int8 >= 32).
 constexpr int64_t kGroupedMinSlots = 32;

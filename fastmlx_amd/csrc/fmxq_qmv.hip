@@ -190,7 +190,7 @@ __global__ __launch_bounds__(256) void gather_qmv_kernel(GatherArgs a) {
   const int64_t e = a.rhs[item];
   const int64_t xi = a.lhs ? (int64_t)a.lhs[item] : item / a.lhs_div;
   const int64_t xr = xi * a.Mx + row;
-  uint16_t* yrow = a.y + slot * a.N;
+  uint16_t* yrow = a.y + (a.yrow ? (int64_t)a.yrow[slot] : slot) * a.N;
   if (e >= a.E || xi >= a.x_batch) {
     if (lane == 0) {
       for (int r = 0; r < R; ++r)

@@ -91,6 +91,38 @@ def gather_qmm(x, w, scales, biases, rhs_indices, lhs_indices=None, lhs_div: int
     return out
 
 
+def switch_glu(x, inds, gate, up, down, group_size: int = 64, bits: int = 4, out=None):
+    """SwitchGLU over stacked quantized experts (switchGLUCore).
+
+    x [T, D] bf16; inds [T, top_k] int32/uint32; gate/up/down are (w, scales, biases)
+    triples with w [E, I, D*bits/32] (gate, up) and [E, D, I*bits/32] (down).
+    Returns [T, top_k, D] bf16."""
+    T, D = x.shape
+    topk = inds.shape[-1]
+    E, I = gate[0].shape[0], gate[0].shape[1]
+    if out is None:
+        out = torch.empty(T, topk, D, dtype=torch.bfloat16, device=x.device)
+    p = [_dev(x, "x", _BF16_LIKE), _dev(inds, "inds", _U32_LIKE)]
+    for name, (w, s, b) in (("gate", gate), ("up", up), ("down", down)):
+        p += [_dev(w, f"{name}.w", _U32_LIKE), _dev(s, f"{name}.scales", _BF16_LIKE),
+              _dev(b, f"{name}.biases", _BF16_LIKE)]
+    check(load().fmxq_switch_glu(*p, _dev(out, "out", _BF16_LIKE), T, topk, E, D, I, group_size,
+                                 bits, _stream(x)))
+    return out
+
+
+def moe_combine(y, weights, shared=None, shared_gate=None, out=None):
+    """sum_j y[:, j] * weights[:, j] (+ shared, optionally sigmoid-gated); y [T, k, D]."""
+    T, topk, D = y.shape
+    if out is None:
+        out = torch.empty(T, D, dtype=torch.bfloat16, device=y.device)
+    sp = None if shared is None else _dev(shared, "shared", _BF16_LIKE)
+    gp = None if shared_gate is None else _dev(shared_gate, "shared_gate", _BF16_LIKE)
+    check(load().fmxq_moe_combine(_dev(y, "y", _BF16_LIKE), _dev(weights, "weights", _BF16_LIKE),
+                                  sp, gp, _dev(out, "out", _BF16_LIKE), T, topk, D, _stream(y)))
+    return out
+
+
 def device_error(device=None) -> None:
     """Raise FmxqError(FMXQ_ERR_INDEX) if a gather met an out-of-range index."""
     dev = torch.device("cuda", torch.cuda.current_device()) if device is None else device

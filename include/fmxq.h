@@ -91,6 +91,39 @@ int fmxq_gather_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* scales
                     bool transpose, int group_size, int bits, bool sorted_indices,
                     void* stream);
 
+/* The SwitchGLU expert MLP over stacked quantized experts -- switchGLUCore with
+ * switchLinearQuantized as the projection (compute/models/switch_glu.go:79-153):
+ *     out[t, j] = down_e( silu(gate_e(x[t])) * up_e(x[t]) ),  e = inds[t, j]
+ * x [T, D] bf16; inds [T, top_k] uint32; gate/up stacks [E, I, D*bits/32] with
+ * [E, I, D/group] scales/biases; down stack [E, D, I*bits/32] with [E, D, I/group];
+ * out [T, top_k, D] bf16 (the [B, L, top_k, D] result before the router weighting).
+ * Below 64 slots (T*top_k) each slot is a gathered GEMV, as the reference's
+ * unsorted branch (switch_glu.go:124-130); from 64 slots on the slots are
+ * counting-sorted by expert on the device, projected by the grouped kernel
+ * and scattered back to token order (the sorted branch, :135-150).  Each op's
+ * result is rounded to bf16 as in the reference chain (gather_qmm, sigmoid,
+ * mul, mul).  Intermediates live in a per-stream scratch area the library
+ * grows on first use of a shape (not allowed during graph capture).
+ * Out-of-range expert ids give zero rows and raise the fmxq_device_error flag. */
+int fmxq_switch_glu(const uint16_t* x, const uint32_t* inds, const uint32_t* w_gate,
+                    const uint16_t* s_gate, const uint16_t* b_gate, const uint32_t* w_up,
+                    const uint16_t* s_up, const uint16_t* b_up, const uint32_t* w_down,
+                    const uint16_t* s_down, const uint16_t* b_down, uint16_t* out, int64_t T,
+                    int64_t top_k, int64_t E, int64_t D, int64_t I, int group_size, int bits,
+                    void* stream);
+
+/* MoE combine: out[t] = sum_j y[t, j] * weights[t, j] (+ shared term), the
+ * weighted top-k sum of qwen3next_forward.go:519-520 / deepseekv3_forward.go:436-437.
+ * y [T, top_k, D], weights [T, top_k], out [T, D], all bf16; D even.  With shared
+ * [T, D] non-NULL the shared expert output is added (deepseekv3_forward.go:438-440);
+ * with shared_gate [T] also non-NULL it is first scaled by sigmoid(shared_gate)
+ * (qwen3next_forward.go:522-524).  Rounding follows the op chain: each product
+ * to bf16, the sum in fp32 rounded once, the gated shared term and the final
+ * add each rounded to bf16. */
+int fmxq_moe_combine(const uint16_t* y, const uint16_t* weights, const uint16_t* shared,
+                     const uint16_t* shared_gate, uint16_t* out, int64_t T, int64_t top_k,
+                     int64_t D, void* stream);
+
 /* Synchronizes `stream`, then reports (and clears) the device-side error flag
  * that gather kernels raise on an out-of-range index: returns FMXQ_OK or
  * FMXQ_ERR_INDEX. */

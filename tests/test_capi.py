@@ -1,0 +1,117 @@
+"""CPU checks of the C ABI: every declared symbol is exported, and argument
+validation rejects bad calls with a status (never a crash) before any GPU work.
+
+Mirrors the reference's error-path tests: unsupported quantization falls back
+to an error rather than a wrong answer (compute/models/quant_test.go:30-59), shape
+guards fire before any kernel (switch_glu_test.go:202-219), and every op reports a
+failure status the binding turns into an error (mlxgo/binding_stub_test.go:125-185).
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+from fastmlx_amd import FmxqError, _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared(header):
+    text = open(os.path.join(ROOT, "include", header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b((?:fmxq|fmx)_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = _lib.load()
+    for header in sorted(os.listdir(os.path.join(ROOT, "include"))):
+        if not header.endswith(".h"):
+            continue
+        names = _declared(header)
+        assert names, header
+        for name in names:
+            assert hasattr(lib, name), f"{header}: {name} missing from libfmxq.so"
+            assert name in _lib.all_symbols(), f"{name} has no ctypes signature"
+
+
+def test_version():
+    assert _lib.load().fmxq_version() >= 100
+
+
+def _qmm(**kw):
+    args = dict(x=None, w=None, s=None, b=None, y=None, M=1, N=16, K=64, transpose=True,
+                group=64, bits=4)
+    args.update(kw)
+    return _lib.load().fmxq_quantized_matmul(args["x"], args["w"], args["s"], args["b"],
+                                             args["y"], args["M"], args["N"], args["K"],
+                                             args["transpose"], args["group"], args["bits"],
+                                             None)
+
+
+def _status(rc):
+    return _lib.STATUS[rc]
+
+
+@pytest.mark.parametrize("bits", [2, 3, 5, 6, 16])
+def test_unsupported_bits_is_an_error(bits):
+    # oQ can emit 2/3/5/6-bit (quant/oq.go:21-27): rejected, never computed wrongly
+    assert _status(_qmm(bits=bits)) == "FMXQ_ERR_UNSUPPORTED"
+    assert b"bits" in _lib.load().fmxq_last_error()
+
+
+def test_group_transpose_and_shape_errors():
+    assert _status(_qmm(group=48)) == "FMXQ_ERR_UNSUPPORTED"
+    assert _status(_qmm(transpose=False)) == "FMXQ_ERR_UNSUPPORTED"
+    assert _status(_qmm(K=100)) == "FMXQ_ERR_SHAPE"
+    assert _status(_qmm(M=-1)) == "FMXQ_ERR_SHAPE"
+    assert _status(_qmm()) == "FMXQ_ERR_INVALID_ARGUMENT"  # null operands
+    assert _qmm(M=0) == 0 and _qmm(N=0) == 0              # empty: nothing to do
+
+
+def test_misaligned_pointer_rejected():
+    buf = (ctypes.c_uint8 * 256)()
+    base = ctypes.addressof(buf)
+    p = base + (16 - base % 16) % 16 + 2  # 2 bytes past 16-byte alignment
+    rc = _qmm(x=p, w=p, s=p, b=p, y=p)
+    assert _status(rc) == "FMXQ_ERR_INVALID_ARGUMENT"
+
+
+def test_gather_and_dequantize_validation():
+    lib = _lib.load()
+    g = lambda **k: lib.fmxq_gather_qmm(
+        k.get("x"), k.get("w"), k.get("s"), k.get("b"), k.get("lhs"), k.get("rhs"), k.get("y"),
+        k.get("batch", 4), k.get("xb", 4), k.get("div", 1), k.get("mx", 1), k.get("N", 8),
+        k.get("K", 64), k.get("E", 2), True, k.get("group", 64), k.get("bits", 4), False, None)
+    assert _status(g(bits=3)) == "FMXQ_ERR_UNSUPPORTED"
+    assert _status(g(E=0)) == "FMXQ_ERR_SHAPE"
+    assert _status(g(div=0)) == "FMXQ_ERR_INVALID_ARGUMENT"
+    assert _status(g(batch=9, xb=2, div=4)) == "FMXQ_ERR_SHAPE"
+    assert _status(g()) == "FMXQ_ERR_INVALID_ARGUMENT"
+    assert g(batch=0) == 0
+    d = lib.fmxq_dequantize
+    assert _status(d(None, None, None, None, 4, 65, 64, 4, None)) == "FMXQ_ERR_SHAPE"
+    assert _status(d(None, None, None, None, 4, 64, 64, 7, None)) == "FMXQ_ERR_UNSUPPORTED"
+    assert d(None, None, None, None, 0, 64, 64, 4, None) == 0
+
+
+def test_switch_glu_and_combine_validation():
+    lib = _lib.load()
+    sg = lambda **k: lib.fmxq_switch_glu(*([None] * 12), k.get("T", 2), k.get("topk", 2),
+                                         k.get("E", 4), k.get("D", 64), k.get("I", 64),
+                                         k.get("group", 64), k.get("bits", 4), None)
+    assert _status(sg(bits=2)) == "FMXQ_ERR_UNSUPPORTED"
+    assert _status(sg(D=100)) == "FMXQ_ERR_SHAPE"
+    assert _status(sg(topk=0)) == "FMXQ_ERR_SHAPE"
+    assert _status(sg()) == "FMXQ_ERR_INVALID_ARGUMENT"
+    assert sg(T=0) == 0
+    mc = lib.fmxq_moe_combine
+    assert _status(mc(None, None, None, None, None, 2, 2, 7, None)) == "FMXQ_ERR_SHAPE"
+    assert _status(mc(None, None, None, None, None, 2, 2, 8, None)) == "FMXQ_ERR_INVALID_ARGUMENT"
+
+
+def test_check_raises_with_message():
+    rc = _qmm(bits=3)
+    with pytest.raises(FmxqError) as ei:
+        _lib.check(rc)
+    assert ei.value.code == 2 and "bits=3" in str(ei.value)

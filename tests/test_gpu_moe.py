@@ -1,0 +1,146 @@
+"""GPU parity: the SwitchGLU MoE expert MLP and the top-k combine vs the oracle.
+
+Shapes mirror the reference's own SwitchGLU tests (compute/models/switch_glu_test.go:
+5 experts, d=64, h=128, group 64 int4 for the unsorted branch with 2x3 slots; 8
+experts with 32x2 = 64 slots for the sorted branch) and BASELINE configs 3 and 4.
+"""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import announce, to_dev, to_np
+from synth import TOL, make_quant, make_x, rel_err, topk_uniform, topk_zipf
+
+pytestmark = pytest.mark.gpu
+
+
+def _stack(rng, E, D, I, bits=4, group=64):
+    return (make_quant(rng, (E, I), D, bits, group), make_quant(rng, (E, I), D, bits, group),
+            make_quant(rng, (E, D), I, bits, group))
+
+
+def _run(gpu, x, inds, gate, up, down, group=64, bits=4):
+    from fastmlx_amd import ops
+
+    dev = lambda t: to_dev(t, gpu)
+    out = ops.switch_glu(dev(x), dev(inds.astype(np.uint32)), tuple(map(dev, gate)),
+                         tuple(map(dev, up)), tuple(map(dev, down)), group, bits)
+    torch.cuda.synchronize()
+    return to_np(out)
+
+
+@pytest.mark.parametrize("E,T,k,D,I,bits", [(5, 2, 3, 64, 128, 4), (8, 32, 2, 64, 128, 4),
+                                            (5, 2, 3, 64, 128, 8), (8, 40, 2, 128, 64, 8)])
+def test_switch_glu_reference_shapes(gpu, oracle, E, T, k, D, I, bits):
+    rng = np.random.default_rng(E * 100 + T + bits)
+    gate, up, down = _stack(rng, E, D, I, bits)
+    x = make_x(rng, T, D)
+    inds = topk_uniform(rng, T, E, k)
+    announce(f"switch_glu E={E} T={T} k={k} slots={T * k} bits={bits}")
+    got = _run(gpu, x, inds, gate, up, down, bits=bits)
+    ref = oracle.switch_glu(x, inds, gate, up, down, 64, bits)
+    assert got.shape == (T, k, D)
+    assert rel_err(oracle.bf16_to_f32(got), oracle.bf16_to_f32(ref)) <= TOL
+
+
+def test_sorted_and_unsorted_branches_agree(gpu, oracle):
+    """63 slots take the per-slot branch, 64 the sorted one; the same tokens give
+    the same rows (switch_glu.go:28-30) up to bf16 rounding."""
+    rng = np.random.default_rng(11)
+    E, D, I, k = 8, 128, 64, 1
+    gate, up, down = _stack(rng, E, D, I)
+    x = make_x(rng, 64, D)
+    inds = topk_uniform(rng, 64, E, k)
+    announce("switch_glu 63 vs 64 slots")
+    a = _run(gpu, x[:63].copy(), inds[:63].copy(), gate, up, down)
+    b = _run(gpu, x, inds, gate, up, down)
+    fa = oracle.bf16_to_f32(a).astype(np.float64)
+    fb = oracle.bf16_to_f32(b[:63]).astype(np.float64)
+    assert np.max(np.abs(fa - fb) / (np.abs(fb) * 2.0 ** -6 + 1e-3)) <= 1.0
+    ref = oracle.switch_glu(x, inds, gate, up, down)
+    assert rel_err(oracle.bf16_to_f32(b), oracle.bf16_to_f32(ref)) <= TOL
+
+
+def test_switch_glu_bad_expert_id(gpu, oracle):
+    from fastmlx_amd import FmxqError, ops
+
+    rng = np.random.default_rng(12)
+    E, D, I = 4, 64, 64
+    gate, up, down = _stack(rng, E, D, I)
+    x = make_x(rng, 40, D)
+    inds = topk_uniform(rng, 40, E, 2)
+    inds[7, 1] = 99
+    announce("switch_glu out-of-range id")
+    got = _run(gpu, x, inds, gate, up, down)
+    assert np.all(got[7, 1] == 0)
+    with pytest.raises(FmxqError):
+        ops.device_error()
+    ok = np.ones(40, dtype=bool)
+    ok[7] = False
+    ref = oracle.switch_glu(x, np.where(inds >= E, 0, inds), gate, up, down,
+                            token_sel=np.nonzero(ok)[0])
+    assert rel_err(oracle.bf16_to_f32(got[ok]), oracle.bf16_to_f32(ref)) <= TOL
+
+
+@pytest.mark.parametrize("cfg,M", [("c3", 1), ("c3", 16), ("c3", 128), ("c4", 1), ("c4", 32)])
+def test_moe_layer_configs(gpu, oracle, cfg, M):
+    """BASELINE configs 3 and 4: SwitchGLU + weighted combine (+ shared expert for
+    config 4, added with weight 1).  The oracle evaluates a sample of tokens."""
+    from fastmlx_amd import ops
+
+    rng = np.random.default_rng(800 + M)
+    if cfg == "c3":
+        E, D, I, k = 512, 2048, 512, 10
+        inds = topk_uniform(rng, M, E, k)
+        logits = rng.standard_normal((M, k)).astype(np.float32)
+        wts = np.exp(logits - logits.max(1, keepdims=True))
+        wts = wts / wts.sum(1, keepdims=True)
+    else:
+        E, D, I, k = 256, 7168, 2048, 8
+        inds = topk_zipf(rng, M, E, k)
+        g = 1 / (1 + np.exp(-rng.standard_normal((M, k))))
+        wts = (g / g.sum(1, keepdims=True)).astype(np.float32)
+    gate, up, down = _stack(rng, E, D, I)
+    x = make_x(rng, M, D)
+    w16 = oracle.f32_to_bf16(wts.astype(np.float32))
+    dev = lambda t: to_dev(t, gpu)
+    announce(f"moe layer {cfg} M={M}")
+    y = ops.switch_glu(dev(x), dev(inds.astype(np.uint32)), tuple(map(dev, gate)),
+                       tuple(map(dev, up)), tuple(map(dev, down)), 64, 4)
+    shared = None
+    if cfg == "c4":
+        shared = make_x(rng, M, D)  # stands in for the shared-expert MLP output
+    out = ops.moe_combine(y, dev(w16), None if shared is None else dev(shared))
+    torch.cuda.synchronize()
+    got = to_np(out)
+    sel = np.unique(np.concatenate([[0, M - 1], rng.choice(M, size=min(M, 3), replace=False)]))
+    ref_y = oracle.switch_glu(x, inds, gate, up, down, token_sel=sel)
+    r16 = lambda v: oracle.bf16_to_f32(oracle.f32_to_bf16(v.astype(np.float32)))
+    prod = r16(oracle.bf16_to_f32(ref_y) * oracle.bf16_to_f32(w16[sel])[:, :, None])
+    comb = r16(prod.sum(1))
+    if shared is not None:
+        comb = r16(comb + oracle.bf16_to_f32(shared[sel]))
+    assert rel_err(oracle.bf16_to_f32(got[sel]), comb) <= TOL
+
+
+def test_moe_combine_op_chain(gpu, oracle):
+    """Combine against the numpy op chain, with and without the gated shared expert."""
+    from fastmlx_amd import ops
+
+    rng = np.random.default_rng(13)
+    T, k, D = 7, 4, 96
+    y = make_x(rng, T, k, D)
+    w = oracle.f32_to_bf16(rng.uniform(0, 1, (T, k)).astype(np.float32))
+    sh = make_x(rng, T, D)
+    sg = make_x(rng, T)
+    r16 = lambda v: oracle.bf16_to_f32(oracle.f32_to_bf16(v.astype(np.float32)))
+    base = r16((r16(oracle.bf16_to_f32(y) * oracle.bf16_to_f32(w)[:, :, None])).sum(1))
+    dev = lambda t: to_dev(t, gpu)
+    announce("moe_combine")
+    plain = to_np(ops.moe_combine(dev(y), dev(w)))
+    gated = to_np(ops.moe_combine(dev(y), dev(w), dev(sh), dev(sg)))
+    torch.cuda.synchronize()
+    sig = r16(1 / (1 + np.exp(-oracle.bf16_to_f32(sg).astype(np.float64))))
+    want_g = r16(base + r16(sig[:, None] * oracle.bf16_to_f32(sh)))
+    assert rel_err(oracle.bf16_to_f32(plain), base) <= 1e-2
+    assert rel_err(oracle.bf16_to_f32(gated), want_g) <= 1e-2
