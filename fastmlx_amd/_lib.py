@@ -22,6 +22,7 @@ FMXQ_SYMBOLS = {
     "fmxq_version": (_int, []),
     "fmxq_last_error": (ctypes.c_char_p, []),
     "fmxq_dequantize": (_int, [_p, _p, _p, _p, _i64, _i64, _int, _int, _p]),
+    "fmxq_dequantize_rows": (_int, [_p] * 5 + [_i64] * 3 + [_int, _int, _p]),
     "fmxq_quantized_matmul": (_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _bool, _int, _int, _p]),
     "fmxq_quantized_matmul_bias": (_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _bool, _int,
                                           _int, _p]),
@@ -30,6 +31,53 @@ FMXQ_SYMBOLS = {
     "fmxq_device_error": (_int, [_p]),
     "fmxq_switch_glu": (_int, [_p] * 12 + [_i64] * 5 + [_int, _int, _p]),
     "fmxq_moe_combine": (_int, [_p] * 5 + [_i64] * 3 + [_p]),
+}
+
+
+
+class FmxArray(ctypes.Structure):
+    """fmx_array handle (include/fmx.h); ctx NULL is the empty array."""
+    _fields_ = [("ctx", ctypes.c_void_p)]
+
+
+class FmxStream(ctypes.Structure):
+    """fmx_stream handle (include/fmx.h)."""
+    _fields_ = [("ctx", ctypes.c_void_p)]
+
+
+_A = FmxArray
+_S = FmxStream
+_Ap = ctypes.POINTER(FmxArray)
+_sz = ctypes.c_size_t
+
+# the array-handle layer of include/fmx.h (mlx-c calling convention)
+FMX_SYMBOLS = {
+    "fmx_array_new": (_A, []),
+    "fmx_array_new_data": (_A, [_p, ctypes.POINTER(_int), _int, _int]),
+    "fmx_array_new_device": (_A, [_p, ctypes.POINTER(_int), _int, _int]),
+    "fmx_array_free": (_int, [_A]),
+    "fmx_array_ndim": (_sz, [_A]),
+    "fmx_array_dim": (_int, [_A, _int]),
+    "fmx_array_dtype": (_int, [_A]),
+    "fmx_array_size": (_sz, [_A]),
+    "fmx_array_nbytes": (_sz, [_A]),
+    "fmx_array_device_ptr": (_p, [_A]),
+    "fmx_array_eval": (_int, [_A]),
+    "fmx_array_data_float32": (ctypes.POINTER(ctypes.c_float), [_A]),
+    "fmx_array_data_int32": (ctypes.POINTER(ctypes.c_int32), [_A]),
+    "fmx_array_to_host": (_int, [_p, _sz, _A]),
+    "fmx_default_gpu_stream_new": (_S, []),
+    "fmx_stream_new": (_S, []),
+    "fmx_stream_wrap": (_S, [_p]),
+    "fmx_stream_free": (_int, [_S]),
+    "fmx_synchronize": (_int, [_S]),
+    "fmx_quantized_matmul": (_int, [_Ap, _A, _A, _A, _A, _bool, _int, _int, _S]),
+    "fmx_gather_qmm": (_int, [_Ap] + [_A] * 6 + [_bool, _int, _int, _bool, _S]),
+    "fmx_dequantize": (_int, [_Ap, _A, _A, _A, _int, _int, _S]),
+    "fmx_quantized_matmul_bias": (_int, [_Ap] + [_A] * 5 + [_bool, _int, _int, _S]),
+    "fmx_moe_combine": (_int, [_Ap] + [_A] * 4 + [_S]),
+    "fmx_dequantize_rows": (_int, [_Ap] + [_A] * 4 + [_int, _int, _S]),
+    "fmx_switch_glu": (_int, [_Ap] + [_A] * 11 + [_int, _int, _S]),
 }
 
 STATUS = {
@@ -53,7 +101,7 @@ class FmxqError(RuntimeError):
 
 
 def all_symbols() -> dict:
-    return dict(FMXQ_SYMBOLS)
+    return {**FMXQ_SYMBOLS, **FMX_SYMBOLS}
 
 
 def load(path: str | None = None):

@@ -18,6 +18,7 @@
 #include <vector>
 
 #include "../../include/fmxq.h"
+#include "fmxq_host.hpp"
 #include "fmxq_internal.hpp"
 
 namespace {
@@ -27,6 +28,14 @@ std::mutex g_err_mu;
 // and alternate so a reader of the previous message is not overwritten mid-read.
 char g_err_buf[2][512];
 int g_err_slot = 0;
+
+// Per-device error flag raised by gather kernels.
+std::mutex g_flag_mu;
+std::vector<uint32_t*> g_flags;
+
+}  // namespace
+
+namespace fmxq {
 
 int fail(int code, const char* fmt, ...) {
   char tmp[512];
@@ -45,27 +54,6 @@ int hip_status(hipError_t e, const char* what) {
   return fail(FMXQ_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
 }
 
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
-int check_quant(int group_size, int bits, int64_t K, bool transpose, const char* op) {
-  if (!transpose)
-    return fail(FMXQ_ERR_UNSUPPORTED, "%s: transpose=false is not supported (the reference "
-                "always passes true)", op);
-  if (bits != 4 && bits != 8)
-    return fail(FMXQ_ERR_UNSUPPORTED, "%s: bits=%d not supported (4 or 8)", op, bits);
-  if (group_size != 32 && group_size != 64 && group_size != 128)
-    return fail(FMXQ_ERR_UNSUPPORTED, "%s: group_size=%d not supported (32, 64 or 128)", op,
-                group_size);
-  if (K <= 0 || K % group_size != 0)
-    return fail(FMXQ_ERR_SHAPE, "%s: K=%lld must be a positive multiple of group_size=%d", op,
-                (long long)K, group_size);
-  return FMXQ_OK;
-}
-
-// Per-device error flag raised by gather kernels.
-std::mutex g_flag_mu;
-std::vector<uint32_t*> g_flags;
-
 int device_flag(uint32_t** out) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return fail(FMXQ_ERR_DEVICE, "hipGetDevice failed");
@@ -82,6 +70,32 @@ int device_flag(uint32_t** out) {
   *out = g_flags[dev];
   return FMXQ_OK;
 }
+
+int check_quant(int group_size, int bits, int64_t K, bool transpose, const char* op) {
+  if (!transpose)
+    return fail(FMXQ_ERR_UNSUPPORTED, "%s: transpose=false is not supported (the reference "
+                "always passes true)", op);
+  if (bits != 4 && bits != 8)
+    return fail(FMXQ_ERR_UNSUPPORTED, "%s: bits=%d not supported (4 or 8)", op, bits);
+  if (group_size != 32 && group_size != 64 && group_size != 128)
+    return fail(FMXQ_ERR_UNSUPPORTED, "%s: group_size=%d not supported (32, 64 or 128)", op,
+                group_size);
+  if (K <= 0 || K % group_size != 0)
+    return fail(FMXQ_ERR_SHAPE, "%s: K=%lld must be a positive multiple of group_size=%d", op,
+                (long long)K, group_size);
+  return FMXQ_OK;
+}
+
+}  // namespace fmxq
+
+using fmxq::check_quant;
+using fmxq::device_flag;
+using fmxq::fail;
+using fmxq::hip_status;
+
+namespace {
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Split-K workspace of the MFMA GEMM, one per (device, stream) so that calls on
 // different streams never share it.  Both arrays are zero between calls: the
@@ -212,6 +226,27 @@ int fmxq_dequantize(const uint32_t* w, const uint16_t* scales, const uint16_t* b
   return hip_status(fmxq::launch_dequantize(w, scales, biases, out, rows, K, group_size, bits,
                                             static_cast<hipStream_t>(stream)),
                     "dequantize");
+}
+
+int fmxq_dequantize_rows(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                         const uint32_t* idx, uint16_t* out, int64_t n_idx, int64_t table_rows,
+                         int64_t K, int group_size, int bits, void* stream) {
+  const char* op = "dequantize_rows";
+  if (int rc = check_quant(group_size, bits, K, true, op)) return rc;
+  if (n_idx < 0 || table_rows < 0) return fail(FMXQ_ERR_SHAPE, "%s: negative size", op);
+  if (n_idx == 0) return FMXQ_OK;
+  if (table_rows == 0)
+    return fail(FMXQ_ERR_SHAPE, "%s: %lld lookups into an empty table", op, (long long)n_idx);
+  if (!w || !scales || !biases || !idx || !out)
+    return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: null operand", op);
+  if (!aligned16(w) || !aligned16(out))
+    return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: w and out must be 16-byte aligned", op);
+  uint32_t* flag = nullptr;
+  if (int rc = device_flag(&flag)) return rc;
+  return hip_status(fmxq::launch_dequantize(w, scales, biases, out, n_idx, K, group_size, bits,
+                                            static_cast<hipStream_t>(stream), idx, table_rows,
+                                            flag),
+                    op);
 }
 
 int fmxq_quantized_matmul(const uint16_t* x, const uint32_t* w, const uint16_t* scales,

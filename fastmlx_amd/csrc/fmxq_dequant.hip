@@ -16,10 +16,15 @@
 
 namespace fmxq {
 
+// Output row r reads table row idx[r] when idx is given (the take-then-dequantize
+// of quantized embedding lookups, compute/models/quant.go:117-142), else row r.
+// A row index >= table_rows yields a zero row and raises *err_flag.
 template <int BITS>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint32_t* __restrict__ w,
                                                       const uint16_t* __restrict__ scales,
                                                       const uint16_t* __restrict__ biases,
+                                                      const uint32_t* __restrict__ idx,
+                                                      int64_t table_rows, uint32_t* err_flag,
                                                       uint16_t* __restrict__ out, int64_t rows,
                                                       int64_t K, int group_size) {
   // Each thread owns 4 consecutive packed words of one row: 32 (4-bit) or 16
@@ -35,14 +40,25 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint32_t* __restrict
        t += (int64_t)gridDim.x * blockDim.x) {
     const int64_t r = t / quads_per_row;
     const int64_t qd = t - r * quads_per_row;
-    const u32x4 words = *reinterpret_cast<const u32x4*>(w + r * wpr + qd * 4);
     const int64_t k0 = qd * 4 * PER;
+    int64_t src = r;
+    if (idx) {
+      src = idx[r];
+      if (src >= table_rows) {
+        u32x4* dst = reinterpret_cast<u32x4*>(out + r * K + k0);
+#pragma unroll
+        for (int v = 0; v < PER / 2; ++v) dst[v] = u32x4{0u, 0u, 0u, 0u};
+        atomicOr(err_flag, 1u);
+        continue;
+      }
+    }
+    const u32x4 words = *reinterpret_cast<const u32x4*>(w + src * wpr + qd * 4);
     uint32_t outw[4 * PER / 2];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int64_t g = (k0 + j * PER) / group_size;
-      const float s = bf16_bits_to_f32(scales[r * gpr + g]);
-      const float b = bf16_bits_to_f32(biases[r * gpr + g]);
+      const float s = bf16_bits_to_f32(scales[src * gpr + g]);
+      const float b = bf16_bits_to_f32(biases[src * gpr + g]);
       const uint32_t word = words[j];
 #pragma unroll
       for (int p = 0; p < PER; p += 2) {
@@ -71,18 +87,19 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint32_t* __restrict
 
 hipError_t launch_dequantize(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                              uint16_t* out, int64_t rows, int64_t K, int group_size, int bits,
-                             hipStream_t stream) {
+                             hipStream_t stream, const uint32_t* idx, int64_t table_rows,
+                             uint32_t* err_flag) {
   const int64_t per = 32 / bits;
   const int64_t total = rows * (K / per / 4);
   if (total == 0) return hipSuccess;
   int64_t blocks = (total + 255) / 256;
   if (blocks > 65536) blocks = 65536;
   if (bits == 4)
-    dequant_kernel<4><<<(unsigned)blocks, 256, 0, stream>>>(w, scales, biases, out, rows, K,
-                                                            group_size);
+    dequant_kernel<4><<<(unsigned)blocks, 256, 0, stream>>>(w, scales, biases, idx, table_rows,
+                                                            err_flag, out, rows, K, group_size);
   else
-    dequant_kernel<8><<<(unsigned)blocks, 256, 0, stream>>>(w, scales, biases, out, rows, K,
-                                                            group_size);
+    dequant_kernel<8><<<(unsigned)blocks, 256, 0, stream>>>(w, scales, biases, idx, table_rows,
+                                                            err_flag, out, rows, K, group_size);
   return hipGetLastError();
 }
 

@@ -1,0 +1,20 @@
+// fmxq_host.hpp -- host-side helpers shared by the two C-ABI files
+// (fmxq_capi.cpp: raw pointer entry points; fmx_array.cpp: array handles).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fmxq {
+
+// Records a message for fmxq_last_error() and returns code.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// FMXQ_OK for hipSuccess, else FMXQ_ERR_DEVICE with the HIP error string.
+int hip_status(hipError_t e, const char* what);
+// The current device's index-error flag (one uint32 in device memory, zeroed
+// once at creation and by fmxq_device_error when it reports).
+int device_flag(uint32_t** out);
+// The quantization geometry every op supports: transpose, bits in {4, 8},
+// group_size in {32, 64, 128}, K a positive multiple of group_size.
+int check_quant(int group_size, int bits, int64_t K, bool transpose, const char* op);
+
+}  // namespace fmxq

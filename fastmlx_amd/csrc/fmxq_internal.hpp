@@ -43,9 +43,29 @@ struct GatherArgs {
                                    // unsort of switchGLUCore fused into the store
 };
 
+// idx (optional, [rows]) maps output row r to table row idx[r] < table_rows;
+// rows whose index is out of range are zeroed and raise *err_flag.
 hipError_t launch_dequantize(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                              uint16_t* out, int64_t rows, int64_t K, int group_size, int bits,
-                             hipStream_t stream);
+                             hipStream_t stream, const uint32_t* idx = nullptr,
+                             int64_t table_rows = 0, uint32_t* err_flag = nullptr);
+
+// Broadcast index materialization for gather_qmm's MLX batch semantics
+// (fmx_index.hip).  out[i] for i over the row-major output batch shape
+// shape[0..ndim) reads src at offset sum_d coord_d * stride_d (stride 0 on
+// broadcast axes) and converts it to uint32: src == nullptr yields the offset
+// itself (an implicit arange); negative or >= 2^32 values become 0xffffffff so
+// the consumer's range check rejects them.  elem_bytes is 1, 2, 4 or 8.
+constexpr int kMaxIndexDims = 8;
+struct IndexMap {
+  int ndim;
+  int elem_bytes;
+  bool is_signed;
+  int64_t shape[kMaxIndexDims];
+  int64_t stride[kMaxIndexDims];
+};
+hipError_t launch_broadcast_index(const void* src, const IndexMap& m, uint32_t* out, int64_t n,
+                                  hipStream_t stream);
 
 // Bandwidth-bound decode GEMV, M <= kQmvMaxM.
 constexpr int kQmvMaxM = 4;

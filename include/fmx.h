@@ -1,0 +1,149 @@
+/*
+ * fmx.h -- array-handle layer of libfmxq.so with mlx-c's calling convention.
+ *
+ * The reference binds MLX through mlx-c (mlxgo/binding_cgo.go:19-23).  For the
+ * quantized-linear path it calls exactly these functions; each fmx_* below has
+ * the same argument list and ownership rules as the mlx_* it replaces, so a Go
+ * binding file built with a `hip` tag can mirror binding_cgo.go line for line:
+ *
+ *   mlx_array_new / _new_data / _free          binding_cgo.go:71-251
+ *   mlx_array_ndim / _dim / _dtype / _size     binding_cgo.go:152-201
+ *   mlx_array_eval, mlx_array_data_float32/int32 binding_cgo.go:204-241
+ *   mlx_default_gpu_stream_new, mlx_synchronize binding_cgo.go:254-275
+ *   mlx_quantized_matmul                        binding_cgo.go:636-643
+ *   mlx_gather_qmm                              binding_cgo.go:645-673
+ *   mlx_dequantize                              binding_cgo.go:675-682
+ *
+ * Ownership: an op writes a newly allocated result into *res (created empty by
+ * fmx_array_new); inputs are borrowed; optional operands (biases, lhs_indices,
+ * rhs_indices) are passed as empty arrays.  Every function returns 0 on
+ * success; on failure *res is left unchanged and fmxq_last_error() has the
+ * reason (statuses are the fmxq_status codes of fmxq.h).
+ * Execution is eager on the stream's HIP queue; fmx_array_eval waits for the
+ * array's stream and reports any device-side index error (FMXQ_ERR_INDEX).
+ * Arrays live in device memory (HBM).  Result buffers come from a per-stream
+ * cache and return to it on fmx_array_free, so steady-state calls do not call
+ * hipMalloc.  An input produced on another stream is waited for with an event,
+ * and a buffer read by other streams is fenced before the cache reuses it.
+ * Streams, like MLX's, live until the process ends; fmx_stream_free releases
+ * only the handle.
+ */
+#ifndef FMX_H
+#define FMX_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same order as the reference's Dtype enum (mlxgo/dtype.go:35-50). */
+typedef enum {
+  FMX_BOOL = 0,
+  FMX_UINT8,
+  FMX_UINT16,
+  FMX_UINT32,
+  FMX_UINT64,
+  FMX_INT8,
+  FMX_INT16,
+  FMX_INT32,
+  FMX_INT64,
+  FMX_FLOAT16,
+  FMX_FLOAT32,
+  FMX_BFLOAT16,
+  FMX_COMPLEX64,
+  FMX_FLOAT64
+} fmx_dtype;
+
+typedef struct fmx_array_ {
+  void* ctx;
+} fmx_array;
+
+typedef struct fmx_stream_ {
+  void* ctx;
+} fmx_stream;
+
+/* ---- arrays ---- */
+fmx_array fmx_array_new(void);
+/* Copies size(shape)*dtype bytes of host data to a new device array
+ * (mlx_array_new_data).  data may be NULL only for an empty shape product. */
+fmx_array fmx_array_new_data(const void* data, const int* shape, int dim, fmx_dtype dtype);
+/* Wraps an existing device buffer without taking ownership (for callers that
+ * manage device memory themselves); freeing the handle leaves the buffer. */
+fmx_array fmx_array_new_device(void* device_ptr, const int* shape, int dim, fmx_dtype dtype);
+int fmx_array_free(fmx_array a);
+size_t fmx_array_ndim(const fmx_array a);
+int fmx_array_dim(const fmx_array a, int dim);
+fmx_dtype fmx_array_dtype(const fmx_array a);
+size_t fmx_array_size(const fmx_array a);
+size_t fmx_array_nbytes(const fmx_array a);
+/* Device pointer of the array's data (NULL for an empty handle). */
+void* fmx_array_device_ptr(const fmx_array a);
+int fmx_array_eval(fmx_array a);
+/* Host copies, valid until the array is freed; float32 accepts float32, bf16
+ * and float16 arrays (converted), int32 accepts int32 and uint32 arrays. */
+const float* fmx_array_data_float32(fmx_array a);
+const int32_t* fmx_array_data_int32(fmx_array a);
+/* Copies the raw element bytes to host memory dst (nbytes). */
+int fmx_array_to_host(void* dst, size_t nbytes, const fmx_array a);
+
+/* ---- streams ---- */
+fmx_stream fmx_default_gpu_stream_new(void);
+fmx_stream fmx_stream_new(void);
+/* Wraps a caller-owned hipStream_t (passed as void*). */
+fmx_stream fmx_stream_wrap(void* hip_stream);
+int fmx_stream_free(fmx_stream s);
+int fmx_synchronize(fmx_stream s);
+
+/* ---- the quantized-linear ops (mlx-c argument lists) ---- */
+/* x [..., K] bf16; w [N, K*bits/32] uint32; scales/biases [N, K/group] bf16;
+ * res [..., N] bf16.  transpose must be true. */
+int fmx_quantized_matmul(fmx_array* res, const fmx_array x, const fmx_array w,
+                         const fmx_array scales, const fmx_array biases, bool transpose,
+                         int group_size, int bits, const fmx_stream s);
+/* x [X..., Mx, K]; w [E, N, K*bits/32]; lhs_indices / rhs_indices integer arrays
+ * (or empty: the arange over x's / w's batch).  lhs and rhs broadcast to the
+ * output batch shape B; res [B..., Mx, N]:
+ *     res[i] = x[lhs[i]] . deq(w[rhs[i]])^T. */
+int fmx_gather_qmm(fmx_array* res, const fmx_array x, const fmx_array w,
+                   const fmx_array scales, const fmx_array biases, const fmx_array lhs_indices,
+                   const fmx_array rhs_indices, bool transpose, int group_size, int bits,
+                   bool sorted_indices, const fmx_stream s);
+/* w [..., K*bits/32] -> res [..., K] bf16. */
+int fmx_dequantize(fmx_array* res, const fmx_array w, const fmx_array scales,
+                   const fmx_array biases, int group_size, int bits, const fmx_stream s);
+
+/* ---- fused neighbours of the ops on the path ---- */
+/* qlinearBias (compute/models/quant.go:105-111): quantized_matmul followed by
+ * the broadcast add of bias [N] bf16 (empty: no add), fused into the epilogue. */
+int fmx_quantized_matmul_bias(fmx_array* res, const fmx_array x, const fmx_array w,
+                              const fmx_array scales, const fmx_array biases,
+                              const fmx_array bias, bool transpose, int group_size, int bits,
+                              const fmx_stream s);
+/* MoE combine (qwen3next_forward.go:520-523, deepseekv3_forward.go:434-440):
+ * res = sum_j y[..., j, :] * weights[..., j]  (+ shared, times sigmoid(shared_gate)
+ * when shared_gate is given).  y [..., k, D] bf16, weights [..., k] bf16,
+ * shared [..., D] bf16 or empty, shared_gate [..., 1] or [...] bf16 or empty;
+ * res [..., D]. */
+int fmx_moe_combine(fmx_array* res, const fmx_array y, const fmx_array weights,
+                    const fmx_array shared, const fmx_array shared_gate, const fmx_stream s);
+/* qembed (compute/models/quant.go:117-142): take rows idx of the packed table,
+ * its scales and biases, then dequantize -- one kernel.  idx integer [...];
+ * res [..., K] bf16. */
+int fmx_dequantize_rows(fmx_array* res, const fmx_array w, const fmx_array scales,
+                        const fmx_array biases, const fmx_array idx, int group_size, int bits,
+                        const fmx_stream s);
+/* switchGLUCore over quantized stacked experts (switch_glu.go:79-153):
+ * x [B, L, D], inds [B, L, top_k] -> res [B, L, top_k, D]. */
+int fmx_switch_glu(fmx_array* res, const fmx_array x, const fmx_array inds,
+                   const fmx_array w_gate, const fmx_array s_gate, const fmx_array b_gate,
+                   const fmx_array w_up, const fmx_array s_up, const fmx_array b_up,
+                   const fmx_array w_down, const fmx_array s_down, const fmx_array b_down,
+                   int group_size, int bits, const fmx_stream s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FMX_H */

@@ -58,6 +58,15 @@ int fmxq_dequantize(const uint32_t* w, const uint16_t* scales, const uint16_t* b
                     uint16_t* out, int64_t rows, int64_t K, int group_size, int bits,
                     void* stream);
 
+/* qembed over a quantized table (compute/models/quant.go:117-142: take rows idx
+ * of w, scales and biases, then dequantize) in one kernel:
+ *     out[i] (K) = deq(table row idx[i]),  i < n_idx,  idx[i] < table_rows.
+ * An out-of-range index zeroes its row and raises the device error flag
+ * (fmxq_device_error reports it). */
+int fmxq_dequantize_rows(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                         const uint32_t* idx, uint16_t* out, int64_t n_idx, int64_t table_rows,
+                         int64_t K, int group_size, int bits, void* stream);
+
 /* y [M, N] = x [M, K] . deq(W)^T, fp32 accumulation, bf16 output.
  * transpose must be true (the only value the reference passes, quant.go:98).
  * Replaces mlx_quantized_matmul (mlxgo/binding_cgo.go:636-643). */
