@@ -43,7 +43,8 @@ __global__ __launch_bounds__(256) void gather_mfma_kernel(GatherArgs a) {
   const int nslots = (int)((S - s0) < 32 ? (S - s0) : 32);
   const int64_t nu = a.K / U;
   const int64_t u0 = ks * nu / KS, u1 = (ks + 1) * nu / KS;
-  const int64_t wpr = a.K * BITS / 32, gpr = a.K / a.group_size;
+  const int gshift = __builtin_ctz((unsigned)a.group_size);  // a power of two
+  const int64_t wpr = a.K * BITS / 32, gpr = a.K >> gshift;
 
   // Slot of this lane (lane halves mirror each other) and its x row / expert.
   const int64_t slot = s0 + (ml < nslots ? ml : 0);
@@ -87,7 +88,7 @@ __global__ __launch_bounds__(256) void gather_mfma_kernel(GatherArgs a) {
 
     auto load = [&](GStage& st, int64_t u) {
       u = u < u1 ? u : u1 - 1;
-      const int64_t g = (u * U + half * (U / 2)) / a.group_size;
+      const int64_t g = (u * U + half * (U / 2)) >> gshift;
       st.w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + u * 8));
       st.sb = (uint32_t)srow[g] | ((uint32_t)brow[g] << 16);
       const u32x4* xs = reinterpret_cast<const u32x4*>(xrow + u * U);

@@ -83,7 +83,8 @@ __global__ __launch_bounds__(256) void qmm_kernel(QmmArgs a) {
   const int64_t m0 = (int64_t)blockIdx.y * BM;
   const int64_t n0 = (int64_t)blockIdx.x * BN;
   const int64_t wpr = a.K * BITS / 32;
-  const int64_t gpr = a.K / a.group_size;
+  const int gshift = __builtin_ctz((unsigned)a.group_size);  // a power of two
+  const int64_t gpr = a.K >> gshift;
   const int64_t nk = (a.K + kBK - 1) / kBK;
 
   // Register staging for one K step.
@@ -112,7 +113,7 @@ __global__ __launch_bounds__(256) void qmm_kernel(QmmArgs a) {
       if (idx < T::BTOTAL && n < a.N && k < a.K) {
         breg[i] = __builtin_nontemporal_load(
             reinterpret_cast<const u32x4*>(a.w + n * wpr + k * BITS / 32));
-        const int64_t g = k / a.group_size;
+        const int64_t g = k >> gshift;
         sreg[i] = bf16_bits_to_f32(a.scales[n * gpr + g]);
         breg_b[i] = bf16_bits_to_f32(a.biases[n * gpr + g]);
       } else {

@@ -35,6 +35,161 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// ---------------------------------------------------------------------------
+// M = 1 decode GEMV with x held in registers.
+//
+// A block is 4 waves: 4/KS row groups x KS slices of the K axis.  Lane l of the
+// wave for slice ks owns 16-byte chunks c0 + l + 64 i (i < CPL) of every row the
+// wave visits, so it builds the x pairs and x sums of those chunks once and keeps
+// them in registers while the wave walks RPW rows, R rows at a time, with the
+// next R rows' weights already in flight (two register buffers, indices fixed at
+// compile time).  Per 16-byte int4 chunk this leaves the exponent-trick unpack
+// and v_dot2 (11 VALU per packed word) plus a 3-op group correction.
+template <int BITS, int CPL, int R, int RPW, int KS>
+__global__ __launch_bounds__(256) void qmv1_kernel(QmmArgs a) {
+  constexpr int CH = 128 / BITS;  // values per 16-byte chunk
+  constexpr int RG = 4 / KS;
+  static_assert(RPW % R == 0, "rows per wave must be a multiple of R");
+  __shared__ float part[KS > 1 ? RG : 1][KS][RPW];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rg = wave / KS, ks = wave % KS;
+  const int nch = (int)(a.K / CH);
+  const int c0 = ks * nch / KS, c1 = (ks + 1) * nch / KS;
+  const int gshift = __builtin_ctz((unsigned)a.group_size);
+  const int chunk_gshift = gshift - __builtin_ctz((unsigned)CH);  // chunk -> group
+  const int64_t wpr = a.K * BITS / 32, gpr = a.K >> gshift;
+  const int64_t nbase = ((int64_t)blockIdx.x * RG + rg) * RPW;
+
+  XChunk<BITS> xc[CPL];
+  bool live[CPL];
+  int cc[CPL];
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = c0 + lane + 64 * i;
+    live[i] = c < c1;
+    cc[i] = live[i] ? c : c0;
+    xc[i].load(a.x, (int64_t)cc[i] * CH);
+    if (!live[i]) xc[i].sum = 0.f;
+  }
+
+  u32x4 wv0[R][CPL], wv1[R][CPL];
+  uint32_t sb0[R][CPL], sb1[R][CPL];
+  auto load = [&](u32x4 (&wv)[R][CPL], uint32_t (&sb)[R][CPL], int rb) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      int64_t n = nbase + rb + r;
+      n = n < a.N ? n : a.N - 1;
+      const u32x4* wr = reinterpret_cast<const u32x4*>(a.w + n * wpr);
+      const uint16_t* sr = a.scales + n * gpr;
+      const uint16_t* br = a.biases + n * gpr;
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        wv[r][i] = __builtin_nontemporal_load(wr + cc[i]);
+        const int g = cc[i] >> chunk_gshift;
+        sb[r][i] = (uint32_t)sr[g] | ((uint32_t)br[g] << 16);
+      }
+    }
+  };
+  float res[RPW];
+  auto compute = [&](const u32x4 (&wv)[R][CPL], const uint32_t (&sb)[R][CPL], int rb) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const float d = chunk_dot<BITS>(wv[r][i], xc[i]);
+        const float s = bf16_lo(sb[r][i]);
+        const float bo = __builtin_fmaf(-magic_offset<BITS>(), s, bf16_hi(sb[r][i]));
+        const float t = __builtin_fmaf(s, d, bo * xc[i].sum);
+        acc += live[i] ? t : 0.f;
+      }
+      res[rb + r] = wave_sum_dpp(acc);
+    }
+  };
+  load(wv0, sb0, 0);
+#pragma unroll
+  for (int rb = 0; rb < RPW; rb += 2 * R) {
+    if (rb + R < RPW) load(wv1, sb1, rb + R);
+    compute(wv0, sb0, rb);
+    if (rb + R < RPW) {
+      if (rb + 2 * R < RPW) load(wv0, sb0, rb + 2 * R);
+      compute(wv1, sb1, rb + R);
+    }
+  }
+
+  if constexpr (KS > 1) {
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) part[rg][ks][r] = res[r];
+    }
+    __syncthreads();
+    if (ks == 0 && lane < RPW) {
+      float v = 0.f;
+#pragma unroll
+      for (int k = 0; k < KS; ++k) v += part[rg][k][lane];
+      const int64_t n = nbase + lane;
+      if (n < a.N) a.y[n] = finish_out(v, a.bias, n);
+    }
+  } else {
+    if (lane < RPW) {
+      float v = res[0];
+#pragma unroll
+      for (int r = 1; r < RPW; ++r) v = lane == r ? res[r] : v;
+      const int64_t n = nbase + lane;
+      if (n < a.N) a.y[n] = finish_out(v, a.bias, n);
+    }
+  }
+}
+
+struct Qmv1Shape {
+  int ks, cpl, rpw;
+};
+// The fewest K slices (1, 2 or 4) that keep a lane at <= 2 chunks per row, and
+// more rows per wave for the longest rows, where building x costs the most.
+static Qmv1Shape pick_qmv1_shape(int64_t nch, int64_t N) {
+  Qmv1Shape sh{4, (int)((nch + 255) / 256), 4};
+  if (nch <= 64) sh = {1, 1, 4};
+  else if (nch <= 128) sh = {2, 1, 4};
+  else if (nch <= 256) sh = {4, 1, 4};
+  if (nch > 256 && sh.cpl <= 2) sh.rpw = 8;
+  if (N <= 2048) sh.rpw = 2;
+  return sh;
+}
+
+template <int BITS, int CPL, int R, int RPW, int KS>
+static hipError_t launch_qmv1_cfg(const QmmArgs& a, hipStream_t stream) {
+  constexpr int64_t rows_per_block = (4 / KS) * RPW;
+  const unsigned blocks = (unsigned)((a.N + rows_per_block - 1) / rows_per_block);
+  qmv1_kernel<BITS, CPL, R, RPW, KS><<<blocks, 256, 0, stream>>>(a);
+  return hipGetLastError();
+}
+
+template <int BITS, int CPL, int KS>
+static hipError_t launch_qmv1_rpw(const QmmArgs& a, int rpw, hipStream_t stream) {
+  if (rpw == 2) return launch_qmv1_cfg<BITS, CPL, 2, 2, KS>(a, stream);
+  if (rpw == 4) return launch_qmv1_cfg<BITS, CPL, 2, 4, KS>(a, stream);
+  return launch_qmv1_cfg<BITS, CPL, 2, 8, KS>(a, stream);
+}
+
+// Chunks per lane above 4 (K beyond 32768 int4 values) use the general kernel.
+static bool qmv1_supported(const QmmArgs& a, int bits) {
+  const int64_t nch = a.K / (128 / bits);
+  return a.M == 1 && pick_qmv1_shape(nch, a.N).cpl <= 4;
+}
+
+template <int BITS>
+static hipError_t launch_qmv1(const QmmArgs& a, hipStream_t stream) {
+  const Qmv1Shape sh = pick_qmv1_shape(a.K / (128 / BITS), a.N);
+  if (sh.ks == 1) return launch_qmv1_rpw<BITS, 1, 1>(a, sh.rpw, stream);
+  if (sh.ks == 2) return launch_qmv1_rpw<BITS, 1, 2>(a, sh.rpw, stream);
+  if (sh.cpl == 1) return launch_qmv1_rpw<BITS, 1, 4>(a, sh.rpw, stream);
+  if (sh.cpl == 2) return launch_qmv1_rpw<BITS, 2, 4>(a, sh.rpw, stream);
+  return launch_qmv1_rpw<BITS, 4, 4>(a, sh.rpw, stream);
+}
+
+// ---------------------------------------------------------------------------
+// General decode GEMV for M <= 4.
+
 template <int BITS, int MM, int R, int CPL, int KS>
 __global__ __launch_bounds__(256) void qmv_kernel(QmmArgs a) {
   constexpr int CH = 128 / BITS;
@@ -45,7 +200,9 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmmArgs a) {
   const int64_t n0 = ((int64_t)blockIdx.x * RG + rg) * R;
   const int64_t nch = a.K / CH;
   const int64_t c0 = ks * nch / KS, c1 = (ks + 1) * nch / KS;
-  const int64_t wpr = a.K * BITS / 32, gpr = a.K / a.group_size;
+  const int gshift = __builtin_ctz((unsigned)a.group_size);
+  const int chunk_gshift = gshift - __builtin_ctz((unsigned)CH);
+  const int64_t wpr = a.K * BITS / 32, gpr = a.K >> gshift;
 
   // Issue every weight and scale/bias load of this wave first.  Rows past N and
   // chunks past the slice are clamped to valid addresses and masked below.
@@ -59,7 +216,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmmArgs a) {
       int64_t c = c0 + lane + 64 * i;
       c = c < c1 ? c : c1 - 1;
       wv[r][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.w + n * wpr) + c);
-      const int64_t g = c * CH / a.group_size;
+      const int64_t g = c >> chunk_gshift;
       sv[r][i] = bf16_bits_to_f32(a.scales[n * gpr + g]);
       bv[r][i] = bf16_bits_to_f32(a.biases[n * gpr + g]);
     }
@@ -169,6 +326,8 @@ static hipError_t launch_qmv_bits(const QmmArgs& a, hipStream_t stream) {
 
 hipError_t launch_qmv(const QmmArgs& a, hipStream_t stream) {
   if (a.M <= 0 || a.N <= 0) return hipSuccess;
+  if (qmv1_supported(a, a.bits))
+    return a.bits == 4 ? launch_qmv1<4>(a, stream) : launch_qmv1<8>(a, stream);
   return a.bits == 4 ? launch_qmv_bits<4>(a, stream) : launch_qmv_bits<8>(a, stream);
 }
 
@@ -199,7 +358,7 @@ __global__ __launch_bounds__(256) void gather_qmv_kernel(GatherArgs a) {
     }
     return;
   }
-  const int64_t wpr = a.K * BITS / 32, gpr = a.K / a.group_size;
+  const int64_t wpr = a.K * BITS / 32, gpr = a.K >> __builtin_ctz((unsigned)a.group_size);
   const uint16_t* xrows[1] = {a.x + xr * a.K};
   float acc[R][1];
   qmv_wave<BITS, 1, R>(xrows, a.w + e * a.N * wpr, a.scales + e * a.N * gpr,

@@ -123,7 +123,8 @@ __device__ __forceinline__ void qmv_wave(const uint16_t* const* xrows,
   const int lane = threadIdx.x & 63;
   const int64_t nchunks = K / CH;
   const int64_t wpr = K * BITS / 32;
-  const int64_t gpr = K / group_size;
+  const int gshift = __builtin_ctz((unsigned)group_size);  // group_size is a power of two
+  const int64_t gpr = K >> gshift;
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -131,7 +132,7 @@ __device__ __forceinline__ void qmv_wave(const uint16_t* const* xrows,
 
   for (int64_t c = lane; c < nchunks; c += 64) {
     const int64_t k0 = c * CH;
-    const int64_t g = k0 / group_size;
+    const int64_t g = k0 >> gshift;
     u32x4 wv[R];
     float s[R], bc[R];
 #pragma unroll

@@ -49,7 +49,8 @@ __global__ __launch_bounds__(256) void qmv_mfma_kernel(QmmArgs a) {
   const int64_t nb = ((int64_t)blockIdx.x * RG + rg) * 32 * NT;
   const int64_t nu = a.K / U;
   const int64_t u0 = ks * nu / KS, u1 = (ks + 1) * nu / KS;
-  const int64_t wpr = a.K * BITS / 32, gpr = a.K / a.group_size;
+  const int gshift = __builtin_ctz((unsigned)a.group_size);  // a power of two
+  const int64_t wpr = a.K * BITS / 32, gpr = a.K >> gshift;
   const int mrow = ml < a.M ? ml : (int)a.M - 1;
   const uint16_t* xrow = a.x + (int64_t)mrow * a.ldx + half * (U / 2);
 
@@ -67,7 +68,7 @@ __global__ __launch_bounds__(256) void qmv_mfma_kernel(QmmArgs a) {
 
   auto load = [&](SkStage<NT>& st, int64_t u) {
     u = u < u1 ? u : u1 - 1;  // tail loads re-read the last unit; never computed
-    const int64_t g = (u * U + half * (U / 2)) / a.group_size;
+    const int64_t g = (u * U + half * (U / 2)) >> gshift;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       st.w[t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[t] + u * 8));
