@@ -59,6 +59,23 @@ def stack_bytes(M, layers, bits):
     return layers * sum(qmm_bytes(M, N, K, bits, GROUP) for _, N, K in LLAMA_PROJ)
 
 
+QMV_UP_PMC = os.path.join(ROOT, "profiles", "qmv1_gate_up_14336x4096_M1_traffic.md")
+
+
+def measured_traffic(path):
+    """HBM bytes per launch of the roofline kernel from its committed rocprofv3 --pmc
+    summary (FETCH_SIZE and WRITE_SIZE, each scaled by the copy-kernel calibration),
+    or None when no summary is present."""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
+
+
 def capture(torch, fn):
     """Warm up fn eagerly on a side stream, then capture it into a HIP graph."""
     side = torch.cuda.Stream()
@@ -216,8 +233,9 @@ def main():
                                       "frac_hbm": round(gbps_dn / HBM_PEAK_GBS, 4),
                                       "distinct_copies": n_dn}
         roof = {"bound": "hbm", "achieved": round(gbps_up, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(gbps_up / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "qmv_kernel<4,1,4> (gate/up 14336x4096, M=1)",
+                "unit": "GB/s", "frac": round(gbps_up / HBM_PEAK_GBS, 4),
+                "traffic": measured_traffic(QMV_UP_PMC),
+                "kernel": "fmxq::qmv1_kernel<4,1,2,4,2> (gate/up 14336x4096, M=1)",
                 "bytes_per_launch": by_up,
                 "timing": "HIP events over a graph of %d back-to-back launches on distinct "
                           "weight copies; per-launch = total / launches" % n_up}

@@ -42,6 +42,16 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, r);
 }
 
+// A compile-time constant materialised in a VGPR.  gfx9 VOP3 encodings take no
+// literal and at most one SGPR, so (w & mask) | magic only becomes a single
+// v_and_or_b32 when one of the two constants already sits in a VGPR; otherwise
+// the compiler splits it into v_and_b32 + v_or_b32 with literals.
+__device__ __forceinline__ uint32_t vgpr_const(uint32_t c) {
+  uint32_t v;
+  asm("v_mov_b32 %0, %1" : "=v"(v) : "i"(c));
+  return v;
+}
+
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
                                          __builtin_bit_cast(bf16x2, b), c, false);

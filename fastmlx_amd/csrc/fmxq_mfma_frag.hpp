@@ -37,15 +37,16 @@ __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t m
   return (a & mask) | magic;
 }
 
+// The magic constants live in VGPRs (vgpr_const) so each pair is one v_and_or_b32.
 template <int BITS>
 __device__ __forceinline__ bf16x8 wfrag(uint32_t w) {
   constexpr uint32_t K = 0x000F000Fu;
   if constexpr (BITS == 4) {
-    constexpr uint32_t M = 0x43004300u;
+    const uint32_t M = vgpr_const(0x43004300u);
     return as_bf16x8(and_or(w, K, M), and_or(w >> 4, K, M), and_or(w >> 8, K, M),
                      and_or(w >> 12, K, M));
   } else {
-    constexpr uint32_t LO = 0x43004300u, HI = 0x45004500u;
+    const uint32_t LO = vgpr_const(0x43004300u), HI = vgpr_const(0x45004500u);
     return as_bf16x8(and_or(w, K, LO), and_or(w >> 4, K, HI), and_or(w >> 8, K, LO),
                      and_or(w >> 12, K, HI));
   }

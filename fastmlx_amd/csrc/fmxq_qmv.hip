@@ -51,7 +51,9 @@ __global__ __launch_bounds__(256) void qmv1_kernel(QmmArgs a) {
   constexpr int RG = 4 / KS;
   static_assert(RPW % R == 0, "rows per wave must be a multiple of R");
   __shared__ float part[KS > 1 ? RG : 1][KS][RPW];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // The wave index is uniform; readfirstlane lets row and slice math run on SALU.
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int rg = wave / KS, ks = wave % KS;
   const int nch = (int)(a.K / CH);
   const int c0 = ks * nch / KS, c1 = (ks + 1) * nch / KS;

@@ -24,6 +24,11 @@ constexpr uint32_t kMagic = 0x43004300u;   // bf16 pair (128, 128) exponent bits
 constexpr uint32_t kNib2 = 0x000F000Fu;    // one nibble in each 16-bit half
 constexpr uint32_t kOnes = 0x3F803F80u;    // bf16 pair (1.0, 1.0)
 
+// (w & kNib2) | magic as one v_and_or_b32 (magic from vgpr_const).
+__device__ __forceinline__ uint32_t nib_pair(uint32_t w, uint32_t vmagic) {
+  return (w & kNib2) | vmagic;
+}
+
 // x pairs matching the nibble pairing of one int4 word: (x0,x4) (x1,x5) (x2,x6) (x3,x7).
 __device__ __forceinline__ void x_pairs_q4(const u32x4 a, uint32_t* p) {
   p[0] = (a[0] & 0xffffu) | (a[2] << 16);
@@ -79,15 +84,16 @@ struct XChunk {
 // before scaling: returns d (int4) or d_lo + 16 d_hi (int8).
 template <int BITS>
 __device__ __forceinline__ float chunk_dot(const u32x4 wv, const XChunk<BITS>& xc) {
+  const uint32_t m = vgpr_const(kMagic);
   if constexpr (BITS == 4) {
     float d = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t w = wv[j];
-      d = dot2_bf16((w & kNib2) | kMagic, xc.p[4 * j + 0], d);
-      d = dot2_bf16(((w >> 4) & kNib2) | kMagic, xc.p[4 * j + 1], d);
-      d = dot2_bf16(((w >> 8) & kNib2) | kMagic, xc.p[4 * j + 2], d);
-      d = dot2_bf16(((w >> 12) & kNib2) | kMagic, xc.p[4 * j + 3], d);
+      d = dot2_bf16(nib_pair(w, m), xc.p[4 * j + 0], d);
+      d = dot2_bf16(nib_pair(w >> 4, m), xc.p[4 * j + 1], d);
+      d = dot2_bf16(nib_pair(w >> 8, m), xc.p[4 * j + 2], d);
+      d = dot2_bf16(nib_pair(w >> 12, m), xc.p[4 * j + 3], d);
     }
     return d;
   } else {
@@ -95,10 +101,10 @@ __device__ __forceinline__ float chunk_dot(const u32x4 wv, const XChunk<BITS>& x
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t w = wv[j];
-      dl = dot2_bf16((w & kNib2) | kMagic, xc.p[2 * j + 0], dl);
-      dh = dot2_bf16(((w >> 4) & kNib2) | kMagic, xc.p[2 * j + 0], dh);
-      dl = dot2_bf16(((w >> 8) & kNib2) | kMagic, xc.p[2 * j + 1], dl);
-      dh = dot2_bf16(((w >> 12) & kNib2) | kMagic, xc.p[2 * j + 1], dh);
+      dl = dot2_bf16(nib_pair(w, m), xc.p[2 * j + 0], dl);
+      dh = dot2_bf16(nib_pair(w >> 4, m), xc.p[2 * j + 0], dh);
+      dl = dot2_bf16(nib_pair(w >> 8, m), xc.p[2 * j + 1], dl);
+      dh = dot2_bf16(nib_pair(w >> 12, m), xc.p[2 * j + 1], dh);
     }
     return dl + 16.f * dh;
   }
