@@ -4,8 +4,9 @@
 // nonzero fmxq_status with a message and leaves the stream untouched, the
 // contract mlxgo relies on when it frees the result handle on rc != 0
 // (mlxgo/binding_cgo.go:636-643).  Dispatch by M:
-//   M <= kQmvMaxM  -> decode GEMV (fmxq_qmv.hip), bandwidth bound, no MFMA
-//   M >  kQmvMaxM  -> LDS-dequant MFMA GEMM (fmxq_qmm.hip)
+//   M <= 8 (x rows fit in registers) -> decode GEMV (fmxq_qmv.hip), no MFMA
+//   M <= 32                          -> MFMA GEMV (fmxq_skinny.hip)
+//   otherwise                        -> LDS-dequant MFMA GEMM (fmxq_qmm.hip)
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
@@ -191,7 +192,7 @@ int qmm_common(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
     return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: x and w must be 16-byte aligned", op);
   fmxq::QmmArgs a{x, w, scales, biases, bias, y, M, N, K, K, N, group_size, bits};
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (M <= fmxq::kQmvMaxM) return hip_status(fmxq::launch_qmv(a, s), op);
+  if (fmxq::qmv_supported(a)) return hip_status(fmxq::launch_qmv(a, s), op);
   if (M <= fmxq::kSkinnyMaxM && fmxq::qmv_mfma_supported(a))
     return hip_status(fmxq::launch_qmv_mfma(a, s), op);
   const fmxq::QmmPlan plan = fmxq::qmm_plan(M, N, K);

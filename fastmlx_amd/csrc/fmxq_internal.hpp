@@ -67,8 +67,10 @@ struct IndexMap {
 hipError_t launch_broadcast_index(const void* src, const IndexMap& m, uint32_t* out, int64_t n,
                                   hipStream_t stream);
 
-// Bandwidth-bound decode GEMV, M <= kQmvMaxM.
+// Bandwidth-bound decode GEMV without MFMA: every M <= kQmvMaxM, and M <= 8
+// where the x rows fit in registers (qmv_supported).
 constexpr int kQmvMaxM = 4;
+bool qmv_supported(const QmmArgs& a);
 hipError_t launch_qmv(const QmmArgs& a, hipStream_t stream);
 
 // MFMA GEMV for 5 <= M <= 32 (int4 with group_size >= 64, int8 with >= 32).

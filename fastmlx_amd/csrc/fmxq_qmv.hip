@@ -36,21 +36,27 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 }
 
 // ---------------------------------------------------------------------------
-// M = 1 decode GEMV with x held in registers.
+// Decode GEMV for M <= 8 with x held in registers.
 //
 // A block is 4 waves: 4/KS row groups x KS slices of the K axis.  Lane l of the
 // wave for slice ks owns 16-byte chunks c0 + l + 64 i (i < CPL) of every row the
-// wave visits, so it builds the x pairs and x sums of those chunks once and keeps
-// them in registers while the wave walks RPW rows, R rows at a time, with the
-// next R rows' weights already in flight (two register buffers, indices fixed at
-// compile time).  Per 16-byte int4 chunk this leaves the exponent-trick unpack
-// and v_dot2 (11 VALU per packed word) plus a 3-op group correction.
-template <int BITS, int CPL, int R, int RPW, int KS>
-__global__ __launch_bounds__(256) void qmv1_kernel(QmmArgs a) {
+// wave visits, so it builds the x pairs and x sums of those chunks (for each of
+// the MM rows of x) once and keeps them in registers while the wave walks RPW
+// weight rows, R rows at a time, with the next R rows' weights already in flight
+// (two register buffers, indices fixed at compile time).  A wave's weight load is
+// 1 KiB contiguous per row.  Each packed word is unpacked once (exponent trick, 7
+// VALU) and dotted against every x row (4 v_dot2 each); a 3-op group correction
+// per chunk and row follows.  The RPW x MM partial sums are reduced together at
+// the end (wave_sum_multi).
+template <int BITS, int MM, int CPL, int R, int RPW, int KS>
+__global__ __launch_bounds__(256) void qmvx_kernel(QmmArgs a) {
   constexpr int CH = 128 / BITS;  // values per 16-byte chunk
   constexpr int RG = 4 / KS;
+  constexpr int V = RPW * MM;     // partial sums per lane
+  constexpr int LV = __builtin_ctz(V);
   static_assert(RPW % R == 0, "rows per wave must be a multiple of R");
-  __shared__ float part[KS > 1 ? RG : 1][KS][RPW];
+  static_assert((V & (V - 1)) == 0 && V <= 64, "RPW * MM must be a power of two <= 64");
+  __shared__ float part[KS > 1 ? RG : 1][KS][V];
   // The wave index is uniform; readfirstlane lets row and slice math run on SALU.
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -62,7 +68,8 @@ __global__ __launch_bounds__(256) void qmv1_kernel(QmmArgs a) {
   const int64_t wpr = a.K * BITS / 32, gpr = a.K >> gshift;
   const int64_t nbase = ((int64_t)blockIdx.x * RG + rg) * RPW;
 
-  XChunk<BITS> xc[CPL];
+  // Rows of x beyond M repeat row M-1; their outputs are never stored.
+  XChunk<BITS> xc[MM][CPL];
   bool live[CPL];
   int cc[CPL];
 #pragma unroll
@@ -70,8 +77,15 @@ __global__ __launch_bounds__(256) void qmv1_kernel(QmmArgs a) {
     const int c = c0 + lane + 64 * i;
     live[i] = c < c1;
     cc[i] = live[i] ? c : c0;
-    xc[i].load(a.x, (int64_t)cc[i] * CH);
-    if (!live[i]) xc[i].sum = 0.f;
+  }
+#pragma unroll
+  for (int m = 0; m < MM; ++m) {
+    const uint16_t* xr = a.x + (int64_t)(m < a.M ? m : a.M - 1) * a.ldx;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      xc[m][i].load(xr, (int64_t)cc[i] * CH);
+      if (!live[i]) xc[m][i].sum = 0.f;
+    }
   }
 
   u32x4 wv0[R][CPL], wv1[R][CPL];
@@ -92,101 +106,145 @@ __global__ __launch_bounds__(256) void qmv1_kernel(QmmArgs a) {
       }
     }
   };
-  float res[RPW];
+  float res[V];  // res[r * MM + m]: this lane's partial for weight row r, x row m
   auto compute = [&](const u32x4 (&wv)[R][CPL], const uint32_t (&sb)[R][CPL], int rb) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      float acc = 0.f;
+      float acc[MM];
+#pragma unroll
+      for (int m = 0; m < MM; ++m) acc[m] = 0.f;
 #pragma unroll
       for (int i = 0; i < CPL; ++i) {
-        const float d = chunk_dot<BITS>(wv[r][i], xc[i]);
         const float s = bf16_lo(sb[r][i]);
         const float bo = __builtin_fmaf(-magic_offset<BITS>(), s, bf16_hi(sb[r][i]));
-        const float t = __builtin_fmaf(s, d, bo * xc[i].sum);
-        acc += live[i] ? t : 0.f;
+        if constexpr (MM == 1) {
+          const float t = __builtin_fmaf(s, chunk_dot<BITS>(wv[r][i], xc[0][i]), bo * xc[0][i].sum);
+          acc[0] += live[i] ? t : 0.f;
+        } else {
+          uint32_t p[16];
+          unpack_chunk(wv[r][i], p);
+#pragma unroll
+          for (int m = 0; m < MM; ++m) {
+            const float t = __builtin_fmaf(s, dot_pairs<BITS>(p, xc[m][i]), bo * xc[m][i].sum);
+            acc[m] += live[i] ? t : 0.f;
+          }
+        }
       }
-      res[rb + r] = wave_sum_dpp(acc);
+#pragma unroll
+      for (int m = 0; m < MM; ++m) res[(rb + r) * MM + m] = acc[m];
     }
   };
+  // With several x rows, sched_barrier(0) pins each prefetch ahead of the compute
+  // that follows it: left alone, the scheduler sinks later rows' loads below the
+  // (long) multi-row math to save registers, which serialises memory latency.
+  auto pin = [] {
+    if constexpr (MM > 1) __builtin_amdgcn_sched_barrier(0);
+  };
   load(wv0, sb0, 0);
+  pin();
 #pragma unroll
   for (int rb = 0; rb < RPW; rb += 2 * R) {
     if (rb + R < RPW) load(wv1, sb1, rb + R);
+    pin();
     compute(wv0, sb0, rb);
     if (rb + R < RPW) {
       if (rb + 2 * R < RPW) load(wv0, sb0, rb + 2 * R);
+      pin();
       compute(wv1, sb1, rb + R);
     }
   }
 
+  // Lane l now holds the total of partial index l >> (6 - LV); the first lane of
+  // each run of 64 / V lanes writes it.
+  const float tot = wave_sum_multi<V>(res, lane);
+  const int idx = lane >> (6 - LV);
+  const bool writer = (lane & ((64 >> LV) - 1)) == 0;
+  const int rr = idx / MM, mr = idx % MM;
+  const int64_t n = nbase + rr;
   if constexpr (KS > 1) {
-    if (lane == 0) {
-#pragma unroll
-      for (int r = 0; r < RPW; ++r) part[rg][ks][r] = res[r];
-    }
+    if (writer) part[rg][ks][idx] = tot;
     __syncthreads();
-    if (ks == 0 && lane < RPW) {
+    if (ks == 0 && writer) {
       float v = 0.f;
 #pragma unroll
-      for (int k = 0; k < KS; ++k) v += part[rg][k][lane];
-      const int64_t n = nbase + lane;
-      if (n < a.N) a.y[n] = finish_out(v, a.bias, n);
+      for (int k = 0; k < KS; ++k) v += part[rg][k][idx];
+      if (n < a.N && mr < a.M) a.y[(int64_t)mr * a.ldy + n] = finish_out(v, a.bias, n);
     }
   } else {
-    if (lane < RPW) {
-      float v = res[0];
-#pragma unroll
-      for (int r = 1; r < RPW; ++r) v = lane == r ? res[r] : v;
-      const int64_t n = nbase + lane;
-      if (n < a.N) a.y[n] = finish_out(v, a.bias, n);
-    }
+    if (writer && n < a.N && mr < a.M) a.y[(int64_t)mr * a.ldy + n] = finish_out(tot, a.bias, n);
   }
 }
 
-struct Qmv1Shape {
+struct QmvxShape {
   int ks, cpl, rpw;
 };
-// The fewest K slices (1, 2 or 4) that keep a lane at <= 2 chunks per row, and
-// more rows per wave for the longest rows, where building x costs the most.
-static Qmv1Shape pick_qmv1_shape(int64_t nch, int64_t N) {
-  Qmv1Shape sh{4, (int)((nch + 255) / 256), 4};
+// The fewest K slices (1, 2 or 4) that keep a lane at <= 2 chunks per row (x in
+// registers grows with MM), and more rows per wave for the longest rows, where
+// building x costs the most.  cpl 0 means the shape is not handled here.
+static QmvxShape pick_qmvx_shape(int64_t nch, int64_t N, int mm) {
+  QmvxShape sh{4, (int)((nch + 255) / 256), 4};
   if (nch <= 64) sh = {1, 1, 4};
   else if (nch <= 128) sh = {2, 1, 4};
   else if (nch <= 256) sh = {4, 1, 4};
   if (nch > 256 && sh.cpl <= 2) sh.rpw = 8;
   if (N <= 2048) sh.rpw = 2;
+  // Register budget: MM x CPL x-chunks of 17 VGPRs each.
+  const int max_cpl = mm == 1 ? 4 : mm == 2 ? 4 : mm == 4 ? 2 : 1;
+  if (sh.cpl > max_cpl) sh.cpl = 0;
+  if (sh.rpw * mm > 64) sh.rpw = 64 / mm;
+  if (mm == 8 && sh.rpw > 4) sh.rpw = 4;
   return sh;
 }
 
-template <int BITS, int CPL, int R, int RPW, int KS>
-static hipError_t launch_qmv1_cfg(const QmmArgs& a, hipStream_t stream) {
+template <int BITS, int MM, int CPL, int RPW, int KS>
+static hipError_t launch_qmvx_cfg(const QmmArgs& a, hipStream_t stream) {
   constexpr int64_t rows_per_block = (4 / KS) * RPW;
   const unsigned blocks = (unsigned)((a.N + rows_per_block - 1) / rows_per_block);
-  qmv1_kernel<BITS, CPL, R, RPW, KS><<<blocks, 256, 0, stream>>>(a);
+  qmvx_kernel<BITS, MM, CPL, 2, RPW, KS><<<blocks, 256, 0, stream>>>(a);
   return hipGetLastError();
 }
 
-template <int BITS, int CPL, int KS>
-static hipError_t launch_qmv1_rpw(const QmmArgs& a, int rpw, hipStream_t stream) {
-  if (rpw == 2) return launch_qmv1_cfg<BITS, CPL, 2, 2, KS>(a, stream);
-  if (rpw == 4) return launch_qmv1_cfg<BITS, CPL, 2, 4, KS>(a, stream);
-  return launch_qmv1_cfg<BITS, CPL, 2, 8, KS>(a, stream);
+template <int BITS, int MM, int CPL, int KS>
+static hipError_t launch_qmvx_rpw(const QmmArgs& a, int rpw, hipStream_t stream) {
+  if (rpw == 2) return launch_qmvx_cfg<BITS, MM, CPL, 2, KS>(a, stream);
+  if constexpr (MM <= 8) {
+    if (rpw == 4) return launch_qmvx_cfg<BITS, MM, CPL, 4, KS>(a, stream);
+  }
+  if constexpr (MM <= 4) return launch_qmvx_cfg<BITS, MM, CPL, 8, KS>(a, stream);
+  return launch_qmvx_cfg<BITS, MM, CPL, 4, KS>(a, stream);
 }
 
-// Chunks per lane above 4 (K beyond 32768 int4 values) use the general kernel.
-static bool qmv1_supported(const QmmArgs& a, int bits) {
+// The M <= 8 rows of x padded to 1, 2, 4 or 8; shapes whose x chunks would not
+// fit in registers use the general kernels.
+static int qmvx_mm(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
+
+static bool qmvx_supported(const QmmArgs& a, int bits) {
+  if (a.M < 1 || a.M > 8) return false;
   const int64_t nch = a.K / (128 / bits);
-  return a.M == 1 && pick_qmv1_shape(nch, a.N).cpl <= 4;
+  return pick_qmvx_shape(nch, a.N, qmvx_mm(a.M)).cpl > 0;
+}
+
+template <int BITS, int MM>
+static hipError_t launch_qmvx_mm(const QmmArgs& a, hipStream_t stream) {
+  const QmvxShape sh = pick_qmvx_shape(a.K / (128 / BITS), a.N, MM);
+  if (sh.ks == 1) return launch_qmvx_rpw<BITS, MM, 1, 1>(a, sh.rpw, stream);
+  if (sh.ks == 2) return launch_qmvx_rpw<BITS, MM, 1, 2>(a, sh.rpw, stream);
+  if (sh.cpl == 1) return launch_qmvx_rpw<BITS, MM, 1, 4>(a, sh.rpw, stream);
+  if constexpr (MM <= 4) {
+    if (sh.cpl == 2) return launch_qmvx_rpw<BITS, MM, 2, 4>(a, sh.rpw, stream);
+  }
+  if constexpr (MM <= 2) return launch_qmvx_rpw<BITS, MM, 4, 4>(a, sh.rpw, stream);
+  return hipErrorInvalidValue;  // excluded by qmvx_supported
 }
 
 template <int BITS>
-static hipError_t launch_qmv1(const QmmArgs& a, hipStream_t stream) {
-  const Qmv1Shape sh = pick_qmv1_shape(a.K / (128 / BITS), a.N);
-  if (sh.ks == 1) return launch_qmv1_rpw<BITS, 1, 1>(a, sh.rpw, stream);
-  if (sh.ks == 2) return launch_qmv1_rpw<BITS, 1, 2>(a, sh.rpw, stream);
-  if (sh.cpl == 1) return launch_qmv1_rpw<BITS, 1, 4>(a, sh.rpw, stream);
-  if (sh.cpl == 2) return launch_qmv1_rpw<BITS, 2, 4>(a, sh.rpw, stream);
-  return launch_qmv1_rpw<BITS, 4, 4>(a, sh.rpw, stream);
+static hipError_t launch_qmvx(const QmmArgs& a, hipStream_t stream) {
+  switch (qmvx_mm(a.M)) {
+    case 1: return launch_qmvx_mm<BITS, 1>(a, stream);
+    case 2: return launch_qmvx_mm<BITS, 2>(a, stream);
+    case 4: return launch_qmvx_mm<BITS, 4>(a, stream);
+    default: return launch_qmvx_mm<BITS, 8>(a, stream);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -326,10 +384,14 @@ static hipError_t launch_qmv_bits(const QmmArgs& a, hipStream_t stream) {
   }
 }
 
+bool qmv_supported(const QmmArgs& a) {
+  return a.M <= kQmvMaxM || qmvx_supported(a, a.bits);
+}
+
 hipError_t launch_qmv(const QmmArgs& a, hipStream_t stream) {
   if (a.M <= 0 || a.N <= 0) return hipSuccess;
-  if (qmv1_supported(a, a.bits))
-    return a.bits == 4 ? launch_qmv1<4>(a, stream) : launch_qmv1<8>(a, stream);
+  if (qmvx_supported(a, a.bits))
+    return a.bits == 4 ? launch_qmvx<4>(a, stream) : launch_qmvx<8>(a, stream);
   return a.bits == 4 ? launch_qmv_bits<4>(a, stream) : launch_qmv_bits<8>(a, stream);
 }
 

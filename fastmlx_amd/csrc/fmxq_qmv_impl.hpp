@@ -110,6 +110,80 @@ __device__ __forceinline__ float chunk_dot(const u32x4 wv, const XChunk<BITS>& x
   }
 }
 
+// The 16 exponent-trick bf16 pairs of one 16-byte weight chunk, unpacked once so
+// several x rows can be dotted against them: p[4j + t] = pair t of word j
+// (nibbles t and t+4 of the word).
+__device__ __forceinline__ void unpack_chunk(const u32x4 wv, uint32_t (&p)[16]) {
+  const uint32_t m = vgpr_const(kMagic);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t w = wv[j];
+    p[4 * j + 0] = nib_pair(w, m);
+    p[4 * j + 1] = nib_pair(w >> 4, m);
+    p[4 * j + 2] = nib_pair(w >> 8, m);
+    p[4 * j + 3] = nib_pair(w >> 12, m);
+  }
+}
+
+// chunk_dot() over pre-unpacked pairs.
+template <int BITS>
+__device__ __forceinline__ float dot_pairs(const uint32_t (&p)[16], const XChunk<BITS>& xc) {
+  if constexpr (BITS == 4) {
+    float d = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) d = dot2_bf16(p[i], xc.p[i], d);
+    return d;
+  } else {
+    float dl = 0.f, dh = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      dl = dot2_bf16(p[4 * j + 0], xc.p[2 * j + 0], dl);
+      dh = dot2_bf16(p[4 * j + 1], xc.p[2 * j + 0], dh);
+      dl = dot2_bf16(p[4 * j + 2], xc.p[2 * j + 1], dl);
+      dh = dot2_bf16(p[4 * j + 3], xc.p[2 * j + 1], dh);
+    }
+    return dl + 16.f * dh;
+  }
+}
+
+// Sums V per-lane partials over the 64 lanes in one pass (V a power of two <= 64):
+// at each offset o = 32, 16, ... the lanes with bit o set keep the upper half of
+// their values and swap the lower half with their partner, halving the count.
+// Lane l returns the total of value index l >> (6 - log2 V); every lane with the
+// same index holds the same total.  Costs about V + log2(64/V) shuffle-adds
+// instead of V full reductions.
+// The halves are chosen with a bit select through an opaque mask: written as
+// `up ? v[a] : v[b]`, the compiler folds the select into a lane-dependent array
+// index, which forces v[] out of registers (into LDS).
+template <int V>
+__device__ __forceinline__ float wave_sum_multi(float (&v)[V], int lane) {
+  static_assert(V >= 1 && V <= 64 && (V & (V - 1)) == 0, "V must be a power of two <= 64");
+#pragma unroll
+  for (int c = V, o = 32; c > 1; c >>= 1, o >>= 1) {
+    uint32_t msk = (lane & o) ? 0xffffffffu : 0u;
+    asm("" : "+v"(msk));
+#pragma unroll
+    for (int i = 0; i < c / 2; ++i) {
+      const uint32_t lo = __float_as_uint(v[i]), hi = __float_as_uint(v[c / 2 + i]);
+      const float keep = __uint_as_float((msk & hi) | (~msk & lo));
+      const float send = __uint_as_float((msk & lo) | (~msk & hi));
+      v[i] = keep + __shfl_xor(send, o, 64);
+    }
+  }
+  // The lanes sharing an index form aligned groups of G = 64 / V.  Within a row of
+  // 16 lanes the group sum uses DPP (quad swaps, half-row and row mirrors); wider
+  // groups fall back to cross-row shuffles.
+  constexpr int G = 64 / V;
+  float s = v[0];
+  if constexpr (G >= 2) s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0xb1, 0xf, 0xf, false));
+  if constexpr (G >= 4) s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x4e, 0xf, 0xf, false));
+  if constexpr (G >= 8) s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x141, 0xf, 0xf, false));
+  if constexpr (G >= 16) s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x140, 0xf, 0xf, false));
+  if constexpr (G >= 32) s += __shfl_xor(s, 16, 64);
+  if constexpr (G >= 64) s += __shfl_xor(s, 32, 64);
+  return s;
+}
+
 // Offset that turns the exponent-trick dot product back into sum x*q.
 template <int BITS>
 __device__ __forceinline__ constexpr float magic_offset() {
