@@ -59,7 +59,7 @@ def stack_bytes(M, layers, bits):
     return layers * sum(qmm_bytes(M, N, K, bits, GROUP) for _, N, K in LLAMA_PROJ)
 
 
-QMV_UP_PMC = os.path.join(ROOT, "profiles", "qmv1_gate_up_14336x4096_M1_traffic.md")
+QMV_UP_PMC = os.path.join(ROOT, "profiles", "qmvx_gate_up_14336x4096_M1_traffic.md")
 
 
 def measured_traffic(path):
@@ -235,7 +235,7 @@ def main():
         roof = {"bound": "hbm", "achieved": round(gbps_up, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(gbps_up / HBM_PEAK_GBS, 4),
                 "traffic": measured_traffic(QMV_UP_PMC),
-                "kernel": "fmxq::qmv1_kernel<4,1,2,4,2> (gate/up 14336x4096, M=1)",
+                "kernel": "fmxq::qmvx_kernel<4,1,1,2,4,2> (gate/up 14336x4096, M=1)",
                 "bytes_per_launch": by_up,
                 "timing": "HIP events over a graph of %d back-to-back launches on distinct "
                           "weight copies; per-launch = total / launches" % n_up}

@@ -1,18 +1,17 @@
-// fmxq_qmv.hip -- decode GEMV (M <= 4) for quantized_matmul and the per-slot
+// fmxq_qmv.hip -- decode GEMV (M <= 8) for quantized_matmul and the per-slot
 // gathered GEMV of gather_qmm.
 //
 // Replaces the decode side of mlx_quantized_matmul (mlxgo/binding_cgo.go:636-643,
 // reached from compute/models/quant.go:91-101 on every decode step) and the
 // short-routing gather of mlx_gather_qmm (switch_glu.go:124-130 -> :179-186).
 //
-// Dense GEMV layout of work: a block is 4 waves.  The K axis is split into KS
-// slices (KS in {1, 2, 4}) so that every wave owns at most CPL 16-byte chunks
-// per row; the 4/KS row groups of a block each take R rows, and the KS waves
-// of a row group split its K axis and meet in LDS at the end.  Every weight
-// load of a wave is issued before any arithmetic, so a wave keeps
-// R*CPL*64*16 bytes in flight; the wave-wide sum is a DPP reduction.
-// The arithmetic per chunk is chunk_dot() (fmxq_qmv_impl.hpp): bf16(128+q)
-// operands from the exponent trick against x pairs, v_dot2_f32_bf16.
+// qmvx_kernel (below) is the main decode kernel: x rows live in registers and a
+// wave walks several weight rows.  qmv_kernel is the general M <= 4 fallback for
+// rows too long to keep x in registers: a block is 4 waves, the K axis is split
+// into KS slices so that every wave owns at most CPL 16-byte chunks per row, and
+// every weight load of a wave is issued before any arithmetic.  The arithmetic
+// per chunk is chunk_dot() (fmxq_qmv_impl.hpp): bf16(128+q) operands from the
+// exponent trick against x pairs, v_dot2_f32_bf16.
 #include "fmxq_internal.hpp"
 #include "fmxq_qmv_impl.hpp"
 
@@ -38,8 +37,9 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 // ---------------------------------------------------------------------------
 // Decode GEMV for M <= 8 with x held in registers.
 //
-// A block is 4 waves: 4/KS row groups x KS slices of the K axis.  Lane l of the
-// wave for slice ks owns 16-byte chunks c0 + l + 64 i (i < CPL) of every row the
+// A block is WAVES (4 or 8) waves: WAVES/KS row groups x KS slices of the K
+// axis.  Lane l of the wave for slice ks owns 16-byte chunks c0 + l + 64 i
+// (i < CPL) of every row the
 // wave visits, so it builds the x pairs and x sums of those chunks (for each of
 // the MM rows of x) once and keeps them in registers while the wave walks RPW
 // weight rows, R rows at a time, with the next R rows' weights already in flight
@@ -48,10 +48,10 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 // VALU) and dotted against every x row (4 v_dot2 each); a 3-op group correction
 // per chunk and row follows.  The RPW x MM partial sums are reduced together at
 // the end (wave_sum_multi).
-template <int BITS, int MM, int CPL, int R, int RPW, int KS>
-__global__ __launch_bounds__(256) void qmvx_kernel(QmmArgs a) {
+template <int BITS, int MM, int CPL, int R, int RPW, int KS, int WAVES = 4>
+__global__ __launch_bounds__(WAVES * 64) void qmvx_kernel(QmmArgs a) {
   constexpr int CH = 128 / BITS;  // values per 16-byte chunk
-  constexpr int RG = 4 / KS;
+  constexpr int RG = WAVES / KS;
   constexpr int V = RPW * MM;     // partial sums per lane
   constexpr int LV = __builtin_ctz(V);
   static_assert(RPW % R == 0, "rows per wave must be a multiple of R");
@@ -176,16 +176,16 @@ __global__ __launch_bounds__(256) void qmvx_kernel(QmmArgs a) {
 }
 
 struct QmvxShape {
-  int ks, cpl, rpw;
+  int ks, cpl, rpw, waves;
 };
 // The fewest K slices (1, 2 or 4) that keep a lane at <= 2 chunks per row (x in
 // registers grows with MM), and more rows per wave for the longest rows, where
 // building x costs the most.  cpl 0 means the shape is not handled here.
 static QmvxShape pick_qmvx_shape(int64_t nch, int64_t N, int mm) {
-  QmvxShape sh{4, (int)((nch + 255) / 256), 4};
-  if (nch <= 64) sh = {1, 1, 4};
-  else if (nch <= 128) sh = {2, 1, 4};
-  else if (nch <= 256) sh = {4, 1, 4};
+  QmvxShape sh{4, (int)((nch + 255) / 256), 4, 4};
+  if (nch <= 64) sh = {1, 1, 4, 4};
+  else if (nch <= 128) sh = {2, 1, 4, 4};
+  else if (nch <= 256) sh = {4, 1, 4, 4};
   if (nch > 256 && sh.cpl <= 2) sh.rpw = 8;
   if (N <= 2048) sh.rpw = 2;
   // Register budget: MM x CPL x-chunks of 17 VGPRs each.
@@ -193,25 +193,32 @@ static QmvxShape pick_qmvx_shape(int64_t nch, int64_t N, int mm) {
   if (sh.cpl > max_cpl) sh.cpl = 0;
   if (sh.rpw * mm > 64) sh.rpw = 64 / mm;
   if (mm == 8 && sh.rpw > 4) sh.rpw = 4;
+  // Eight rows of x and long rows: eight K slices (8-wave blocks) keep one chunk
+  // per lane.
+  if (mm == 8 && nch > 256 && nch <= 512) {
+    sh.ks = 8;
+    sh.cpl = 1;
+    sh.waves = 8;
+  }
   return sh;
 }
 
-template <int BITS, int MM, int CPL, int RPW, int KS>
+template <int BITS, int MM, int CPL, int RPW, int KS, int WAVES>
 static hipError_t launch_qmvx_cfg(const QmmArgs& a, hipStream_t stream) {
-  constexpr int64_t rows_per_block = (4 / KS) * RPW;
+  constexpr int64_t rows_per_block = (WAVES / KS) * RPW;
   const unsigned blocks = (unsigned)((a.N + rows_per_block - 1) / rows_per_block);
-  qmvx_kernel<BITS, MM, CPL, 2, RPW, KS><<<blocks, 256, 0, stream>>>(a);
+  qmvx_kernel<BITS, MM, CPL, 2, RPW, KS, WAVES><<<blocks, WAVES * 64, 0, stream>>>(a);
   return hipGetLastError();
 }
 
-template <int BITS, int MM, int CPL, int KS>
+template <int BITS, int MM, int CPL, int KS, int WAVES = 4>
 static hipError_t launch_qmvx_rpw(const QmmArgs& a, int rpw, hipStream_t stream) {
-  if (rpw == 2) return launch_qmvx_cfg<BITS, MM, CPL, 2, KS>(a, stream);
+  if (rpw == 2) return launch_qmvx_cfg<BITS, MM, CPL, 2, KS, WAVES>(a, stream);
   if constexpr (MM <= 8) {
-    if (rpw == 4) return launch_qmvx_cfg<BITS, MM, CPL, 4, KS>(a, stream);
+    if (rpw == 4) return launch_qmvx_cfg<BITS, MM, CPL, 4, KS, WAVES>(a, stream);
   }
-  if constexpr (MM <= 4) return launch_qmvx_cfg<BITS, MM, CPL, 8, KS>(a, stream);
-  return launch_qmvx_cfg<BITS, MM, CPL, 4, KS>(a, stream);
+  if constexpr (MM <= 4) return launch_qmvx_cfg<BITS, MM, CPL, 8, KS, WAVES>(a, stream);
+  return launch_qmvx_cfg<BITS, MM, CPL, 4, KS, WAVES>(a, stream);
 }
 
 // The M <= 8 rows of x padded to 1, 2, 4 or 8; shapes whose x chunks would not
@@ -227,6 +234,7 @@ static bool qmvx_supported(const QmmArgs& a, int bits) {
 template <int BITS, int MM>
 static hipError_t launch_qmvx_mm(const QmmArgs& a, hipStream_t stream) {
   const QmvxShape sh = pick_qmvx_shape(a.K / (128 / BITS), a.N, MM);
+  if (sh.ks == 8) return launch_qmvx_rpw<BITS, MM, 1, 8, 8>(a, sh.rpw, stream);
   if (sh.ks == 1) return launch_qmvx_rpw<BITS, MM, 1, 1>(a, sh.rpw, stream);
   if (sh.ks == 2) return launch_qmvx_rpw<BITS, MM, 1, 2>(a, sh.rpw, stream);
   if (sh.cpl == 1) return launch_qmvx_rpw<BITS, MM, 1, 4>(a, sh.rpw, stream);
