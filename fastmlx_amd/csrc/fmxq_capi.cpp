@@ -195,6 +195,7 @@ int qmm_common(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
   if (fmxq::qmv_supported(a)) return hip_status(fmxq::launch_qmv(a, s), op);
   if (M <= fmxq::kSkinnyMaxM && fmxq::qmv_mfma_supported(a))
     return hip_status(fmxq::launch_qmv_mfma(a, s), op);
+  if (fmxq::qmm_prefill_supported(a)) return hip_status(fmxq::launch_qmm_prefill(a, s), op);
   const fmxq::QmmPlan plan = fmxq::qmm_plan(M, N, K);
   if (plan.splits > 1) {
     if (int rc = split_workspace(s, plan, &a.ws, &a.tile_count)) return rc;

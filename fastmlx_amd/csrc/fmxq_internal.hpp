@@ -88,6 +88,12 @@ struct QmmPlan {
 QmmPlan qmm_plan(int64_t M, int64_t N, int64_t K);
 hipError_t launch_qmm(const QmmArgs& a, hipStream_t stream);
 
+// Prefill GEMM for M > kPrefillMinM (fmxq_qmm_prefill.hip): K a multiple of 64,
+// x rows 16-byte aligned, 4- or 8-bit with group_size >= 32, no split-K.
+constexpr int64_t kPrefillMinM = 64;
+bool qmm_prefill_supported(const QmmArgs& a);
+hipError_t launch_qmm_prefill(const QmmArgs& a, hipStream_t stream);
+
 hipError_t launch_gather_qmv(const GatherArgs& a, hipStream_t stream);
 
 // MoE pieces around gather_qmm (fmxq_moe.hip).

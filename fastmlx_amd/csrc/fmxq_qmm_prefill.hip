@@ -1,0 +1,376 @@
+// fmxq_qmm_prefill.hip -- MFMA GEMM for quantized_matmul at prefill sizes (M > 64).
+//
+// Replaces the GEMM side of mlx_quantized_matmul (mlxgo/binding_cgo.go:636-643)
+// for x [M, K] with M = batch * seq rows (prefill at batch_generator.go:258).
+//
+// Block tile BM x BN over 64-deep K steps, 8 waves in a WM x WN grid (two waves
+// per SIMD), each wave owning a (BM/WM) x (BN/WN) patch of
+// v_mfma_f32_32x32x16_bf16 tiles.  Per step the block
+//   - copies the x tile (BM rows x 128 bytes) global -> LDS with buffer_load ...
+//     lds (no VGPR staging), two steps ahead, into one of three x stages;
+//   - loads the packed weight tile two steps ahead into registers and, one step
+//     later, dequantizes it into one of two bf16 weight stages in LDS:
+//     w = bf16(s * q + b), for 4-bit one v_dot2_f32_bf16 per value on
+//     (128 + q, exponent trick) x (s, 0) plus (b - 128 s), products exact;
+//   - runs its MFMAs from LDS in four k16 sub-steps, fragments read one
+//     sub-step ahead.
+// One barrier per step.  Before it each wave waits only for the loads issued one
+// step earlier, so this step's loads stay in flight across it; the barrier sits
+// before the last sub-step's MFMAs so those overlap the next step's first
+// fragment reads.
+//
+// LDS rows are 128 bytes (64 bf16 along K) with 16-byte chunk c of row r stored
+// at position c ^ swz(r): 32 consecutive rows read at one chunk hit distinct
+// banks both as 8 rows per 128 bytes and as 16 rows per 256 bytes.
+//
+// The MFMA A operand is the weight fragment and B the x fragment, so a lane
+// holds 4 consecutive output columns of one row and stores them as 8 bytes.
+#include "fmxq_common.hpp"
+#include "fmxq_internal.hpp"
+
+namespace fmxq {
+namespace {
+
+typedef __attribute__((address_space(3))) void lds_t;
+
+constexpr int kStepK = 64;
+
+__device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+// s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding, expcnt left alone).
+#define FMXQ_WAIT_VM_LGKM0(n) \
+  __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4))
+
+// One 4-bit word (values q0..q7, least significant first) -> bf16 pairs
+// (w0,w1) (w2,w3) (w4,w5) (w6,w7) of w = s*q + b.  p_i holds bf16(128 + q_i)
+// and bf16(128 + q_{i+4}); s_lo / s_hi are the pairs (s, 0) / (0, s) and
+// c = b - 128 s.
+__device__ __forceinline__ void dequant_word4(uint32_t w, uint32_t s_lo, uint32_t s_hi, float c,
+                                              uint32_t magic, uint32_t* out) {
+  constexpr uint32_t K = 0x000F000Fu;
+  const uint32_t p0 = (w & K) | magic, p1 = ((w >> 4) & K) | magic;
+  const uint32_t p2 = ((w >> 8) & K) | magic, p3 = ((w >> 12) & K) | magic;
+  out[0] = pack_bf16x2(dot2_bf16(p0, s_lo, c), dot2_bf16(p1, s_lo, c));
+  out[1] = pack_bf16x2(dot2_bf16(p2, s_lo, c), dot2_bf16(p3, s_lo, c));
+  out[2] = pack_bf16x2(dot2_bf16(p0, s_hi, c), dot2_bf16(p1, s_hi, c));
+  out[3] = pack_bf16x2(dot2_bf16(p2, s_hi, c), dot2_bf16(p3, s_hi, c));
+}
+// Two 8-bit words (values e0..e7) -> 4 bf16 pairs of w = s*q + b.
+__device__ __forceinline__ void dequant_words8(uint32_t w0, uint32_t w1, float s, float b,
+                                               uint32_t* out) {
+  out[0] = pack_bf16x2(__builtin_fmaf(s, (float)(w0 & 0xffu), b),
+                       __builtin_fmaf(s, (float)((w0 >> 8) & 0xffu), b));
+  out[1] = pack_bf16x2(__builtin_fmaf(s, (float)((w0 >> 16) & 0xffu), b),
+                       __builtin_fmaf(s, (float)(w0 >> 24), b));
+  out[2] = pack_bf16x2(__builtin_fmaf(s, (float)(w1 & 0xffu), b),
+                       __builtin_fmaf(s, (float)((w1 >> 8) & 0xffu), b));
+  out[3] = pack_bf16x2(__builtin_fmaf(s, (float)((w1 >> 16) & 0xffu), b),
+                       __builtin_fmaf(s, (float)(w1 >> 24), b));
+}
+
+template <int BITS, int BM, int BN, int WM, int WN>
+struct PrefillTile {
+  static constexpr int T = WM * WN * 64;                 // threads
+  static constexpr int WTM = BM / WM, WTN = BN / WN;     // wave patch
+  static constexpr int TM = WTM / 32, TN = WTN / 32;     // 32x32 tiles per wave
+  // A weight unit is UW words (16 or 8 bytes) of one row; each thread owns BU
+  // units per step.
+  static constexpr int UW = (BN * (kStepK * BITS / 128) >= T) ? 4 : 2;
+  static constexpr int CHU = UW * 32 / BITS;             // values per unit
+  static constexpr int UPR = kStepK / CHU;               // units per row
+  static constexpr int BU = BN * UPR / T;
+  static constexpr int NWD = BITS == 4 ? UW : UW / 2;    // 16-byte chunks per unit
+  static constexpr int AI = BM * 128 / 1024 / (T / 64);  // x DMA instructions per wave
+  static constexpr int NV = AI + 3 * BU;                 // loads each thread issues per step
+  static_assert(WM * WN == 8, "8 waves");
+  static_assert(BU >= 1 && BN * UPR == BU * T, "weight units");
+  static_assert(AI >= 1 && AI * (T / 64) * 1024 == BM * 128, "x DMA split");
+  static_assert(TM >= 1 && TN >= 1, "wave patch");
+  static_assert(3 * BM * 128 + 2 * BN * 128 <= 160 * 1024, "LDS budget");
+};
+
+template <int BITS, int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(WM * WN * 64, 1) void qmm_prefill_kernel(QmmArgs a) {
+  using P = PrefillTile<BITS, BM, BN, WM, WN>;
+  constexpr int T = P::T, TM = P::TM, TN = P::TN, UW = P::UW, BU = P::BU, AI = P::AI;
+  constexpr int NWD = P::NWD;
+  // Three x stages and two weight stages, each its own LDS object so the
+  // compiler can tell reads of one stage from the DMA into another.
+  __shared__ __attribute__((aligned(1024))) uint8_t xs0[BM * 128];
+  __shared__ __attribute__((aligned(1024))) uint8_t xs1[BM * 128];
+  __shared__ __attribute__((aligned(1024))) uint8_t xs2[BM * 128];
+  __shared__ __attribute__((aligned(1024))) uint8_t ws0[BN * 128];
+  __shared__ __attribute__((aligned(1024))) uint8_t ws1[BN * 128];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+
+  // Blocks are dealt to the 8 XCDs round robin; consecutive tiles (M fastest)
+  // go to one XCD so its resident blocks share weight rows through its L2.
+  const int nt_m = (int)((a.M + BM - 1) / BM);
+  const int nblk = gridDim.x;
+  int t = blockIdx.x;
+  if ((nblk & 7) == 0) t = (t & 7) * (nblk >> 3) + (t >> 3);
+  const int64_t m0 = (int64_t)(t % nt_m) * BM;
+  const int64_t n0 = (int64_t)(t / nt_m) * BN;
+
+  const int64_t wpr = a.K * BITS / 32;
+  const int gshift = __builtin_ctz((unsigned)a.group_size);
+  const int64_t gpr = a.K >> gshift;
+  const int nk = (int)(a.K / kStepK);
+
+  // x rows of this block through a buffer resource: rows past M read as zero.
+  const int64_t rows_here = a.M - m0 < BM ? a.M - m0 : BM;
+  const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.x + m0 * a.ldx), (short)0, (int)(rows_here * a.ldx * 2), 0x00020000);
+  // DMA instruction j of this wave fills rows 8 (wave AI + j) .. +8 of a stage:
+  // lane L lands at row + L/8, position L%8, so it fetches chunk (L%8) ^ swz(row).
+  uint32_t aoff[AI];
+#pragma unroll
+  for (int j = 0; j < AI; ++j) {
+    const int row = 8 * (wave * AI + j) + (lane >> 3);
+    const int c = (lane & 7) ^ swz(row);
+    aoff[j] = (uint32_t)((row * a.ldx + c * 8) * 2);
+  }
+
+  const uint32_t* wrow[BU];
+  int64_t srow[BU];
+  int u_row[BU], u_idx[BU];
+#pragma unroll
+  for (int i = 0; i < BU; ++i) {
+    const int q = tid + T * i;
+    u_row[i] = q / P::UPR;
+    u_idx[i] = q % P::UPR;
+    int64_t n = n0 + u_row[i];
+    if (n > a.N - 1) n = a.N - 1;  // rows past N load row N-1; their outputs are not stored
+    wrow[i] = a.w + n * wpr + u_idx[i] * UW;
+    srow[i] = n * gpr;
+  }
+
+  typedef uint32_t uvec __attribute__((ext_vector_type(UW)));
+  auto issue_x = [&](int kt, uint8_t* xs) {
+    kt = kt < nk ? kt : nk - 1;
+    const int soff = kt * kStepK * 2;
+#pragma unroll
+    for (int j = 0; j < AI; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (lds_t*)(xs + (wave * AI + j) * 1024), 16,
+                                               (int)aoff[j], soff, 0, 0);
+  };
+  auto load_w = [&](int kt, uvec* wq, uint32_t* sq, uint32_t* bq) {
+    kt = kt < nk ? kt : nk - 1;
+    const int64_t k0 = (int64_t)kt * kStepK;
+#pragma unroll
+    for (int i = 0; i < BU; ++i) {
+      wq[i] = __builtin_nontemporal_load(reinterpret_cast<const uvec*>(wrow[i] + k0 * BITS / 32));
+      const int64_t g = (k0 + u_idx[i] * P::CHU) >> gshift;
+      sq[i] = a.scales[srow[i] + g];
+      bq[i] = a.biases[srow[i] + g];
+    }
+  };
+  // Dequantize chunk v of every unit of this thread into weight stage ws.
+  auto store_chunk = [&](uint8_t* ws, const uvec* wq, const uint32_t* sq, const uint32_t* bq, int v) {
+    const uint32_t magic = vgpr_const(0x43004300u);
+#pragma unroll
+    for (int i = 0; i < BU; ++i) {
+      const int r = u_row[i];
+      uint32_t d[4];
+      if constexpr (BITS == 4) {
+        const float c = __builtin_fmaf(-128.f, bf16_bits_to_f32(sq[i]), bf16_bits_to_f32(bq[i]));
+        dequant_word4(wq[i][v], sq[i], sq[i] << 16, c, magic, d);
+      } else {
+        dequant_words8(wq[i][2 * v], wq[i][2 * v + 1], bf16_bits_to_f32(sq[i]),
+                       bf16_bits_to_f32(bq[i]), d);
+      }
+      const int ch = u_idx[i] * NWD + v;
+      *reinterpret_cast<u32x4*>(ws + r * 128 + ((ch ^ swz(r)) << 4)) = u32x4{d[0], d[1], d[2], d[3]};
+    }
+  };
+
+  // Fragment offsets: row (lane % 32) of each 32-row tile, chunk 2 s + lane / 32.
+  const int fr = lane & 31, fh = lane >> 5;
+  uint32_t xro[4], wro[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int rx = wm * P::WTM + fr, rw = wn * P::WTN + fr;
+    xro[s] = rx * 128 + (((2 * s + fh) ^ swz(rx)) << 4);
+    wro[s] = rw * 128 + (((2 * s + fh) ^ swz(rw)) << 4);
+  }
+
+  // acc[i][j]: lane l holds output row 32 i + l % 32 of the wave patch and, in
+  // register r, column 32 j + 8 (r / 4) + 4 (l / 32) + r % 4.
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  auto read_frags = [&](const uint8_t* xs, const uint8_t* ws, int s, bf16x8* xf, bf16x8* wf) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) xf[i] = *reinterpret_cast<const bf16x8*>(xs + xro[s] + i * 32 * 128);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) wf[j] = *reinterpret_cast<const bf16x8*>(ws + wro[s] + j * 32 * 128);
+  };
+  auto mfmas = [&](const bf16x8* xf, const bf16x8* wf) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[j], xf[i], acc[i][j], 0, 0, 0);
+  };
+
+  uvec w0[BU], w1[BU];
+  uint32_t s0[BU], s1[BU], b0[BU], b1[BU];
+  bf16x8 xf0[TM], wf0[TN], xf1[TM], wf1[TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) xf1[i] = bf16x8{};
+#pragma unroll
+  for (int j = 0; j < TN; ++j) wf1[j] = bf16x8{};
+
+  auto dequant_part = [&](uint8_t* ws, const uvec* wq, const uint32_t* sq, const uint32_t* bq,
+                          int part) {
+#pragma unroll
+    for (int v = 0; v < NWD; ++v)
+      if (v * 3 / NWD == part) store_chunk(ws, wq, sq, bq, v);
+  };
+  // Step kt reads x stage kt%3 and weight stage kt%2.  It loads the weights of
+  // step kt+2 into register set kt%2, DMAs the x of step kt+2 into stage
+  // (kt+2)%3 and dequantizes the weights of step kt+1 (register set (kt+1)%2,
+  // loaded one step earlier) into weight stage (kt+1)%2 across sub-steps 0..2.
+  // The first step's "previous" MFMAs run on zero fragments.  sched_barrier
+  // keeps each sub-step's fragment reads ahead of the MFMAs they feed.
+  auto step = [&](const uint8_t* xr, const uint8_t* wr, uint8_t* xn, uint8_t* wn_, int kt,
+                  uvec* wl, uint32_t* sl, uint32_t* bl, const uvec* wd_in,
+                  const uint32_t* sd_in, const uint32_t* bd_in) {
+    read_frags(xr, wr, 0, xf0, wf0);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(xf1, wf1);
+    load_w(kt + 2, wl, sl, bl);
+    issue_x(kt + 2, xn);
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(xr, wr, 1, xf1, wf1);
+    __builtin_amdgcn_sched_barrier(0);
+    // The empty asm keeps arithmetic on the weights loaded one step earlier from
+    // being hoisted up to their loads, which would wait for them too early.
+    uvec wd[BU];
+    uint32_t sd[BU], bd[BU];
+#pragma unroll
+    for (int i = 0; i < BU; ++i) {
+      wd[i] = wd_in[i];
+      sd[i] = sd_in[i];
+      bd[i] = bd_in[i];
+      asm volatile("" : "+v"(wd[i]), "+v"(sd[i]), "+v"(bd[i]));
+    }
+    mfmas(xf0, wf0);
+    dequant_part(wn_, wd, sd, bd, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(xr, wr, 2, xf0, wf0);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(xf1, wf1);
+    dequant_part(wn_, wd, sd, bd, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(xr, wr, 3, xf1, wf1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(xf0, wf0);
+    dequant_part(wn_, wd, sd, bd, 2);
+    FMXQ_WAIT_VM_LGKM0(P::NV);
+    __builtin_amdgcn_s_barrier();
+  };
+
+  issue_x(0, xs0);
+  issue_x(1, xs1);
+  load_w(0, w0, s0, b0);
+  load_w(1, w1, s1, b1);
+  FMXQ_WAIT_VM_LGKM0(0);
+#pragma unroll
+  for (int v = 0; v < NWD; ++v) store_chunk(ws0, w0, s0, b0, v);
+  FMXQ_WAIT_VM_LGKM0(0);
+  __builtin_amdgcn_s_barrier();
+
+  // Six steps per iteration so every stage and register set is a fixed name.
+#define FMXQ_STEP(j)                                                                         \
+  step((j) % 3 == 0 ? xs0 : (j) % 3 == 1 ? xs1 : xs2, (j) % 2 ? ws1 : ws0,                   \
+       ((j) + 2) % 3 == 0 ? xs0 : ((j) + 2) % 3 == 1 ? xs1 : xs2, (j) % 2 ? ws0 : ws1, kt + (j), \
+       (j) % 2 ? w1 : w0, (j) % 2 ? s1 : s0, (j) % 2 ? b1 : b0, (j) % 2 ? w0 : w1,             \
+       (j) % 2 ? s0 : s1, (j) % 2 ? b0 : b1)
+  int kt = 0;
+  for (; kt + 6 <= nk; kt += 6) {
+    FMXQ_STEP(0); FMXQ_STEP(1); FMXQ_STEP(2); FMXQ_STEP(3); FMXQ_STEP(4); FMXQ_STEP(5);
+  }
+  switch (nk - kt) {
+    case 5: FMXQ_STEP(0); FMXQ_STEP(1); FMXQ_STEP(2); FMXQ_STEP(3); FMXQ_STEP(4); break;
+    case 4: FMXQ_STEP(0); FMXQ_STEP(1); FMXQ_STEP(2); FMXQ_STEP(3); break;
+    case 3: FMXQ_STEP(0); FMXQ_STEP(1); FMXQ_STEP(2); break;
+    case 2: FMXQ_STEP(0); FMXQ_STEP(1); break;
+    case 1: FMXQ_STEP(0); break;
+    default: break;
+  }
+#undef FMXQ_STEP
+  mfmas(xf1, wf1);
+
+  // Epilogue: bf16 (round to nearest even), then the optional additive bias as a
+  // second bf16 add (the qlinear-then-add chain, compute/models/quant.go:105-111).
+  const bool fast = ((a.ldy & 3) == 0) && ((reinterpret_cast<uintptr_t>(a.y) & 7) == 0);
+  const int64_t m_l = m0 + wm * P::WTM + fr;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int64_t m = m_l + i * 32;
+    if (m >= a.M) continue;
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int64_t n = n0 + wn * P::WTN + j * 32 + 8 * g + 4 * fh;
+        if (n >= a.N) continue;
+        uint32_t p0 = pack_bf16x2(acc[i][j][4 * g], acc[i][j][4 * g + 1]);
+        uint32_t p1 = pack_bf16x2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+        if (a.bias) {
+          float bv[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bv[e] = n + e < a.N ? bf16_bits_to_f32(a.bias[n + e]) : 0.f;
+          p0 = pack_bf16x2(bf16_lo(p0) + bv[0], bf16_hi(p0) + bv[1]);
+          p1 = pack_bf16x2(bf16_lo(p1) + bv[2], bf16_hi(p1) + bv[3]);
+        }
+        uint16_t* dst = a.y + m * a.ldy + n;
+        if (fast && n + 3 < a.N) {
+          *reinterpret_cast<u32x2*>(dst) = u32x2{p0, p1};
+        } else {
+          const uint16_t v[4] = {(uint16_t)p0, (uint16_t)(p0 >> 16), (uint16_t)p1,
+                                 (uint16_t)(p1 >> 16)};
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < a.N) dst[e] = v[e];
+        }
+      }
+  }
+}
+
+template <int BITS, int BM, int BN, int WM, int WN>
+hipError_t launch_tile(const QmmArgs& a, hipStream_t stream) {
+  const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+  qmm_prefill_kernel<BITS, BM, BN, WM, WN><<<(unsigned)tiles, WM * WN * 64, 0, stream>>>(a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool qmm_prefill_supported(const QmmArgs& a) {
+  return a.M > kPrefillMinM && a.K % kStepK == 0 && a.K > 0 && a.ldx % 8 == 0 &&
+         (a.bits == 4 || a.bits == 8) && a.group_size >= 32 && a.splits == 1 &&
+         (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
+         (reinterpret_cast<uintptr_t>(a.w) & 15) == 0 &&
+         // the per-block x buffer resource counts bytes in 32 bits
+         256 * a.ldx * 2 < ((int64_t)1 << 31) && a.N < ((int64_t)1 << 31) / 256;
+}
+
+hipError_t launch_qmm_prefill(const QmmArgs& a, hipStream_t stream) {
+  if (!qmm_prefill_supported(a)) return hipErrorInvalidValue;
+  // 128 x 256 tiles for M <= 128 (4-bit; the 8-bit form of that tile spills).
+  if (a.bits == 8) return launch_tile<8, 256, 128, 4, 2>(a, stream);
+  if (a.M > 128) return launch_tile<4, 256, 128, 4, 2>(a, stream);
+  return launch_tile<4, 128, 256, 2, 4>(a, stream);
+}
+
+}  // namespace fmxq

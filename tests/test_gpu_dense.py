@@ -122,6 +122,22 @@ def test_qmm_ragged_n(gpu, oracle):
     _qmm_case(gpu, oracle, 130, 77, 160, 8, 32, seed=7)
 
 
+@pytest.mark.parametrize("M,N,K,bits,group", [
+    (65, 333, 64, 4, 64),        # one K step; 128x256 tile with ragged N
+    (129, 1000, 320, 4, 32),     # five steps (tail only); first 256x128 size
+    (257, 256, 448, 4, 64),      # seven steps: one six-step pass plus a tail of one
+    (200, 192, 640, 4, 128),     # ten steps: a tail of four
+    (300, 520, 832, 8, 64),      # thirteen steps, 8-bit, ragged M and N
+    (100, 384, 1024, 8, 32),     # 8-bit at M <= 128 takes the 256x128 tile
+    (512, 128, 2048, 8, 128),
+    (1000, 2048, 768, 4, 64),
+])
+def test_qmm_prefill_tiles(gpu, oracle, M, N, K, bits, group):
+    """The M > 64 prefill GEMM: every step-count remainder of its six-step loop,
+    both tiles, ragged M and N, both bit widths and every group size."""
+    _qmm_case(gpu, oracle, M, N, K, bits, group, seed=7000 + M + N + K + bits + group)
+
+
 @pytest.mark.parametrize("M", [5, 7, 8, 9, 13, 16, 17, 24, 25, 31, 32])
 @pytest.mark.parametrize("bits,group,K", [(4, 64, 192), (4, 128, 1024), (8, 32, 96),
                                           (8, 64, 2048)])
@@ -131,7 +147,7 @@ def test_skinny_mfma_rows_and_groups(gpu, oracle, M, bits, group, K):
     _qmm_case(gpu, oracle, M, 333, K, bits, group, seed=900 + M * 3 + bits + group)
 
 
-@pytest.mark.parametrize("M", [1, 9, 70])
+@pytest.mark.parametrize("M", [1, 9, 70, 300])
 def test_qlinear_bias_epilogue(gpu, oracle, M):
     _qmm_case(gpu, oracle, M, 512, 1024, 4, 64, seed=300 + M, bias=True)
 
