@@ -235,7 +235,7 @@ def main():
         roof = {"bound": "hbm", "achieved": round(gbps_up, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(gbps_up / HBM_PEAK_GBS, 4),
                 "traffic": measured_traffic(QMV_UP_PMC),
-                "kernel": "fmxq::qmvx_kernel<4,1,1,2,4,2> (gate/up 14336x4096, M=1)",
+                "kernel": "fmxq::qmv1_kernel<4,1,4,4,2,4,1> (gate/up 14336x4096, M=1)",
                 "bytes_per_launch": by_up,
                 "timing": "HIP events over a graph of %d back-to-back launches on distinct "
                           "weight copies; per-launch = total / launches" % n_up}

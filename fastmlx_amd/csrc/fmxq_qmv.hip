@@ -68,8 +68,6 @@ __global__ __launch_bounds__(WAVES * 64) void qmvx_kernel(QmmArgs a) {
   const int64_t wpr = a.K * BITS / 32, gpr = a.K >> gshift;
   const int64_t nbase = ((int64_t)blockIdx.x * RG + rg) * RPW;
 
-  // Rows of x beyond M repeat row M-1; their outputs are never stored.
-  XChunk<BITS> xc[MM][CPL];
   bool live[CPL];
   int cc[CPL];
 #pragma unroll
@@ -78,19 +76,13 @@ __global__ __launch_bounds__(WAVES * 64) void qmvx_kernel(QmmArgs a) {
     live[i] = c < c1;
     cc[i] = live[i] ? c : c0;
   }
-#pragma unroll
-  for (int m = 0; m < MM; ++m) {
-    const uint16_t* xr = a.x + (int64_t)(m < a.M ? m : a.M - 1) * a.ldx;
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      xc[m][i].load(xr, (int64_t)cc[i] * CH);
-      if (!live[i]) xc[m][i].sum = 0.f;
-    }
-  }
 
+  XChunk<BITS> xc[MM][CPL];
   u32x4 wv0[R][CPL], wv1[R][CPL];
-  uint32_t sb0[R][CPL], sb1[R][CPL];
-  auto load = [&](u32x4 (&wv)[R][CPL], uint32_t (&sb)[R][CPL], int rb) {
+  // Scale and bias bits stay in separate registers until the arithmetic: packing
+  // them at load time would make the compiler wait for each load right away.
+  uint32_t sb0[R][CPL][2], sb1[R][CPL][2];
+  auto load = [&](u32x4 (&wv)[R][CPL], uint32_t (&sb)[R][CPL][2], int rb) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       int64_t n = nbase + rb + r;
@@ -102,12 +94,13 @@ __global__ __launch_bounds__(WAVES * 64) void qmvx_kernel(QmmArgs a) {
       for (int i = 0; i < CPL; ++i) {
         wv[r][i] = __builtin_nontemporal_load(wr + cc[i]);
         const int g = cc[i] >> chunk_gshift;
-        sb[r][i] = (uint32_t)sr[g] | ((uint32_t)br[g] << 16);
+        sb[r][i][0] = sr[g];
+        sb[r][i][1] = br[g];
       }
     }
   };
   float res[V];  // res[r * MM + m]: this lane's partial for weight row r, x row m
-  auto compute = [&](const u32x4 (&wv)[R][CPL], const uint32_t (&sb)[R][CPL], int rb) {
+  auto compute = [&](const u32x4 (&wv)[R][CPL], const uint32_t (&sb)[R][CPL][2], int rb) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       float acc[MM];
@@ -115,8 +108,8 @@ __global__ __launch_bounds__(WAVES * 64) void qmvx_kernel(QmmArgs a) {
       for (int m = 0; m < MM; ++m) acc[m] = 0.f;
 #pragma unroll
       for (int i = 0; i < CPL; ++i) {
-        const float s = bf16_lo(sb[r][i]);
-        const float bo = __builtin_fmaf(-magic_offset<BITS>(), s, bf16_hi(sb[r][i]));
+        const float s = bf16_bits_to_f32(sb[r][i][0]);
+        const float bo = __builtin_fmaf(-magic_offset<BITS>(), s, bf16_bits_to_f32(sb[r][i][1]));
         if constexpr (MM == 1) {
           const float t = __builtin_fmaf(s, chunk_dot<BITS>(wv[r][i], xc[0][i]), bo * xc[0][i].sum);
           acc[0] += live[i] ? t : 0.f;
@@ -140,7 +133,23 @@ __global__ __launch_bounds__(WAVES * 64) void qmvx_kernel(QmmArgs a) {
   auto pin = [] {
     if constexpr (MM > 1) __builtin_amdgcn_sched_barrier(0);
   };
+  // The first weight rows are requested before x is built (x is an L2 hit for
+  // all but the first waves; the weights are not).  Rows of x beyond M repeat
+  // row M-1; their outputs are never stored.
   load(wv0, sb0, 0);
+  // Keep all of the first group's weight loads ahead of x; left alone the
+  // scheduler issues the x loads first and holds back the last weight rows to
+  // reuse x's registers.
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int m = 0; m < MM; ++m) {
+    const uint16_t* xr = a.x + (int64_t)(m < a.M ? m : a.M - 1) * a.ldx;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      xc[m][i].load(xr, (int64_t)cc[i] * CH);
+      if (!live[i]) xc[m][i].sum = 0.f;
+    }
+  }
   pin();
 #pragma unroll
   for (int rb = 0; rb < RPW; rb += 2 * R) {
@@ -175,8 +184,130 @@ __global__ __launch_bounds__(WAVES * 64) void qmvx_kernel(QmmArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Decode GEMV for exactly one row of x, the shape of every decode step.
+//
+// Same work split as qmvx_kernel with one 16-byte chunk per lane (CPL) and a
+// wave walking RPW weight rows in groups of R with P groups in flight: every
+// load of the first P groups is issued before x is read, the next group's loads
+// are issued as each group's arithmetic finishes.  Scale and bias bits are
+// packed into one register per (row, chunk).
+template <int BITS, int CPL, int R, int RPW, int KS, int WAVES, int P>
+__global__ __launch_bounds__(WAVES * 64) void qmv1_kernel(QmmArgs a) {
+  constexpr int CH = 128 / BITS;
+  constexpr int RG = WAVES / KS;
+  constexpr int V = RPW;
+  constexpr int LV = __builtin_ctz(V);
+  constexpr int G = RPW / R;  // row groups per wave
+  static_assert(RPW % R == 0 && P >= 1 && P <= G, "row groups");
+  static_assert((V & (V - 1)) == 0 && V <= 64, "RPW must be a power of two <= 64");
+  __shared__ float part[KS > 1 ? RG : 1][KS][V];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rg = wave / KS, ks = wave % KS;
+  const int nch = (int)(a.K / CH);
+  const int c0 = ks * nch / KS, c1 = (ks + 1) * nch / KS;
+  const int gshift = __builtin_ctz((unsigned)a.group_size);
+  const int chunk_gshift = gshift - __builtin_ctz((unsigned)CH);
+  const int64_t wpr = a.K * BITS / 32, gpr = a.K >> gshift;
+  const int64_t nbase = ((int64_t)blockIdx.x * RG + rg) * RPW;
+
+  bool live[CPL];
+  int cc[CPL];
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = c0 + lane + 64 * i;
+    live[i] = c < c1;
+    cc[i] = live[i] ? c : c0;
+  }
+  u32x4 wv[P][R][CPL];
+  uint32_t sb[P][R][CPL];
+  auto load = [&](int slot, int rb) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      int64_t n = nbase + rb + r;
+      n = n < a.N ? n : a.N - 1;  // rows past N load row N-1; their outputs are not stored
+      const u32x4* wr = reinterpret_cast<const u32x4*>(a.w + n * wpr);
+      const uint16_t* sr = a.scales + n * gpr;
+      const uint16_t* br = a.biases + n * gpr;
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        wv[slot][r][i] = __builtin_nontemporal_load(wr + cc[i]);
+        const int g = cc[i] >> chunk_gshift;
+        sb[slot][r][i] = (uint32_t)sr[g] | ((uint32_t)br[g] << 16);
+      }
+    }
+  };
+#pragma unroll
+  for (int g = 0; g < P; ++g) load(g, g * R);
+  XChunk<BITS> xc[CPL];
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    xc[i].load(a.x, (int64_t)cc[i] * CH);
+    if (!live[i]) xc[i].sum = 0.f;
+  }
+  float res[V];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int slot = g % P;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const float s = bf16_lo(sb[slot][r][i]);
+        const float bo = __builtin_fmaf(-magic_offset<BITS>(), s, bf16_hi(sb[slot][r][i]));
+        const float t = __builtin_fmaf(s, chunk_dot<BITS>(wv[slot][r][i], xc[i]), bo * xc[i].sum);
+        acc += live[i] ? t : 0.f;
+      }
+      res[g * R + r] = acc;
+    }
+    if (g + P < G) load(slot, (g + P) * R);
+  }
+  // Lane l holds the total of row l >> (6 - LV); the first lane of each run writes.
+  const float tot = wave_sum_multi<V>(res, lane);
+  const int idx = lane >> (6 - LV);
+  const bool writer = (lane & ((64 >> LV) - 1)) == 0;
+  const int64_t n = nbase + idx;
+  if constexpr (KS > 1) {
+    if (writer) part[rg][ks][idx] = tot;
+    __syncthreads();
+    if (ks == 0 && writer) {
+      float v = 0.f;
+#pragma unroll
+      for (int k = 0; k < KS; ++k) v += part[rg][k][idx];
+      if (n < a.N) a.y[n] = finish_out(v, a.bias, n);
+    }
+  } else {
+    if (writer && n < a.N) a.y[n] = finish_out(tot, a.bias, n);
+  }
+}
+
+template <int BITS, int CPL, int R, int RPW, int KS, int WAVES, int P>
+static hipError_t launch_qmv1_cfg(const QmmArgs& a, hipStream_t stream) {
+  constexpr int64_t rows_per_block = (WAVES / KS) * RPW;
+  const unsigned blocks = (unsigned)((a.N + rows_per_block - 1) / rows_per_block);
+  qmv1_kernel<BITS, CPL, R, RPW, KS, WAVES, P><<<blocks, WAVES * 64, 0, stream>>>(a);
+  return hipGetLastError();
+}
+
+// Shapes measured on the Llama-3-8B projections (graphs of launches over
+// distinct weight copies): 4-bit rows of 65..128 chunks (K = 4096) and of
+// 257..512 chunks (K = 14336).  Returns hipErrorNotSupported for other shapes.
+static hipError_t launch_qmv1(const QmmArgs& a, hipStream_t stream) {
+  if (a.M != 1 || a.bits != 4 || a.ldx % 8 != 0) return hipErrorNotSupported;
+  const int64_t nch = a.K / 32;
+  if (nch > 64 && nch <= 128) {
+    if (a.N >= 8192) return launch_qmv1_cfg<4, 1, 4, 4, 2, 4, 1>(a, stream);
+    return launch_qmv1_cfg<4, 1, 2, 2, 2, 4, 1>(a, stream);
+  }
+  if (nch > 256 && nch <= 512) return launch_qmv1_cfg<4, 1, 4, 4, 8, 8, 1>(a, stream);
+  return hipErrorNotSupported;
+}
+
 struct QmvxShape {
   int ks, cpl, rpw, waves;
+  int r = 2;  // rows per load group (all rpw rows at once when r == rpw)
 };
 // The fewest K slices (1, 2 or 4) that keep a lane at <= 2 chunks per row (x in
 // registers grows with MM), and more rows per wave for the longest rows, where
@@ -203,16 +334,19 @@ static QmvxShape pick_qmvx_shape(int64_t nch, int64_t N, int mm) {
   return sh;
 }
 
-template <int BITS, int MM, int CPL, int RPW, int KS, int WAVES>
+template <int BITS, int MM, int CPL, int RPW, int KS, int WAVES, int R = 2>
 static hipError_t launch_qmvx_cfg(const QmmArgs& a, hipStream_t stream) {
   constexpr int64_t rows_per_block = (WAVES / KS) * RPW;
   const unsigned blocks = (unsigned)((a.N + rows_per_block - 1) / rows_per_block);
-  qmvx_kernel<BITS, MM, CPL, 2, RPW, KS, WAVES><<<blocks, WAVES * 64, 0, stream>>>(a);
+  qmvx_kernel<BITS, MM, CPL, R, RPW, KS, WAVES><<<blocks, WAVES * 64, 0, stream>>>(a);
   return hipGetLastError();
 }
 
 template <int BITS, int MM, int CPL, int KS, int WAVES = 4>
-static hipError_t launch_qmvx_rpw(const QmmArgs& a, int rpw, hipStream_t stream) {
+static hipError_t launch_qmvx_rpw(const QmmArgs& a, int rpw, hipStream_t stream, int r = 2) {
+  if constexpr (MM == 1 && CPL == 1) {
+    if (rpw == 4 && r == 4) return launch_qmvx_cfg<BITS, MM, CPL, 4, KS, WAVES, 4>(a, stream);
+  }
   if (rpw == 2) return launch_qmvx_cfg<BITS, MM, CPL, 2, KS, WAVES>(a, stream);
   if constexpr (MM <= 8) {
     if (rpw == 4) return launch_qmvx_cfg<BITS, MM, CPL, 4, KS, WAVES>(a, stream);
@@ -234,9 +368,12 @@ static bool qmvx_supported(const QmmArgs& a, int bits) {
 template <int BITS, int MM>
 static hipError_t launch_qmvx_mm(const QmmArgs& a, hipStream_t stream) {
   const QmvxShape sh = pick_qmvx_shape(a.K / (128 / BITS), a.N, MM);
-  if (sh.ks == 8) return launch_qmvx_rpw<BITS, MM, 1, 8, 8>(a, sh.rpw, stream);
+  if (sh.ks == 8) return launch_qmvx_rpw<BITS, MM, 1, 8, 8>(a, sh.rpw, stream, sh.r);
   if (sh.ks == 1) return launch_qmvx_rpw<BITS, MM, 1, 1>(a, sh.rpw, stream);
-  if (sh.ks == 2) return launch_qmvx_rpw<BITS, MM, 1, 2>(a, sh.rpw, stream);
+  if (sh.ks == 2) {
+    if (sh.waves == 8) return launch_qmvx_rpw<BITS, MM, 1, 2, 8>(a, sh.rpw, stream, sh.r);
+    return launch_qmvx_rpw<BITS, MM, 1, 2>(a, sh.rpw, stream, sh.r);
+  }
   if (sh.cpl == 1) return launch_qmvx_rpw<BITS, MM, 1, 4>(a, sh.rpw, stream);
   if constexpr (MM <= 4) {
     if (sh.cpl == 2) return launch_qmvx_rpw<BITS, MM, 2, 4>(a, sh.rpw, stream);
@@ -398,6 +535,8 @@ bool qmv_supported(const QmmArgs& a) {
 
 hipError_t launch_qmv(const QmmArgs& a, hipStream_t stream) {
   if (a.M <= 0 || a.N <= 0) return hipSuccess;
+  const hipError_t e1 = launch_qmv1(a, stream);
+  if (e1 != hipErrorNotSupported) return e1;
   if (qmvx_supported(a, a.bits))
     return a.bits == 4 ? launch_qmvx<4>(a, stream) : launch_qmvx<8>(a, stream);
   return a.bits == 4 ? launch_qmv_bits<4>(a, stream) : launch_qmv_bits<8>(a, stream);
