@@ -59,7 +59,7 @@ def stack_bytes(M, layers, bits):
     return layers * sum(qmm_bytes(M, N, K, bits, GROUP) for _, N, K in LLAMA_PROJ)
 
 
-QMV_UP_PMC = os.path.join(ROOT, "profiles", "qmvx_gate_up_14336x4096_M1_traffic.md")
+QMV_UP_PMC = os.path.join(ROOT, "profiles", "qmv1_gate_up_14336x4096_M1_traffic.md")
 
 
 def measured_traffic(path):
