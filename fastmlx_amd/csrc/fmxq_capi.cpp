@@ -398,6 +398,53 @@ extern "C" int fmxq_switch_glu(const uint16_t* x, const uint32_t* inds, const ui
   return gather_dispatch(d, sort, s);
 }
 
+namespace {
+int route_common(const void* logits, int logits_bf16, const float* bias, int64_t T, int64_t E,
+                 int top_k, int n_group, int topk_group, float scale, bool norm, uint32_t* inds,
+                 void* weights, int weights_bf16, bool group, void* stream, const char* op) {
+  if (T < 0) return fail(FMXQ_ERR_SHAPE, "%s: negative token count %lld", op, (long long)T);
+  if (E < 1 || E > fmxq::kRouteMaxExperts)
+    return fail(FMXQ_ERR_UNSUPPORTED, "%s: %lld experts (1..%lld supported)", op, (long long)E,
+                (long long)fmxq::kRouteMaxExperts);
+  if (top_k < 1 || top_k > 64 || top_k > E)
+    return fail(FMXQ_ERR_SHAPE, "%s: top_k=%d must be in 1..min(64, E=%lld)", op, top_k,
+                (long long)E);
+  if (group && (n_group < 1 || n_group > 64 || E % n_group != 0 || topk_group < 1 ||
+                topk_group > n_group))
+    return fail(FMXQ_ERR_SHAPE,
+                "%s: n_group=%d must divide E=%lld (at most 64 groups) and topk_group=%d be in "
+                "1..n_group", op, n_group, (long long)E, topk_group);
+  if (T == 0) return FMXQ_OK;
+  if (!logits || !inds || !weights) return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: null operand", op);
+  const uintptr_t la = reinterpret_cast<uintptr_t>(logits);
+  if ((logits_bf16 ? la & 1 : la & 3) || (reinterpret_cast<uintptr_t>(inds) & 3) ||
+      (reinterpret_cast<uintptr_t>(weights) & (weights_bf16 ? 1 : 3)) ||
+      (bias && (reinterpret_cast<uintptr_t>(bias) & 3)))
+    return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: operands must be aligned to their element size", op);
+  fmxq::RouteArgs a{logits, bias, inds, weights, T, E, top_k, n_group, topk_group, scale,
+                    norm, logits_bf16 != 0, weights_bf16 != 0};
+  return hip_status(fmxq::launch_route(a, group, static_cast<hipStream_t>(stream)), op);
+}
+}  // namespace
+
+extern "C" int fmxq_route_softmax_topk(const void* logits, int logits_bf16, int64_t T,
+                                       int64_t E, int top_k, bool norm_topk_prob,
+                                       uint32_t* inds, void* weights, int weights_bf16,
+                                       void* stream) {
+  return route_common(logits, logits_bf16, nullptr, T, E, top_k, 1, 1, 1.f, norm_topk_prob, inds,
+                      weights, weights_bf16, false, stream, "route_softmax_topk");
+}
+
+extern "C" int fmxq_route_group_topk(const void* gates, int gates_bf16, const float* bias,
+                                     int64_t T, int64_t E, int top_k, int n_group, int topk_group,
+                                     float routed_scaling_factor, bool norm_topk_prob,
+                                     uint32_t* inds, void* weights, int weights_bf16,
+                                     void* stream) {
+  return route_common(gates, gates_bf16, bias, T, E, top_k, n_group, topk_group,
+                      routed_scaling_factor, norm_topk_prob, inds, weights, weights_bf16, true,
+                      stream, "route_group_topk");
+}
+
 extern "C" int fmxq_moe_combine(const uint16_t* y, const uint16_t* weights,
                                 const uint16_t* shared, const uint16_t* shared_gate,
                                 uint16_t* out, int64_t T, int64_t topk, int64_t D, void* stream) {

@@ -106,6 +106,23 @@ hipError_t launch_moe_combine(const uint16_t* y, const uint16_t* w, const uint16
                               const uint16_t* sgate, uint16_t* out, int64_t T, int64_t topk,
                               int64_t D, hipStream_t stream);
 
+// MoE routers (fmxq_route.hip).  logits [T, E] (bf16 when in_bf16, else fp32);
+// bias [E] fp32 or null (group router only); inds [T, k] uint32; weights [T, k]
+// (bf16 when out_bf16, else fp32).  group selects the DeepSeek group-limited
+// sigmoid router, otherwise the softmax router.
+constexpr int64_t kRouteMaxExperts = 1024;
+struct RouteArgs {
+  const void* logits;
+  const float* bias;
+  uint32_t* inds;
+  void* weights;
+  int64_t T, E;
+  int k, n_group, topk_group;
+  float scale;
+  bool norm, in_bf16, out_bf16;
+};
+hipError_t launch_route(const RouteArgs& a, bool group, hipStream_t stream);
+
 // Grouped MFMA gather for expert-sorted batches (int4 group_size >= 64, int8 >= 32).
 constexpr int64_t kGroupedMinSlots = 32;
 bool gather_mfma_supported(const GatherArgs& a);

@@ -123,6 +123,45 @@ def moe_combine(y, weights, shared=None, shared_gate=None, out=None):
     return out
 
 
+def _route_io(logits, T, k, weights_dtype):
+    if logits.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"router logits must be bfloat16 or float32, got {logits.dtype}")
+    if weights_dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"router weights must be bfloat16 or float32, got {weights_dtype}")
+    inds = torch.empty(T, k, dtype=torch.int32, device=logits.device)
+    weights = torch.empty(T, k, dtype=weights_dtype, device=logits.device)
+    return inds, weights
+
+
+def route_softmax_topk(logits, top_k, norm_topk_prob=True, weights_dtype=torch.bfloat16):
+    """Softmax router (qwen3next_forward.go:513-518): logits [T, E] -> (inds [T, k] int32
+    holding uint32 ids, weights [T, k]), largest gate first."""
+    T, E = logits.shape
+    inds, weights = _route_io(logits, T, top_k, weights_dtype)
+    ptr = _dev(logits, "logits", (torch.bfloat16, torch.float32))
+    check(load().fmxq_route_softmax_topk(ptr, int(logits.dtype == torch.bfloat16), T, E, top_k,
+                                         bool(norm_topk_prob), _dev(inds, "inds", _U32_LIKE),
+                                         weights.data_ptr(),
+                                         int(weights_dtype == torch.bfloat16), _stream(logits)))
+    return inds, weights
+
+
+def route_group_topk(gates, bias, top_k, n_group, topk_group, routed_scaling_factor=1.0,
+                     norm_topk_prob=True, weights_dtype=torch.float32):
+    """DeepSeek-V3 group-limited router (deepseekv3_forward.go:452-491): gates [T, E],
+    bias [E] float32 or None -> (inds [T, k] int32 holding uint32 ids, weights [T, k])."""
+    T, E = gates.shape
+    inds, weights = _route_io(gates, T, top_k, weights_dtype)
+    bptr = None if bias is None else _dev(bias, "bias", (torch.float32,))
+    ptr = _dev(gates, "gates", (torch.bfloat16, torch.float32))
+    check(load().fmxq_route_group_topk(ptr, int(gates.dtype == torch.bfloat16), bptr, T, E, top_k,
+                                       n_group, topk_group, float(routed_scaling_factor),
+                                       bool(norm_topk_prob), _dev(inds, "inds", _U32_LIKE),
+                                       weights.data_ptr(), int(weights_dtype == torch.bfloat16),
+                                       _stream(gates)))
+    return inds, weights
+
+
 def device_error(device=None) -> None:
     """Raise FmxqError(FMXQ_ERR_INDEX) if a gather met an out-of-range index."""
     dev = torch.device("cuda", torch.cuda.current_device()) if device is None else device

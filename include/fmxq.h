@@ -133,6 +133,31 @@ int fmxq_moe_combine(const uint16_t* y, const uint16_t* weights, const uint16_t*
                      const uint16_t* shared_gate, uint16_t* out, int64_t T, int64_t top_k,
                      int64_t D, void* stream);
 
+/* Softmax MoE router of qwen3NextMoE (compute/models/qwen3next_forward.go:513-518):
+ *     gates = softmax(logits[t]); inds[t] = the top_k experts by gate (equal gates
+ *     to the lower index); weights[t, j] = gates[inds[t, j]], divided by their sum
+ *     when norm_topk_prob.
+ * logits [T, E] (bf16 when logits_bf16, else fp32), E <= 1024, top_k <= min(E, 64);
+ * inds [T, top_k] uint32 and weights [T, top_k] (bf16 when weights_bf16, else fp32),
+ * both in selection order (largest gate first).  fp32 arithmetic throughout. */
+int fmxq_route_softmax_topk(const void* logits, int logits_bf16, int64_t T, int64_t E,
+                            int top_k, bool norm_topk_prob, uint32_t* inds, void* weights,
+                            int weights_bf16, void* stream);
+
+/* DeepSeek-V3 group-limited router: routeExperts (compute/models/deepseekv3_forward.go:
+ * 452-491), restated on the CPU as GroupExpertSelect (deepseekv3.go:305-384).
+ *     o = sigmoid(gates[t]); b = o + bias; with n_group > 1 the groups outside the
+ *     topk_group best (a group scores the sum of its two best b) get b = 0; inds[t] =
+ *     the top_k experts by b (ties to the lower index); weights = o[inds], divided by
+ *     their sum when norm_topk_prob and top_k > 1, times routed_scaling_factor.
+ * gates [T, E] (bf16 when gates_bf16, else fp32); bias [E] fp32 or NULL; n_group
+ * divides E (<= 64 groups), 1 <= topk_group <= n_group; outputs as for the softmax
+ * router. */
+int fmxq_route_group_topk(const void* gates, int gates_bf16, const float* bias, int64_t T,
+                          int64_t E, int top_k, int n_group, int topk_group,
+                          float routed_scaling_factor, bool norm_topk_prob, uint32_t* inds,
+                          void* weights, int weights_bf16, void* stream);
+
 /* Synchronizes `stream`, then reports (and clears) the device-side error flag
  * that gather kernels raise on an out-of-range index: returns FMXQ_OK or
  * FMXQ_ERR_INDEX. */

@@ -53,6 +53,9 @@ def lib():
         L.oracle_bf16_to_f32.argtypes = [ctypes.c_uint16]
         L.oracle_bf16_to_f32.restype = ctypes.c_float
         L.oracle_num_threads.restype = _int
+        L.oracle_route_group_topk.argtypes = [_p, _p, _i64, _i64, _int, _int, _int,
+                                              ctypes.c_double, _int, _p, _p]
+        L.oracle_route_softmax_topk.argtypes = [_p, _i64, _i64, _int, _int, _p, _p]
         _lib = L
     return _lib
 
@@ -157,3 +160,30 @@ def qmm_cpu_fast(x, w, scales, biases, group_size=64, bits=4):
     _check(lib().oracle_qmm_cpu_fast(_ptr(x), _ptr(w), _ptr(scales), _ptr(biases), _ptr(y),
                                      M, N, K, group_size, bits), "qmm_cpu_fast")
     return y
+
+
+def route_group_topk(gates, bias, top_k, n_group, topk_group, scale=1.0, norm=True):
+    """GroupExpertSelect (compute/models/deepseekv3.go:305-384) per row of gates [T, E]:
+    returns (inds [T, k] int32, scores [T, k] float64) in selection order."""
+    g = np.ascontiguousarray(np.atleast_2d(gates), dtype=np.float32)
+    T, E = g.shape
+    k = min(top_k, E)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    inds = np.zeros((T, k), np.int32)
+    sc = np.zeros((T, k), np.float64)
+    _check(lib().oracle_route_group_topk(_ptr(g), None if b is None else _ptr(b), T, E, k,
+                                         n_group, topk_group, float(scale), int(bool(norm)),
+                                         _ptr(inds), _ptr(sc)), "route_group_topk")
+    return inds, sc
+
+
+def route_softmax_topk(logits, top_k, norm=True):
+    """qwen3NextMoE's router (compute/models/qwen3next_forward.go:513-518) per row of
+    logits [T, E]: returns (inds [T, k] int32, weights [T, k] float64)."""
+    x = np.ascontiguousarray(np.atleast_2d(logits), dtype=np.float32)
+    T, E = x.shape
+    inds = np.zeros((T, top_k), np.int32)
+    w = np.zeros((T, top_k), np.float64)
+    _check(lib().oracle_route_softmax_topk(_ptr(x), T, E, top_k, int(bool(norm)), _ptr(inds),
+                                           _ptr(w)), "route_softmax_topk")
+    return inds, w

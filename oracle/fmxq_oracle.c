@@ -302,3 +302,96 @@ int oracle_num_threads(void) {
   return 1;
 #endif
 }
+
+
+/* ---- MoE routers ------------------------------------------------------- */
+
+/* Indices 0..n-1 ordered by val descending; equal values keep index order (the
+ * reference's sort.SliceStable on an ascending index list). */
+static void stable_desc_order(const double *val, int64_t n, int64_t *order) {
+  for (int64_t i = 0; i < n; ++i) order[i] = i;
+  for (int64_t i = 1; i < n; ++i) { /* insertion sort: stable */
+    const int64_t cur = order[i];
+    int64_t j = i - 1;
+    while (j >= 0 && val[order[j]] < val[cur]) {
+      order[j + 1] = order[j];
+      --j;
+    }
+    order[j + 1] = cur;
+  }
+}
+
+/* GroupExpertSelect, compute/models/deepseekv3.go:305-384. */
+int oracle_route_group_topk(const float *gates, const float *bias, int64_t T, int64_t E,
+                            int top_k, int n_group, int topk_group, double scale, int norm,
+                            int32_t *inds, double *scores) {
+  if (T < 0 || E < 1 || top_k < 1 || n_group < 1 || E % n_group) return -1;
+  if (top_k > E) top_k = (int)E; /* :354-356 */
+  double *orig = malloc(sizeof(double) * E), *biased = malloc(sizeof(double) * E);
+  double *gscore = malloc(sizeof(double) * n_group);
+  int64_t *order = malloc(sizeof(int64_t) * E), *gorder = malloc(sizeof(int64_t) * n_group);
+  char *keep = malloc(n_group);
+  for (int64_t t = 0; t < T; ++t) {
+    const float *g = gates + t * E;
+    for (int64_t i = 0; i < E; ++i) { /* :307-316 */
+      orig[i] = 1.0 / (1.0 + exp(-(double)g[i]));
+      biased[i] = orig[i] + (bias ? (double)bias[i] : 0.0);
+    }
+    if (n_group > 1) { /* :318-346 */
+      const int64_t per = E / n_group;
+      for (int grp = 0; grp < n_group; ++grp) {
+        /* the group's two best biased scores (one when the group has one expert) */
+        double t1 = -INFINITY, t2 = -INFINITY;
+        for (int64_t j = grp * per; j < (grp + 1) * per; ++j) {
+          const double v = biased[j];
+          if (v > t1) { t2 = t1; t1 = v; } else if (v > t2) { t2 = v; }
+        }
+        gscore[grp] = per > 1 ? t1 + t2 : t1;
+      }
+      stable_desc_order(gscore, n_group, gorder);
+      for (int grp = 0; grp < n_group; ++grp) keep[grp] = 0;
+      for (int i = 0; i < topk_group && i < n_group; ++i) keep[gorder[i]] = 1;
+      for (int grp = 0; grp < n_group; ++grp)
+        if (!keep[grp])
+          for (int64_t j = grp * per; j < (grp + 1) * per; ++j) biased[j] = 0.0;
+    }
+    stable_desc_order(biased, E, order); /* :349-353 */
+    double denom = 0.0;
+    for (int j = 0; j < top_k; ++j) {
+      inds[t * top_k + j] = (int32_t)order[j];
+      scores[t * top_k + j] = orig[order[j]]; /* :359-362 */
+      denom += scores[t * top_k + j];
+    }
+    if (top_k > 1 && norm && denom != 0.0) /* :363-372 */
+      for (int j = 0; j < top_k; ++j) scores[t * top_k + j] /= denom;
+    for (int j = 0; j < top_k; ++j) scores[t * top_k + j] *= scale; /* :373-375 */
+  }
+  free(orig); free(biased); free(gscore); free(order); free(gorder); free(keep);
+  return 0;
+}
+
+/* qwen3NextMoE's router, compute/models/qwen3next_forward.go:513-518. */
+int oracle_route_softmax_topk(const float *logits, int64_t T, int64_t E, int top_k, int norm,
+                              int32_t *inds, double *weights) {
+  if (T < 0 || E < 1 || top_k < 1 || top_k > E) return -1;
+  double *p = malloc(sizeof(double) * E);
+  int64_t *order = malloc(sizeof(int64_t) * E);
+  for (int64_t t = 0; t < T; ++t) {
+    const float *x = logits + t * E;
+    double m = -INFINITY, s = 0.0;
+    for (int64_t i = 0; i < E; ++i) m = x[i] > m ? x[i] : m;
+    for (int64_t i = 0; i < E; ++i) { p[i] = exp((double)x[i] - m); s += p[i]; }
+    for (int64_t i = 0; i < E; ++i) p[i] /= s; /* softmax, :514 */
+    stable_desc_order(p, E, order);              /* argpartition top-k, :515 */
+    double sel = 0.0;
+    for (int j = 0; j < top_k; ++j) {
+      inds[t * top_k + j] = (int32_t)order[j];
+      weights[t * top_k + j] = p[order[j]]; /* takeAlongAxis, :516 */
+      sel += p[order[j]];
+    }
+    if (norm) /* :517-518 */
+      for (int j = 0; j < top_k; ++j) weights[t * top_k + j] /= sel;
+  }
+  free(p); free(order);
+  return 0;
+}

@@ -94,6 +94,20 @@ int oracle_qmm_cpu_fast(const uint16_t *x, const uint32_t *w,
 
 int oracle_num_threads(void);
 
+/* MoE routers (double arithmetic; top-k by a stable descending sort, so equal
+ * scores go to the lower index).
+ * oracle_route_group_topk restates GroupExpertSelect
+ * (compute/models/deepseekv3.go:305-384) row by row: gates [T, E] fp32, bias [E]
+ * fp32 or NULL, inds [T, k], scores [T, k] in selection order.
+ * oracle_route_softmax_topk restates the router of qwen3NextMoE
+ * (compute/models/qwen3next_forward.go:513-518): softmax over the row, the top_k
+ * gates, renormalized over the selection when norm. */
+int oracle_route_group_topk(const float *gates, const float *bias, int64_t T, int64_t E,
+                            int top_k, int n_group, int topk_group, double scale, int norm,
+                            int32_t *inds, double *scores);
+int oracle_route_softmax_topk(const float *logits, int64_t T, int64_t E, int top_k, int norm,
+                              int32_t *inds, double *weights);
+
 #ifdef __cplusplus
 }
 #endif

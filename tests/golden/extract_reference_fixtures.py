@@ -1,8 +1,11 @@
 """Copy the reference's own fixture rows for this path into tests/golden/.
 
 Run here (where /root/reference exists); the GPU box only reads the committed
-JSON.  Source: quant/testdata/oq.json "tensor_bytes", the fixture of
-TestTensorQuantizedBytesParity (quant/oq_test.go:158-165).
+JSON.  Sources:
+  - quant/testdata/oq.json "tensor_bytes", the fixture of
+    TestTensorQuantizedBytesParity (quant/oq_test.go:158-165);
+  - compute/testdata/deepseek_args.json "routing", the fixture of
+    TestDeepseekV3GroupExpertSelectParity (compute/models/deepseekv3_test.go:130-163).
 """
 import json
 import os
@@ -18,6 +21,12 @@ def main() -> int:
         data = json.load(f)
     out = {"source": "quant/testdata/oq.json#tensor_bytes", "tensor_bytes": data["tensor_bytes"]}
     with open(os.path.join(HERE, "oq_tensor_bytes.json"), "w") as f:
+        json.dump(out, f, indent=1)
+        f.write("\n")
+    with open(os.path.join(REF, "compute", "testdata", "deepseek_args.json")) as f:
+        routing = json.load(f)["routing"]
+    out = {"source": "compute/testdata/deepseek_args.json#routing", "routing": routing}
+    with open(os.path.join(HERE, "deepseek_routing.json"), "w") as f:
         json.dump(out, f, indent=1)
         f.write("\n")
     return 0

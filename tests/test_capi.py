@@ -110,6 +110,31 @@ def test_switch_glu_and_combine_validation():
     assert _status(mc(None, None, None, None, None, 2, 2, 8, None)) == "FMXQ_ERR_INVALID_ARGUMENT"
 
 
+def test_router_validation():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x1000)
+
+    def soft(T=4, E=64, k=4, logits=fake, inds=fake, w=fake, lbf=1, wbf=1):
+        return lib.fmxq_route_softmax_topk(logits, lbf, T, E, k, True, inds, w, wbf, None)
+
+    def grp(T=4, E=64, k=4, ng=8, tg=4, bias=None, logits=fake, inds=fake, w=fake):
+        return lib.fmxq_route_group_topk(logits, 0, bias, T, E, k, ng, tg, 1.0, True, inds, w, 0,
+                                         None)
+
+    assert _status(soft(E=2048)) == "FMXQ_ERR_UNSUPPORTED"   # more experts than a wave holds
+    assert _status(soft(k=0)) == "FMXQ_ERR_SHAPE"
+    assert _status(soft(E=8, k=9)) == "FMXQ_ERR_SHAPE"
+    assert _status(soft(T=-1)) == "FMXQ_ERR_SHAPE"
+    assert _status(soft(logits=None)) == "FMXQ_ERR_INVALID_ARGUMENT"
+    assert _status(soft(logits=ctypes.c_void_p(0x1001))) == "FMXQ_ERR_INVALID_ARGUMENT"
+    assert soft(T=0) == 0
+    assert _status(grp(ng=7)) == "FMXQ_ERR_SHAPE"            # groups must divide E
+    assert _status(grp(tg=9)) == "FMXQ_ERR_SHAPE"
+    assert _status(grp(tg=0)) == "FMXQ_ERR_SHAPE"
+    assert _status(grp(bias=ctypes.c_void_p(0x1002))) == "FMXQ_ERR_INVALID_ARGUMENT"
+    assert grp(T=0) == 0
+
+
 def test_check_raises_with_message():
     rc = _qmm(bits=3)
     with pytest.raises(FmxqError) as ei:

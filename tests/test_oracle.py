@@ -260,3 +260,77 @@ def test_tensor_bytes_formula_matches_reference_fixture():
     assert rows
     for r in rows:
         assert quantized_tensor_bytes(r["shape"], r["bits"], r["gs"], r["mode"]) == r["bytes"], r
+
+
+# ---- MoE routers -------------------------------------------------------------
+
+def _routing_fixture():
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                        "deepseek_routing.json")
+    with open(path) as f:
+        return json.load(f)["routing"]
+
+
+@pytest.mark.parametrize("case", _routing_fixture(), ids=lambda c: c["label"])
+def test_route_group_oracle_matches_reference_fixture(oracle, case):
+    """The reference's own vectors for GroupExpertSelect, compared the way
+    TestDeepseekV3GroupExpertSelectParity does (compute/models/deepseekv3_test.go:
+    130-163): the expert -> weight map at 1e-5 relative."""
+    inds, sc = oracle.route_group_topk(case["gates"], case["bias"], case["top_k"],
+                                       case["n_group"], case["topk_group"],
+                                       case["routed_scaling_factor"], case["norm_topk_prob"])
+    got = dict(zip(inds[0].tolist(), sc[0].tolist()))
+    want = dict(zip(case["inds"], case["scores"]))
+    assert set(got) == set(want)
+    for e, w in want.items():
+        assert abs(got[e] - w) <= 1e-5 * abs(w)
+
+
+def test_route_group_oracle_invariants(oracle):
+    rng = np.random.default_rng(71)
+    T, E, k = 40, 64, 6
+    gates = rng.standard_normal((T, E)).astype(np.float32)
+    bias = (rng.standard_normal(E) * 0.05).astype(np.float32)
+    # keeping every group is the same as one group
+    a = oracle.route_group_topk(gates, bias, k, 8, 8, 1.7, True)
+    b = oracle.route_group_topk(gates, bias, k, 1, 1, 1.7, True)
+    assert np.array_equal(a[0], b[0]) and np.allclose(a[1], b[1])
+    # weights are the unbiased sigmoids of the picks, renormalized and scaled
+    sig = 1.0 / (1.0 + np.exp(-gates.astype(np.float64)))
+    inds, sc = oracle.route_group_topk(gates, bias, k, 8, 3, 2.5, True)
+    picked = np.take_along_axis(sig, inds.astype(np.int64), axis=1)
+    assert np.allclose(sc, 2.5 * picked / picked.sum(axis=1, keepdims=True))
+    # without bias every score is positive, so every pick lies in a kept group:
+    # at most topk_group distinct groups
+    inds, _ = oracle.route_group_topk(gates, None, k, 8, 3, 1.0, False)
+    assert all(len(set((r // 8).tolist())) <= 3 for r in inds)
+    # the kept groups are the ones with the best two-expert sums
+    g2 = np.sort(sig.reshape(T, 8, 8), axis=2)[:, :, -2:].sum(axis=2)
+    best = np.argsort(-g2, axis=1, kind="stable")[:, :3]
+    for t in range(T):
+        assert set((inds[t] // 8).tolist()) <= set(best[t].tolist())
+    # picks come out in descending biased score
+    ninds, _ = oracle.route_group_topk(gates, bias, E, 1, 1, 1.0, False)
+    biased = sig + bias
+    assert np.all(np.diff(np.take_along_axis(biased, ninds.astype(np.int64), 1), axis=1) <= 0)
+
+
+def test_route_softmax_oracle_closed_forms(oracle):
+    rng = np.random.default_rng(72)
+    T, E, k = 30, 128, 10
+    x = rng.standard_normal((T, E)).astype(np.float32)
+    inds, w = oracle.route_softmax_topk(x, k, norm=True)
+    # the renormalized top-k of a softmax is the softmax of the top-k logits
+    sel = np.take_along_axis(x.astype(np.float64), inds.astype(np.int64), axis=1)
+    ref = np.exp(sel - sel.max(axis=1, keepdims=True))
+    assert np.allclose(w, ref / ref.sum(axis=1, keepdims=True), rtol=1e-12)
+    # the picks are the k largest logits, in descending order
+    assert np.array_equal(inds, np.argsort(-x, axis=1, kind="stable")[:, :k])
+    # with every expert and no renormalization the weights are the softmax
+    _, full = oracle.route_softmax_topk(x, E, norm=False)
+    assert np.allclose(full.sum(axis=1), 1.0)
+    # equal gates go to the lower index
+    tied = np.zeros((1, 16), np.float32)
+    tied[0, [3, 9, 12]] = 2.0
+    ti, _ = oracle.route_softmax_topk(tied, 4, norm=True)
+    assert ti[0].tolist() == [3, 9, 12, 0]
