@@ -81,6 +81,9 @@ FMX_SYMBOLS = {
     "fmx_moe_combine": (_int, [_Ap] + [_A] * 4 + [_S]),
     "fmx_dequantize_rows": (_int, [_Ap] + [_A] * 4 + [_int, _int, _S]),
     "fmx_switch_glu": (_int, [_Ap] + [_A] * 11 + [_int, _int, _S]),
+    "fmx_route_softmax_topk": (_int, [_Ap, _Ap, _A, _int, _bool, _S]),
+    "fmx_route_group_topk": (_int, [_Ap, _Ap, _A, _A, _int, _int, _int, ctypes.c_float, _bool,
+                                    _S]),
 }
 
 STATUS = {

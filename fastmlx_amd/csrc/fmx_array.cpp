@@ -758,6 +758,63 @@ int fmx_moe_combine(fmx_array* res, const fmx_array y, const fmx_array weights,
   return commit(res, r, rc);
 }
 
+namespace {
+int route_handles(fmx_array* inds, fmx_array* weights, const fmx_array logits,
+                  const fmx_array bias, int top_k, int n_group, int topk_group, float scale,
+                  bool norm, bool group, const fmx_stream s, const char* op) {
+  if (!inds || !weights) return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: null result", op);
+  Array* X;
+  if (int rc = need(logits, op, "logits", &X)) return rc;
+  if (X->dtype != FMX_BFLOAT16 && X->dtype != FMX_FLOAT32)
+    return fail(FMXQ_ERR_UNSUPPORTED, "%s: logits must be bfloat16 or float32", op);
+  if (X->shape.empty()) return fail(FMXQ_ERR_SHAPE, "%s: logits must be [..., E]", op);
+  const int64_t E = X->shape.back();
+  Array* Bi = group ? arr(bias) : nullptr;
+  if (Bi) {
+    if (int rc = need_dtype(Bi, FMX_FLOAT32, op, "bias")) return rc;
+    if (int rc = need_shape(Bi, {E}, op, "bias")) return rc;
+  }
+  std::vector<int64_t> oshape(X->shape.begin(), X->shape.end() - 1);
+  const int64_t T = prod(oshape);
+  oshape.push_back(top_k);
+  Launch L;
+  if (int rc = begin(L, s, {X, Bi})) return rc;
+  Array *ri = nullptr, *rw = nullptr;
+  if (int rc = new_result(L, oshape, FMX_UINT32, &ri)) return rc;
+  if (int rc = new_result(L, oshape, X->dtype, &rw)) {
+    commit(inds, ri, rc);
+    return rc;
+  }
+  const int bf = X->dtype == FMX_BFLOAT16;
+  int rc = group ? fmxq_route_group_topk(X->data, bf, Bi ? static_cast<const float*>(Bi->data)
+                                                           : nullptr,
+                                         T, E, top_k, n_group, topk_group, scale, norm,
+                                         static_cast<uint32_t*>(ri->data), rw->data, bf, L.s)
+                 : fmxq_route_softmax_topk(X->data, bf, T, E, top_k, norm,
+                                           static_cast<uint32_t*>(ri->data), rw->data, bf, L.s);
+  finish(L);
+  if (rc) {
+    commit(inds, ri, rc);
+    return commit(weights, rw, rc);
+  }
+  commit(inds, ri, 0);
+  return commit(weights, rw, 0);
+}
+}  // namespace
+
+int fmx_route_softmax_topk(fmx_array* inds, fmx_array* weights, const fmx_array logits,
+                           int top_k, bool norm_topk_prob, const fmx_stream s) {
+  return route_handles(inds, weights, logits, fmx_array{nullptr}, top_k, 1, 1, 1.f,
+                       norm_topk_prob, false, s, "route_softmax_topk");
+}
+
+int fmx_route_group_topk(fmx_array* inds, fmx_array* weights, const fmx_array gates,
+                         const fmx_array bias, int top_k, int n_group, int topk_group,
+                         float routed_scaling_factor, bool norm_topk_prob, const fmx_stream s) {
+  return route_handles(inds, weights, gates, bias, top_k, n_group, topk_group,
+                       routed_scaling_factor, norm_topk_prob, true, s, "route_group_topk");
+}
+
 int fmx_gather_qmm(fmx_array* res, const fmx_array x, const fmx_array w,
                    const fmx_array scales, const fmx_array biases, const fmx_array lhs_indices,
                    const fmx_array rhs_indices, bool transpose, int group_size, int bits,

@@ -357,6 +357,27 @@ def switch_glu(x: Array, inds: Array, gate, up, down, group_size: int, bits: int
     return _op(load().fmx_switch_glu, *args, int(group_size), int(bits), _sh(s))
 
 
+def _op2(fn, *args):
+    a, b = FmxArray(None), FmxArray(None)
+    _check(fn(ctypes.byref(a), ctypes.byref(b), *args))
+    return Array(a), Array(b)
+
+
+def route_softmax_topk(logits: Array, top_k: int, norm_topk_prob: bool,
+                       s: Optional[Stream] = None):
+    """qwen3NextMoE's router (qwen3next_forward.go:513-518): (inds, scores)."""
+    return _op2(load().fmx_route_softmax_topk, _ah(logits), int(top_k), bool(norm_topk_prob),
+                _sh(s))
+
+
+def route_group_topk(gates: Array, bias: Optional[Array], top_k: int, n_group: int,
+                     topk_group: int, routed_scaling_factor: float, norm_topk_prob: bool,
+                     s: Optional[Stream] = None):
+    """DeepSeek-V3 routeExperts (deepseekv3_forward.go:452-491): (inds, weights)."""
+    return _op2(load().fmx_route_group_topk, _ah(gates), _ah(bias), int(top_k), int(n_group),
+                int(topk_group), float(routed_scaling_factor), bool(norm_topk_prob), _sh(s))
+
+
 def moe_combine(y: Array, weights: Array, shared: Optional[Array] = None,
                 shared_gate: Optional[Array] = None, s: Optional[Stream] = None) -> Array:
     """sum over top-k of y * weights (+ shared, sigmoid-gated when shared_gate)."""

@@ -20,7 +20,7 @@ from __future__ import annotations
 
 import json
 from dataclasses import dataclass
-from typing import Dict, Optional
+from typing import Dict, Optional, Tuple
 
 from . import mlxgo
 from .mlxgo import Array, MLXError, Stream
@@ -187,6 +187,25 @@ class FB:
             return None
         return self._run(mlxgo.switch_glu, x, inds, gate.triple(), up.triple(), down.triple(),
                          gate.group_size, gate.bits, self.s)
+
+    # qwen3next_forward.go:513-518: softmax over the router logits, the top-k
+    # experts and their gates, renormalized when norm_topk_prob.
+    def route_softmax(self, gates_logits: Array, top_k: int,
+                      norm_topk_prob: bool) -> Tuple[Optional[Array], Optional[Array]]:
+        if self.err is not None:
+            return None, None
+        out = self._run(mlxgo.route_softmax_topk, gates_logits, top_k, norm_topk_prob, self.s)
+        return (None, None) if out is None else out
+
+    # deepseekv3_forward.go:452-491 (routeExperts): group-limited sigmoid routing.
+    def route_experts(self, gates: Array, bias: Optional[Array], top_k: int, n_group: int,
+                      topk_group: int, routed_scaling_factor: float,
+                      norm_topk_prob: bool) -> Tuple[Optional[Array], Optional[Array]]:
+        if self.err is not None:
+            return None, None
+        out = self._run(mlxgo.route_group_topk, gates, bias, top_k, n_group, topk_group,
+                        routed_scaling_factor, norm_topk_prob, self.s)
+        return (None, None) if out is None else out
 
     # qwen3next_forward.go:520-523 / deepseekv3_forward.go:434-440
     def moe_combine(self, y: Array, scores: Array, shared: Optional[Array] = None,

@@ -142,6 +142,19 @@ int fmx_switch_glu(fmx_array* res, const fmx_array x, const fmx_array inds,
                    const fmx_array w_up, const fmx_array s_up, const fmx_array b_up,
                    const fmx_array w_down, const fmx_array s_down, const fmx_array b_down,
                    int group_size, int bits, const fmx_stream s);
+/* MoE routers over a row of expert logits (bf16 or float32 [..., E], E <= 1024);
+ * results inds [..., top_k] uint32 and weights [..., top_k] in the logits' dtype,
+ * largest first, equal scores to the lower expert id.
+ * fmx_route_softmax_topk: qwen3NextMoE's softmax top-k with optional
+ * renormalization (compute/models/qwen3next_forward.go:513-518).
+ * fmx_route_group_topk: DeepSeek-V3's group-limited sigmoid router routeExperts
+ * (compute/models/deepseekv3_forward.go:452-491); bias float32 [E] or empty.
+ * On failure neither result is touched. */
+int fmx_route_softmax_topk(fmx_array* inds, fmx_array* weights, const fmx_array logits,
+                           int top_k, bool norm_topk_prob, const fmx_stream s);
+int fmx_route_group_topk(fmx_array* inds, fmx_array* weights, const fmx_array gates,
+                         const fmx_array bias, int top_k, int n_group, int topk_group,
+                         float routed_scaling_factor, bool norm_topk_prob, const fmx_stream s);
 
 #ifdef __cplusplus
 }

@@ -273,3 +273,62 @@ def test_buffer_cache_and_cross_stream(fx, oracle):
     # replacing a live result handle in place (mlx-c set semantics) keeps it valid
     y2.free()
     z.free()
+
+
+def test_fb_moe_layer_router_switch_combine(fx, oracle):
+    """A Qwen3-Next MoE block through the handle layer (qwen3next_forward.go:510-525,
+    routed part): router logits from qlinear, softmax top-k router, switchGLU over
+    the picked experts, weighted combine; against the oracle on the same bytes."""
+    from fastmlx_amd.models import FB, QLinear
+
+    rng = np.random.default_rng(77)
+    E, D, I, k, L = 16, 128, 64, 4, 6
+    router = make_quant(rng, (E,), D)
+    gate, up = make_quant(rng, (E, I), D), make_quant(rng, (E, I), D)
+    down = make_quant(rng, (E, D), I)
+    x = make_x(rng, 1, L, D)
+    ql = lambda t: QLinear(*quant_arrays(fx, t), group_size=64, bits=4)
+    announce(f"fmx MoE block L={L} E={E} k={k}")
+    b = FB()
+    logits = b.qlinear(BF(fx, x), ql(router))
+    inds, scores = b.route_softmax(logits, k, True)
+    y = b.switch_glu_for(BF(fx, x), ql(gate), ql(up), ql(down), inds)
+    out = b.moe_combine(y, scores)
+    assert b.err is None
+    assert inds.shape() == [1, L, k] and scores.shape() == [1, L, k] and out.shape() == [1, L, D]
+    lg = f32(oracle, logits.to_numpy().reshape(L, E))
+    oi, ow = oracle.route_softmax_topk(lg, k, norm=True)
+    assert np.array_equal(inds.to_numpy().view(np.uint32).reshape(L, k), oi)
+    got_w = f32(oracle, scores.to_numpy().reshape(L, k))
+    assert np.allclose(got_w, ow, rtol=2 ** -8, atol=1e-6)
+    ys = oracle.switch_glu(x.reshape(L, D), oi, gate, up, down)
+    want = (f32(oracle, ys) * got_w[:, :, None]).sum(axis=1)
+    assert rel_err(f32(oracle, out.to_numpy().reshape(L, D)), want) <= TOL
+
+
+def test_fb_route_experts_reference_vectors(fx):
+    """DeepSeek routeExperts through the handle layer on the reference's routing
+    vectors (compute/models/deepseekv3_test.go:130-163)."""
+    import json
+    import os
+
+    from fastmlx_amd.models import FB
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                        "deepseek_routing.json")
+    with open(path) as f:
+        cases = json.load(f)["routing"]
+    b = FB()
+    for c in cases:
+        announce(f"fmx route_experts {c['label']}")
+        g = A(fx, np.array([[c["gates"]]], np.float32))
+        bias = A(fx, np.array(c["bias"], np.float32))
+        inds, w = b.route_experts(g, bias, c["top_k"], c["n_group"], c["topk_group"],
+                                  c["routed_scaling_factor"], c["norm_topk_prob"])
+        assert b.err is None and inds.shape() == [1, 1, c["top_k"]]
+        got = dict(zip(inds.to_numpy().view(np.uint32).ravel().tolist(),
+                       w.to_numpy().view(np.float32).ravel().tolist()))
+        want = dict(zip(c["inds"], c["scores"]))
+        assert set(got) == set(want)
+        for e, v in want.items():
+            assert abs(got[e] - v) <= 1e-5 * abs(v)
