@@ -192,6 +192,11 @@ int qmm_common(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
     return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: x and w must be 16-byte aligned", op);
   fmxq::QmmArgs a{x, w, scales, biases, bias, y, M, N, K, K, N, group_size, bits};
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // M <= 4: dot2 GEMV.  5 <= M <= 32: qmvs, except that narrow outputs (N < 2048)
+  // at M <= 8 stay on the dot2 GEMV, which is quicker there.
+  const bool skinny = M > fmxq::kQmvMaxM && M <= fmxq::kSkinnyMaxM && fmxq::qmvs_supported(a) &&
+                      !(M <= 8 && N < 2048 && fmxq::qmv_supported(a));
+  if (skinny) return hip_status(fmxq::launch_qmvs(a, s), op);
   if (fmxq::qmv_supported(a)) return hip_status(fmxq::launch_qmv(a, s), op);
   if (M <= fmxq::kSkinnyMaxM && fmxq::qmv_mfma_supported(a))
     return hip_status(fmxq::launch_qmv_mfma(a, s), op);

@@ -73,8 +73,12 @@ constexpr int kQmvMaxM = 4;
 bool qmv_supported(const QmmArgs& a);
 hipError_t launch_qmv(const QmmArgs& a, hipStream_t stream);
 
-// MFMA GEMV for 5 <= M <= 32 (int4 with group_size >= 64, int8 with >= 32).
+// MFMA GEMV for 5 <= M <= 32 (fmxq_skinny.hip): qmvs for int4 group 64 with K a
+// multiple of 256 and aligned operands, qmv_mfma for the other int4 (group_size
+// >= 64) and int8 (group_size >= 32) cases.
 constexpr int kSkinnyMaxM = 32;
+bool qmvs_supported(const QmmArgs& a);
+hipError_t launch_qmvs(const QmmArgs& a, hipStream_t stream);
 bool qmv_mfma_supported(const QmmArgs& a);
 hipError_t launch_qmv_mfma(const QmmArgs& a, hipStream_t stream);
 

@@ -147,6 +147,25 @@ def test_skinny_mfma_rows_and_groups(gpu, oracle, M, bits, group, K):
     _qmm_case(gpu, oracle, M, 333, K, bits, group, seed=900 + M * 3 + bits + group)
 
 
+@pytest.mark.parametrize("M", [5, 8, 9, 16, 17, 32])
+@pytest.mark.parametrize("N,K", [
+    (8200, 1024),   # 32-row blocks (N >= 8192), ragged N, one 4-unit step per wave
+    (2100, 8192),   # 16-row blocks with 8-unit steps, ragged N
+    (2064, 256),    # a single step: three of the four waves of a block get none
+    (2048, 768),    # three steps over four waves
+    (4096, 4352),   # seventeen steps: uneven slices and an odd step count per wave
+])
+def test_qmvs_blocks_and_steps(gpu, oracle, M, N, K):
+    """The int4 group-64 skinny GEMV (qmvs): both block heights, both step sizes,
+    slices with no steps or an odd number of them, one and two 16-row x tiles."""
+    _qmm_case(gpu, oracle, M, N, K, 4, 64, seed=9100 + M * 7 + N + K)
+
+
+def test_qmvs_bias(gpu, oracle):
+    _qmm_case(gpu, oracle, 12, 8256, 512, 4, 64, seed=9201, bias=True)
+    _qmm_case(gpu, oracle, 30, 2080, 1024, 4, 64, seed=9202, bias=True)
+
+
 @pytest.mark.parametrize("M", [1, 9, 70, 300])
 def test_qlinear_bias_epilogue(gpu, oracle, M):
     _qmm_case(gpu, oracle, M, 512, 1024, 4, 64, seed=300 + M, bias=True)
