@@ -10,7 +10,8 @@ the 256 MB MALL cannot hold them); x ~ N(0,1) bf16.
 value = algorithmic HBM bytes of the step / measured step time (GB/s).
 Also reported, as extra fields: the same stack at M in {4, 8, 16, 32}, the
 north-star qmv points (4-bit 14336x4096 and 4096x14336 at M=1, rotating over
-distinct weight copies) and the qmm point (4-bit 14336x4096 at M=2048).
+distinct weight copies), the qmm points (4-bit, M=2048) and one MoE layer of
+configs 3 and 4 (moe_c3_M*, moe_c4_M*).
 
 The CPU baseline times the oracle's OpenMP routine (oracle/, kind "port") on a
 bounded sample of the same stack.
@@ -115,6 +116,90 @@ def stack_step_fn(torch, ops, stack, xs, outs, bits):
     return step
 
 
+def moe_points(torch, ops, gen, dev):
+    """Configs 3 and 4: one MoE layer per step (SwitchGLU over the routed experts,
+    the weighted top-k combine, and for config 4 the shared expert).  Each step of
+    a replayed graph uses its own routing (and, for config 4, its own shared
+    expert) so that consecutive steps do not find their experts in the 256 MB
+    last-level cache."""
+    from fastmlx_amd.roofline import HBM_PEAK_GBS, moe_bytes
+
+    def stacks(E, N, K):
+        return gen_quant_stack(torch, E, N, K, gen, dev)
+
+    out = {}
+    # config 3: 512 experts, 2048 -> 512 -> 2048, top-10 uniform, softmax weights
+    E, D, I, k = 512, 2048, 512, 10
+    gate, up, down = stacks(E, I, D), stacks(E, I, D), stacks(E, D, I)
+    for M in (1, 16, 128, 512):
+        R = 16 if M <= 16 else 4
+        x = torch.randn(M, D, device=dev, generator=gen).to(torch.bfloat16)
+        routes = []
+        for _ in range(R):
+            inds = torch.argsort(torch.rand(M, E, device=dev, generator=gen), dim=1)[:, :k]
+            w = torch.softmax(torch.randn(M, k, device=dev, generator=gen), dim=1)
+            routes.append((inds.to(torch.int32).contiguous(), w.to(torch.bfloat16)))
+        ys = torch.empty(M, k, D, device=dev, dtype=torch.bfloat16)
+        yo = torch.empty(M, D, device=dev, dtype=torch.bfloat16)
+
+        def fn():
+            for inds, w in routes:
+                ops.switch_glu(x, inds, gate, up, down, GROUP, 4, out=ys)
+                ops.moe_combine(ys, w, out=yo)
+        g = capture(torch, fn)
+        per = time_graph(torch, g, 10, 2) / R
+        hit = sum(int(torch.unique(r[0]).numel()) for r in routes) / R
+        by = moe_bytes(M, D, I, k, int(round(hit)), 4, GROUP)
+        gbps = by / (per * 1e-3) / 1e9
+        out[f"moe_c3_M{M}"] = {"us": round(per * 1e3, 2), "GBps": round(gbps, 1),
+                               "frac_hbm": round(gbps / HBM_PEAK_GBS, 4),
+                               "experts_hit": round(hit, 1), "distinct_routings": R}
+    del gate, up, down
+    # config 4: 256 routed experts + 1 shared, 7168 -> 2048 -> 7168, top-8 Zipf(1.1)
+    E, D, I, k = 256, 7168, 2048, 8
+    gate, up, down = stacks(E, I, D), stacks(E, I, D), stacks(E, D, I)
+    R = 8
+    shared = [(stacks(1, I, D), stacks(1, I, D), stacks(1, D, I)) for _ in range(R)]
+    pz = torch.arange(1, E + 1, device=dev, dtype=torch.float64) ** -1.1
+    for M in (1, 32, 256):
+        x = torch.randn(M, D, device=dev, generator=gen).to(torch.bfloat16)
+        routes = []
+        for _ in range(R):
+            # sequential draws without replacement; ids permuted per step so that the
+            # hot ranks land on different experts from step to step
+            ranks = torch.multinomial(pz.expand(M, E), k, replacement=False, generator=gen)
+            perm = torch.randperm(E, device=dev, generator=gen)
+            inds = perm[ranks]
+            w = torch.sigmoid(torch.randn(M, k, device=dev, generator=gen))
+            w = w / w.sum(dim=1, keepdim=True)
+            routes.append((inds.to(torch.int32).contiguous(), w.to(torch.bfloat16)))
+        zero = torch.zeros(M, 1, device=dev, dtype=torch.int32)
+        ys = torch.empty(M, k, D, device=dev, dtype=torch.bfloat16)
+        ysh = torch.empty(M, 1, D, device=dev, dtype=torch.bfloat16)
+        yo = torch.empty(M, D, device=dev, dtype=torch.bfloat16)
+
+        def fn():
+            for (inds, w), (sg, su, sd) in zip(routes, shared):
+                ops.switch_glu(x, inds, gate, up, down, GROUP, 4, out=ys)
+                ops.switch_glu(x, zero, sg, su, sd, GROUP, 4, out=ysh)
+                ops.moe_combine(ys, w, shared=ysh.view(M, D), out=yo)
+        g = capture(torch, fn)
+        per = time_graph(torch, g, 6, 1) / R
+        hit = sum(int(torch.unique(r[0]).numel()) for r in routes) / R
+        by = moe_bytes(M, D, I, k, int(round(hit)), 4, GROUP, shared_I=I)
+        gbps = by / (per * 1e-3) / 1e9
+        out[f"moe_c4_M{M}"] = {"us": round(per * 1e3, 2), "GBps": round(gbps, 1),
+                               "frac_hbm": round(gbps / HBM_PEAK_GBS, 4),
+                               "experts_hit": round(hit, 1), "distinct_routings": R}
+    return out
+
+
+def gen_quant_stack(torch, E, N, K, gen, dev):
+    """Stacked experts [E, N, K/8] with the same value distributions as gen_quant."""
+    w, s, b = gen_quant(torch, E * N, K, 4, gen, dev)
+    return w.view(E, N, -1), s.view(E, N, -1), b.view(E, N, -1)
+
+
 def cpu_baseline(torch, stack, xs, M, bits, target_s=10.0):
     """Oracle CPU routine on the first layers of the same stack (same bytes)."""
     import numpy as np
@@ -164,6 +249,7 @@ def main():
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="skip the secondary points")
+    ap.add_argument("--no-moe", action="store_true", help="skip the MoE layer points")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path has no "
@@ -254,6 +340,9 @@ def main():
             tf = qmm_flops(2048, N, K) / (per * 1e-3) / 1e12
             extra[f"qmm_{N}x{K}_M2048"] = {"us": round(per * 1e3, 2), "TFLOPs": round(tf, 1),
                                            "frac_mfma": round(tf / BF16_MFMA_PEAK_TFLOPS, 4)}
+
+        if not args.no_moe:
+            extra.update(moe_points(torch, ops, gen, dev))
 
     result = {
         "metric": "qmv HBM GB/s (% peak) at M=1; qmm TFLOP/s (% MFMA) at M=2048; vs CPU",

@@ -178,6 +178,37 @@ int stream_arena(hipStream_t s, size_t bytes, void** out, const char* op) {
   return FMXQ_OK;
 }
 
+size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Counting sort in one block keeps two (E + 1)-entry tables in LDS.
+constexpr int64_t kSortMaxExperts = 16384;
+// Segments run along the grid's y axis.
+constexpr int64_t kMaxSegmentsGrid = 65535;
+
+// Scratch of the segmented MoE product in the stream arena: the sorted order,
+// ids and x rows of S slots, the segment table and count, and (SwitchGLU) the
+// h rows of the sorted slots.
+struct MoeScratch {
+  uint32_t *order, *rhs, *lhs, *seg, *nseg;
+  uint16_t* h;
+};
+int moe_scratch(hipStream_t s, int64_t S, int64_t h_cols, int64_t max_seg, MoeScratch* m,
+                const char* op) {
+  const size_t ib = align_up((size_t)S * sizeof(uint32_t));
+  const size_t sb = align_up((size_t)max_seg * 2 * sizeof(uint32_t));
+  const size_t hb = align_up((size_t)S * h_cols * sizeof(uint16_t));
+  void* arena = nullptr;
+  if (int rc = stream_arena(s, 3 * ib + sb + 256 + hb, &arena, op)) return rc;
+  char* p = static_cast<char*>(arena);
+  m->order = reinterpret_cast<uint32_t*>(p);
+  m->rhs = reinterpret_cast<uint32_t*>(p + ib);
+  m->lhs = reinterpret_cast<uint32_t*>(p + 2 * ib);
+  m->seg = reinterpret_cast<uint32_t*>(p + 3 * ib);
+  m->nseg = reinterpret_cast<uint32_t*>(p + 3 * ib + sb);
+  m->h = h_cols ? reinterpret_cast<uint16_t*>(p + 3 * ib + sb + 256) : nullptr;
+  return FMXQ_OK;
+}
+
 int qmm_common(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
                const uint16_t* biases, const uint16_t* bias, uint16_t* y, int64_t M, int64_t N,
                int64_t K, bool transpose, int group_size, int bits, void* stream,
@@ -300,10 +331,29 @@ int fmxq_gather_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* scales
     return fail(FMXQ_ERR_SHAPE, "%s: batch*Mx=%lld too large", op, (long long)(batch * Mx));
   uint32_t* flag = nullptr;
   if (int rc = device_flag(&flag)) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (Mx == 1 && E <= kSortMaxExperts && fmxq::moe_qmvs_supported(N, K, bits, group_size) &&
+      aligned16(scales) && aligned16(biases)) {
+    // Items sorted by expert, then one grouped product per expert segment; the
+    // sort's order maps each sorted item back to its output row.
+    const int window = fmxq::moe_window(batch, E);
+    const int64_t max_seg = fmxq::moe_max_segments(batch, E, window);
+    if (max_seg <= kMaxSegmentsGrid) {
+      MoeScratch m;
+      if (int rc = moe_scratch(s, batch, 0, max_seg, &m, op)) return rc;
+      if (int rc = hip_status(fmxq::launch_sort_slots(rhs_indices, batch, lhs_div, E, m.order,
+                                                      m.rhs, m.lhs, s, lhs_indices, m.seg,
+                                                      m.nseg, window),
+                              "gather_qmm: sort"))
+        return rc;
+      fmxq::MoeArgs a{x, m.lhs, {w, nullptr}, {scales, nullptr}, {biases, nullptr}, m.rhs,
+                      m.seg, m.nseg, y, m.order, batch, N, K, E, x_batch, flag};
+      return hip_status(fmxq::launch_moe_qmvs(a, 1, window, max_seg, s), op);
+    }
+  }
   fmxq::GatherArgs a{x,      w,     scales,  biases, lhs_indices, rhs_indices, y,
                      batch,  x_batch, lhs_div, Mx,   N,           K,           E,
                      group_size, bits, flag};
-  hipStream_t s = static_cast<hipStream_t>(stream);
   if (sorted_indices && batch * Mx >= fmxq::kGroupedMinSlots && fmxq::gather_mfma_supported(a))
     return hip_status(fmxq::launch_gather_mfma(a, s), op);
   return hip_status(fmxq::launch_gather_qmv(a, s), op);
@@ -337,8 +387,6 @@ int gather_dispatch(const fmxq::GatherArgs& a, bool sorted, hipStream_t s) {
   return hip_status(fmxq::launch_gather_qmv(a, s), "switch_glu: gather");
 }
 
-size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
-
 }  // namespace
 
 extern "C" int fmxq_switch_glu(const uint16_t* x, const uint32_t* inds, const uint32_t* w_gate,
@@ -363,11 +411,36 @@ extern "C" int fmxq_switch_glu(const uint16_t* x, const uint32_t* inds, const ui
       !aligned16(out))
     return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: x, weights and out must be 16-byte aligned", op);
   if (S > 0x7fffffffLL) return fail(FMXQ_ERR_SHAPE, "%s: too many slots", op);
-  // The reference sorts once routing reaches 64 slots (switch_glu.go:119-124).
-  const bool sort = S >= 64 && E <= 16384;
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint32_t* flag = nullptr;
   if (int rc = device_flag(&flag)) return rc;
+  const int window = fmxq::moe_window(S, E);
+  const int64_t max_seg = fmxq::moe_max_segments(S, E, window);
+  if (E <= kSortMaxExperts && max_seg <= kMaxSegmentsGrid &&
+      fmxq::moe_qmvs_supported(I, D, bits, group_size) &&
+      fmxq::moe_qmvs_supported(D, I, bits, group_size) && aligned16(s_gate) &&
+      aligned16(b_gate) && aligned16(s_up) && aligned16(b_up) && aligned16(s_down) &&
+      aligned16(b_down)) {
+    // Sorted slots (for every slot count: the order cannot change a value, each
+    // slot being its own product row), then gate and up fused with silu * up into
+    // h in sorted order, then down written to each slot's own output row.
+    MoeScratch m;
+    if (int rc = moe_scratch(s, S, I, max_seg, &m, op)) return rc;
+    if (int rc = hip_status(fmxq::launch_sort_slots(inds, S, topk, E, m.order, m.rhs, m.lhs, s,
+                                                    nullptr, m.seg, m.nseg, window),
+                            "switch_glu: sort"))
+      return rc;
+    fmxq::MoeArgs gu{x, m.lhs, {w_gate, w_up}, {s_gate, s_up}, {b_gate, b_up}, m.rhs, m.seg,
+                     m.nseg, m.h, nullptr, S, I, D, E, T, flag};
+    if (int rc = hip_status(fmxq::launch_moe_qmvs(gu, 2, window, max_seg, s),
+                            "switch_glu: gate/up"))
+      return rc;
+    fmxq::MoeArgs dn{m.h, nullptr, {w_down, nullptr}, {s_down, nullptr}, {b_down, nullptr},
+                     m.rhs, m.seg, m.nseg, out, m.order, S, D, I, E, S, flag};
+    return hip_status(fmxq::launch_moe_qmvs(dn, 1, window, max_seg, s), "switch_glu: down");
+  }
+  // The reference sorts once routing reaches 64 slots (switch_glu.go:119-124).
+  const bool sort = S >= 64 && E <= kSortMaxExperts;
   const size_t hbytes = align_up((size_t)S * I * sizeof(uint16_t));
   const size_t ibytes = align_up((size_t)S * sizeof(uint32_t));
   void* arena = nullptr;

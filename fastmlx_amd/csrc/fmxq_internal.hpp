@@ -100,10 +100,15 @@ hipError_t launch_qmm_prefill(const QmmArgs& a, hipStream_t stream);
 
 hipError_t launch_gather_qmv(const GatherArgs& a, hipStream_t stream);
 
-// MoE pieces around gather_qmm (fmxq_moe.hip).
-hipError_t launch_sort_slots(const uint32_t* inds, int64_t S, int64_t topk, int64_t E,
+// MoE pieces around gather_qmm (fmxq_moe.hip).  The sort orders the S slots by
+// expert id (ids >= E last); lhs_sorted[pos] = lhs ? lhs[s] : s / lhs_div for the
+// slot s moved to pos.  With seg non-null it also writes the segment table of the
+// sorted order ((start, len) pairs, each run of one id cut at multiples of
+// `window` slots) and the segment count to *nseg.
+hipError_t launch_sort_slots(const uint32_t* inds, int64_t S, int64_t lhs_div, int64_t E,
                              uint32_t* order, uint32_t* rhs_sorted, uint32_t* lhs_sorted,
-                             hipStream_t stream);
+                             hipStream_t stream, const uint32_t* lhs = nullptr,
+                             uint32_t* seg = nullptr, uint32_t* nseg = nullptr, int window = 16);
 hipError_t launch_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* h, int64_t n,
                            hipStream_t stream);
 hipError_t launch_moe_combine(const uint16_t* y, const uint16_t* w, const uint16_t* shared,
@@ -126,6 +131,30 @@ struct RouteArgs {
   bool norm, in_bf16, out_bf16;
 };
 hipError_t launch_route(const RouteArgs& a, bool group, hipStream_t stream);
+
+// Grouped int4 (group 64, K a multiple of 256) product over expert segments of
+// a sorted slot order (fmxq_moe_gemm.hip).  w/s/b hold NMAT stacks [E, N, .]
+// (gate and up for NMAT = 2, which writes silu(gate) * up); slot s reads x row
+// lhs ? lhs[s] : s and writes output row yrow ? yrow[s] : s.
+struct MoeArgs {
+  const uint16_t* x;        // [x_rows, K]
+  const uint32_t* lhs;      // [S] or null
+  const uint32_t* w[2];
+  const uint16_t* s[2];
+  const uint16_t* b[2];
+  const uint32_t* rhs;      // [S] expert of each slot, sorted
+  const uint32_t* seg;      // (start, len) pairs
+  const uint32_t* nseg;     // segment count (device)
+  uint16_t* y;              // [rows, N]
+  const uint32_t* yrow;     // [S] or null
+  int64_t S, N, K, E, x_rows;
+  uint32_t* err_flag;
+};
+bool moe_qmvs_supported(int64_t N, int64_t K, int bits, int group_size);
+int moe_window(int64_t S, int64_t E);
+int64_t moe_max_segments(int64_t S, int64_t E, int window);
+hipError_t launch_moe_qmvs(const MoeArgs& a, int nmat, int window, int64_t max_seg,
+                           hipStream_t stream);
 
 // Grouped MFMA gather for expert-sorted batches (int4 group_size >= 64, int8 >= 32).
 constexpr int64_t kGroupedMinSlots = 32;

@@ -7,7 +7,8 @@
 //   - sort_slots_kernel: a counting sort of the flattened routing slots by
 //     expert id in one block (replaces argsort + take + floor_divide); the
 //     order inside an expert is arbitrary, which cannot change any value
-//     because every slot is its own GEMM row;
+//     because every slot is its own GEMM row.  It also cuts the sorted order
+//     into the expert segments the grouped product (fmxq_moe_gemm.hip) runs on;
 //   - silu_mul_kernel: h = bf16(bf16(g * bf16(sigmoid(g))) * u), the rounding of
 //     the silu (sigmoid then mul, qwen3_forward.go:229-239) then mul op chain;
 //   - the unsort is fused into the down projection's store (GatherArgs::yrow).
@@ -18,14 +19,56 @@
 
 namespace fmxq {
 
+// Exclusive prefix sum of one value per thread over the block; *total gets the
+// sum.  wsum: one LDS word per wave.
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* wsum,
+                                                         uint32_t* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t inc = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t t = (uint32_t)__shfl_up((int)inc, off, 64);
+    if (lane >= off) inc += t;
+  }
+  if (lane == 63) wsum[wave] = inc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t run = 0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) {
+      const uint32_t t = wsum[w];
+      wsum[w] = run;
+      run += t;
+    }
+    *total = run;
+  }
+  __syncthreads();
+  const uint32_t r = wsum[wave] + inc - v;
+  __syncthreads();
+  return r;
+}
+
+// Pieces of the sorted range [off, off + c) cut at multiples of window.
+__device__ __forceinline__ uint32_t range_pieces(uint32_t off, uint32_t c, uint32_t window) {
+  return c ? (off + c - 1) / window - off / window + 1 : 0u;
+}
+
 // One block: counts per expert in LDS, exclusive scan, scatter.  Ids >= E go
 // to a final bucket (the gather kernels zero those rows and raise the flag).
+// Each thread owns a run of consecutive buckets for the scans.  With seg
+// non-null, before the scatter: the pieces of every bucket's range
+// [off, off + count) cut at multiples of `window`, as (start, len) pairs in
+// bucket order, and their number in *nseg.
 __global__ __launch_bounds__(1024) void sort_slots_kernel(const uint32_t* __restrict__ inds,
-                                                          int64_t S, int64_t topk, int64_t E,
+                                                          int64_t S, int64_t lhs_div, int64_t E,
                                                           uint32_t* __restrict__ order,
                                                           uint32_t* __restrict__ rhs_sorted,
-                                                          uint32_t* __restrict__ lhs_sorted) {
+                                                          uint32_t* __restrict__ lhs_sorted,
+                                                          const uint32_t* __restrict__ lhs,
+                                                          uint32_t* __restrict__ seg,
+                                                          uint32_t* __restrict__ nseg,
+                                                          int window) {
   extern __shared__ uint32_t cnt[];  // E + 1 counters, then E + 1 cursors
+  __shared__ uint32_t wsum[16], total;
   const int64_t nb = E + 1;
   uint32_t* cur = cnt + nb;
   for (int64_t i = threadIdx.x; i < nb; i += blockDim.x) cnt[i] = 0;
@@ -35,20 +78,40 @@ __global__ __launch_bounds__(1024) void sort_slots_kernel(const uint32_t* __rest
     atomicAdd(&cnt[e < (uint64_t)E ? e : E], 1u);
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t run = 0;
-    for (int64_t i = 0; i < nb; ++i) {
-      cur[i] = run;
-      run += cnt[i];
-    }
+  const int64_t per = (nb + blockDim.x - 1) / blockDim.x;
+  const int64_t b0 = threadIdx.x * per < nb ? threadIdx.x * per : nb;
+  const int64_t b1 = b0 + per < nb ? b0 + per : nb;
+  uint32_t local = 0;
+  for (int64_t i = b0; i < b1; ++i) local += cnt[i];
+  uint32_t base = block_exclusive_scan(local, wsum, &total);
+  for (int64_t i = b0; i < b1; ++i) {
+    cur[i] = base;
+    base += cnt[i];
   }
   __syncthreads();
+  if (seg) {
+    uint32_t lp = 0;
+    for (int64_t i = b0; i < b1; ++i) lp += range_pieces(cur[i], cnt[i], (uint32_t)window);
+    uint32_t k = block_exclusive_scan(lp, wsum, &total);
+    if (threadIdx.x == 0) *nseg = total;
+    for (int64_t i = b0; i < b1; ++i) {
+      const uint32_t end = cur[i] + cnt[i];
+      for (uint32_t p = cur[i]; p < end; ++k) {
+        const uint32_t wend = (p / window + 1) * window;
+        const uint32_t q = wend < end ? wend : end;
+        seg[2 * k] = p;
+        seg[2 * k + 1] = q - p;
+        p = q;
+      }
+    }
+    __syncthreads();  // the scatter below advances cur
+  }
   for (int64_t s = threadIdx.x; s < S; s += blockDim.x) {
     const uint32_t e = inds[s];
     const uint32_t pos = atomicAdd(&cur[e < (uint64_t)E ? e : E], 1u);
     order[pos] = (uint32_t)s;
     rhs_sorted[pos] = e;
-    lhs_sorted[pos] = (uint32_t)(s / topk);
+    lhs_sorted[pos] = lhs ? lhs[s] : (uint32_t)(s / lhs_div);
   }
 }
 
@@ -117,11 +180,14 @@ static unsigned grid_for(int64_t items, int64_t per_block) {
   return (unsigned)(b < 1 ? 1 : b);
 }
 
-hipError_t launch_sort_slots(const uint32_t* inds, int64_t S, int64_t topk, int64_t E,
+hipError_t launch_sort_slots(const uint32_t* inds, int64_t S, int64_t lhs_div, int64_t E,
                              uint32_t* order, uint32_t* rhs_sorted, uint32_t* lhs_sorted,
-                             hipStream_t stream) {
+                             hipStream_t stream, const uint32_t* lhs, uint32_t* seg,
+                             uint32_t* nseg, int window) {
+  if (seg && (!nseg || window < 1)) return hipErrorInvalidValue;
   const size_t lds = (size_t)(E + 1) * 2 * sizeof(uint32_t);
-  sort_slots_kernel<<<1, 1024, lds, stream>>>(inds, S, topk, E, order, rhs_sorted, lhs_sorted);
+  sort_slots_kernel<<<1, 1024, lds, stream>>>(inds, S, lhs_div, E, order, rhs_sorted, lhs_sorted,
+                                              lhs, seg, nseg, window);
   return hipGetLastError();
 }
 

@@ -1,0 +1,206 @@
+// fmxq_moe_gemm.hip -- grouped int4 (group 64) product over expert segments:
+// the gather_qmm calls of a SwitchGLU layer (compute/models/switch_glu.go:107-153;
+// mlx_gather_qmm, mlxgo/binding_cgo.go:645-673) once the routing slots are sorted
+// by expert.
+//
+// Slots sorted by expert id form runs; a segment is the part of one run inside
+// one aligned window of W slots (W = 16 MT), so a segment holds at most 16 MT
+// slots of one expert (a block of a 32-slot window whose segment has at most 16
+// slots walks one 16-row tile only).  sort_slots_kernel (fmxq_moe.hip) writes the segment table
+// while it sorts.  Grid: (column tiles, segment bound); blocks past the actual
+// segment count return at once.  A block of 4 waves = WC column groups x KS K
+// slices computes its segment's rows against 16 NTT WC columns of that expert's
+// weights with the skinny-product walk of fmxq_qmvs.hpp (whole-segment weight
+// loads through LDS, v_mfma_f32_16x16x32_bf16), so each expert's weights are read
+// once per segment whatever the number of slots.
+//
+// NMAT = 2 fuses the gate and up projections: both walk the same x rows and the
+// block writes h = silu(gate) * up with the op chain's bf16 roundings
+// (qwen3_forward.go:229-239): g, u rounded to bf16, sigmoid rounded, g * sigmoid
+// rounded, times u rounded.  NMAT = 1 writes bf16(acc) to output row yrow[slot]
+// (the unsort of switch_glu.go:150-152) or to row slot.
+//
+// A slot whose expert id is >= E or whose x row is >= x_rows gets a zero output
+// row and raises err_flag.
+#include "fmxq_common.hpp"
+#include "fmxq_internal.hpp"
+#include "fmxq_qmvs.hpp"
+
+namespace fmxq {
+namespace {
+
+__device__ __forceinline__ float r16(float v) { return bf16_bits_to_f32(f32_to_bf16_rne(v)); }
+
+template <int MT, int NTT, int WC, int NMAT>
+__global__ __launch_bounds__(256) void moe_qmvs_kernel(MoeArgs a) {
+  constexpr int SU = 4;
+  constexpr int KS = 4 / WC;
+  using G = QmvsGeom<NTT, SU>;
+  __shared__ __attribute__((aligned(16))) uint8_t stage[4][NMAT * G::STAGE];
+  __shared__ float red[KS > 1 ? KS - 1 : 1][WC][NMAT][MT][NTT][4][64];
+
+  const int64_t sg = blockIdx.y;
+  if (sg >= (int64_t)*a.nseg) return;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wc = wave % WC, ks = wave / WC;
+  const int c16 = lane & 15, q = lane >> 4;
+  const int64_t start = a.seg[2 * sg], len = a.seg[2 * sg + 1];
+  const uint32_t e = a.rhs[start];
+  const int64_t nb = (int64_t)blockIdx.x * (16 * NTT * WC) + wc * (16 * NTT);
+  const bool bad_e = (int64_t)e >= a.E;
+
+  // x row of each of this lane's slots (row of the segment's first slot for lanes
+  // past its end; a bad slot reads row 0 and is zeroed at the store).
+  const uint16_t* xrow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = 16 * mt + c16;
+    const int64_t slot = start + (m < len ? m : 0);
+    int64_t xr = a.lhs ? (int64_t)a.lhs[slot] : slot;
+    if (xr >= a.x_rows) xr = 0;
+    xrow[mt] = a.x + xr * a.K + q * 16;
+  }
+
+  f32x4 acc[NMAT][MT][NTT];
+#pragma unroll
+  for (int p = 0; p < NMAT; ++p)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int t = 0; t < NTT; ++t) acc[p][mt][t] = f32x4{};
+  if (!bad_e) {
+    const int64_t wpr = a.K / 8, gpr = a.K / 64;
+    const uint32_t* w[NMAT];
+    const uint16_t* sc[NMAT];
+    const uint16_t* bi[NMAT];
+#pragma unroll
+    for (int p = 0; p < NMAT; ++p) {
+      w[p] = a.w[p] + (int64_t)e * a.N * wpr;
+      sc[p] = a.s[p] + (int64_t)e * a.N * gpr;
+      bi[p] = a.b[p] + (int64_t)e * a.N * gpr;
+    }
+    const int64_t nst = a.K / (SU * 64);
+    const int64_t st0 = ks * nst / KS, st1 = (ks + 1) * nst / KS;
+    if (MT == 2 && len <= 16) {
+      // Short segment of a 32-slot window: the 16-row walk (the second tile's
+      // accumulators stay zero and no row of it is stored).
+      const uint16_t* const x1[1] = {xrow[0]};
+      f32x4 acc1[NMAT][1][NTT];
+#pragma unroll
+      for (int p = 0; p < NMAT; ++p)
+#pragma unroll
+        for (int t = 0; t < NTT; ++t) acc1[p][0][t] = f32x4{};
+      qmvs_slice<1, NTT, SU, NMAT>(stage[wave], w, sc, bi, nb, a.N, a.K, x1, st0, st1, acc1);
+#pragma unroll
+      for (int p = 0; p < NMAT; ++p)
+#pragma unroll
+        for (int t = 0; t < NTT; ++t) acc[p][0][t] = acc1[p][0][t];
+    } else {
+      qmvs_slice<MT, NTT, SU, NMAT>(stage[wave], w, sc, bi, nb, a.N, a.K, xrow, st0, st1, acc);
+    }
+  }
+
+  if constexpr (KS > 1) {
+    if (ks > 0) {
+#pragma unroll
+      for (int p = 0; p < NMAT; ++p)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int t = 0; t < NTT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[ks - 1][wc][p][mt][t][r][lane] = acc[p][mt][t][r];
+    }
+    __syncthreads();
+    if (ks > 0) return;
+#pragma unroll
+    for (int p = 0; p < NMAT; ++p)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int t = 0; t < NTT; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int k = 0; k < KS - 1; ++k) acc[p][mt][t][r] += red[k][wc][p][mt][t][r][lane];
+  }
+
+  // C layout of a 16x16 tile: register r of lane l is row 4 (l / 16) + r,
+  // column l % 16.  Row m of tile mt is slot start + 16 mt + m.
+  bool raise = false;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 16 * mt + 4 * q + r;
+      if (m >= len) continue;
+      const int64_t slot = start + m;
+      const int64_t xr = a.lhs ? (int64_t)a.lhs[slot] : slot;
+      const bool bad = bad_e || xr >= a.x_rows;
+      raise |= bad;
+      const int64_t orow = a.yrow ? (int64_t)a.yrow[slot] : slot;
+      uint16_t* yr = a.y + orow * a.N;
+#pragma unroll
+      for (int t = 0; t < NTT; ++t) {
+        const int64_t n = nb + 16 * t + c16;
+        if (n >= a.N) continue;
+        uint16_t v;
+        if (bad) {
+          v = 0;
+        } else if constexpr (NMAT == 2) {
+          const float g = r16(acc[0][mt][t][r]), u = r16(acc[1][mt][t][r]);
+          const float sg_ = r16(1.f / (1.f + __expf(-g)));
+          v = (uint16_t)f32_to_bf16_rne(r16(r16(g * sg_) * u));
+        } else {
+          v = (uint16_t)f32_to_bf16_rne(acc[0][mt][t][r]);
+        }
+        yr[n] = v;
+      }
+    }
+  if (raise) atomicOr(a.err_flag, 1u);
+}
+
+template <int MT, int NTT, int NMAT>
+static hipError_t launch_wc(const MoeArgs& a, int wc, int64_t max_seg, hipStream_t stream) {
+  const int64_t cols = 16 * NTT * wc;
+  dim3 grid((unsigned)((a.N + cols - 1) / cols), (unsigned)max_seg);
+  if (wc == 1) moe_qmvs_kernel<MT, NTT, 1, NMAT><<<grid, 256, 0, stream>>>(a);
+  else if (wc == 2) moe_qmvs_kernel<MT, NTT, 2, NMAT><<<grid, 256, 0, stream>>>(a);
+  else moe_qmvs_kernel<MT, NTT, 4, NMAT><<<grid, 256, 0, stream>>>(a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool moe_qmvs_supported(int64_t N, int64_t K, int bits, int group_size) {
+  return bits == 4 && group_size == 64 && K % 256 == 0 && N >= 1;
+}
+
+int moe_window(int64_t S, int64_t E) { return S >= 2 * E ? 32 : 16; }
+
+int64_t moe_max_segments(int64_t S, int64_t E, int window) {
+  const int64_t runs = S < E + 1 ? S : E + 1;
+  const int64_t b = runs + (S + window - 1) / window;
+  return b < S ? b : S;
+}
+
+hipError_t launch_moe_qmvs(const MoeArgs& a, int nmat, int window, int64_t max_seg,
+                           hipStream_t stream) {
+  if (a.S <= 0 || a.N <= 0 || max_seg <= 0) return hipSuccess;
+  if (!moe_qmvs_supported(a.N, a.K, 4, 64) || (window != 16 && window != 32) ||
+      (nmat != 1 && nmat != 2))
+    return hipErrorInvalidValue;
+  // K slices per block: about four 4-unit steps per wave, at most 4 slices; the
+  // remaining waves of the block take further column groups.
+  const int64_t nst = a.K / 256;
+  const int ks = nst >= 16 ? 4 : (nst >= 8 ? 2 : 1);
+  const int wc = 4 / ks;
+  if (nmat == 2)
+    return window == 16 ? launch_wc<1, 1, 2>(a, wc, max_seg, stream)
+                        : launch_wc<2, 1, 2>(a, wc, max_seg, stream);
+  return window == 16 ? launch_wc<1, 2, 1>(a, wc, max_seg, stream)
+                      : launch_wc<2, 2, 1>(a, wc, max_seg, stream);
+}
+
+}  // namespace fmxq

@@ -1,0 +1,209 @@
+// fmxq_qmvs.hpp -- the K walk of one wave of the int4 (group 64) skinny MFMA
+// product, shared by the dense GEMV (qmvs_kernel, fmxq_skinny.hip) and the
+// grouped MoE product (fmxq_moe_gemm.hip).
+//
+// A wave owns 16 NTT output columns (rows of W) starting at nb, up to 16 MT rows
+// of x (lane (m = l % 16, q = l / 16) holds the pointer to its x row, advanced by
+// 16 q elements), NMAT weight matrices sharing those x rows (gate and up of a
+// SwitchGLU), and the steps [s0, s1) of SU 64-value units each.
+//
+// Per step, for each matrix:
+//   - the 16 NTT rows x 32 SU bytes of packed weights are read with whole-segment
+//     loads (instruction i, lane L -> row i * (64 / LPR) + L / LPR, 16-byte chunk
+//     L % LPR) two steps ahead into registers and written to the wave's LDS stage
+//     at XOR-swizzled chunk positions;
+//   - the stage is read back in the v_mfma_f32_16x16x32_bf16 B layout: lane
+//     (c = l % 16, q) takes words 2q, 2q+1 of its row's unit, MFMA i word 2q+i,
+//     as bf16(128 + q) pairs (exponent trick, fmxq_mfma_frag.hpp);
+//   - scales and biases of the step come as one load per lane and reach the
+//     lanes that use them through ds_bpermute.
+// A = x in the same k order (xfrag4 of two 16-byte pieces per unit), XD units
+// ahead.  Per group: P = sum x (128 + q), xs = sum x (MFMA against ones),
+// acc += s P + (b - 128 s) xs.
+//
+// The stage needs no barrier: a wave reads only what it wrote, and the LDS
+// operations of one wave complete in order.  Rows past N re-read row N-1 and
+// steps past s1 re-read step s1-1; neither reaches an output.
+#pragma once
+#include "fmxq_common.hpp"
+#include "fmxq_mfma_frag.hpp"
+
+namespace fmxq {
+
+constexpr int kQmvsXD = 4;  // x units in flight per wave
+
+// Stage position of 16-byte chunk c of row r: 128-byte rows (SU = 4) use the
+// 8-chunk XOR pattern, 256-byte rows (SU = 8) XOR with the row's low 4 bits, so
+// the 16 rows a B-fragment read touches at one chunk land on distinct banks.
+template <int SU>
+__device__ __forceinline__ int qmvs_pos(int c, int r) {
+  if constexpr (SU == 4) return c ^ ((r & 7) ^ ((r >> 3) & 1));
+  else return c ^ (r & 15);
+}
+
+template <int NTT, int SU>
+struct QmvsGeom {
+  static constexpr int ROWS = 16 * NTT;
+  static constexpr int RB = SU * 32;           // bytes of one row per step
+  static constexpr int LPR = RB / 16;          // lanes per row in one load instruction
+  static constexpr int NI = ROWS * RB / 1024;  // load instructions per step
+  static constexpr int SPL = (64 / ROWS == 2) ? SU : SU / 2;  // groups per scale load
+  static constexpr int STAGE = ROWS * RB;      // LDS bytes per matrix
+};
+
+// w, sc, bi: the NMAT matrices ([N, K/8] u32, [N, K/64] bf16 x2).  stage: this
+// wave's NMAT * STAGE bytes of LDS.  xrow: per-lane x row pointers (see above).
+template <int MT, int NTT, int SU, int NMAT>
+__device__ __forceinline__ void qmvs_slice(uint8_t* stage, const uint32_t* const (&w)[NMAT],
+                                           const uint16_t* const (&sc)[NMAT],
+                                           const uint16_t* const (&bi)[NMAT], int64_t nb,
+                                           int64_t N, int64_t K, const uint16_t* const (&xrow)[MT],
+                                           int64_t s0, int64_t s1,
+                                           f32x4 (&acc)[NMAT][MT][NTT]) {
+  using G = QmvsGeom<NTT, SU>;
+  constexpr int XD = kQmvsXD, U = 64, NI = G::NI, LPR = G::LPR, RB = G::RB, ROWS = G::ROWS;
+  constexpr int SPL = G::SPL;
+  typedef uint32_t sbv_t __attribute__((ext_vector_type(SPL / 2)));
+  const int lane = threadIdx.x & 63;
+  const int c16 = lane & 15, q = lane >> 4;
+  const int64_t wpr = K / 8, gpr = K / 64;
+
+  int64_t wq[NI];
+  int wo[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int r = i * (64 / LPR) + lane / LPR;
+    int64_t n = nb + r;
+    n = n < N ? n : N - 1;
+    wq[i] = n * wpr + (lane % LPR) * 4;
+    wo[i] = r * RB + (qmvs_pos<SU>(lane % LPR, r) << 4);
+  }
+  int wr[NTT][SU];
+#pragma unroll
+  for (int t = 0; t < NTT; ++t)
+#pragma unroll
+    for (int j = 0; j < SU; ++j) {
+      const int r = 16 * t + c16;
+      wr[t][j] = r * RB + (qmvs_pos<SU>(2 * j + (q >> 1), r) << 4) + (q & 1) * 8;
+    }
+  // Scale loads: lane -> row l % ROWS, kind (l / ROWS) & 1 (0 scales, 1 biases)
+  // and, for 16-row tiles, which half of the step's groups (l / ROWS / 2).
+  const int sh = lane / ROWS;
+  int64_t nrow = nb + lane % ROWS;
+  nrow = nrow < N ? nrow : N - 1;
+  const int64_t soff = nrow * gpr + ((64 / ROWS == 2) ? 0 : (sh >> 1) * SPL);
+  const uint16_t* sbrow[NMAT];
+#pragma unroll
+  for (int p = 0; p < NMAT; ++p) sbrow[p] = ((sh & 1) ? bi[p] : sc[p]) + soff;
+
+  u32x4 wbuf[2][NMAT][NI];
+  sbv_t sbuf[2][NMAT];
+  u32x4 xv[XD][MT][2];
+  auto load_w = [&](int d, int64_t st) {
+    st = st < s1 ? st : s1 - 1;
+#pragma unroll
+    for (int p = 0; p < NMAT; ++p) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+        wbuf[d][p][i] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(w[p] + wq[i] + st * SU * 8));
+      sbuf[d][p] = *reinterpret_cast<const sbv_t*>(sbrow[p] + st * SU);
+    }
+  };
+  const int64_t u_end = s1 * SU;
+  auto load_x = [&](int d, int64_t u) {
+    u = u < u_end ? u : u_end - 1;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const u32x4* xs = reinterpret_cast<const u32x4*>(xrow[mt] + u * U);
+      xv[d][mt][0] = xs[0];
+      xv[d][mt][1] = xs[1];
+    }
+  };
+  const bf16x8 ones = as_bf16x8(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+
+  if (s1 <= s0) return;
+  load_w(0, s0);
+  load_w(1, s0 + 1);
+#pragma unroll
+  for (int d = 0; d < XD; ++d) load_x(d, s0 * SU + d);
+  for (int64_t st = s0; st < s1; st += 2) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int64_t stp = st + e;
+      if (stp < s1) {
+#pragma unroll
+        for (int p = 0; p < NMAT; ++p)
+#pragma unroll
+          for (int i = 0; i < NI; ++i)
+            *reinterpret_cast<u32x4*>(stage + p * G::STAGE + wo[i]) = wbuf[e][p][i];
+        sbv_t mine[NMAT];
+#pragma unroll
+        for (int p = 0; p < NMAT; ++p) mine[p] = sbuf[e][p];
+        load_w(e, stp + 2);
+        // Scale and bias pairs (groups 2k, 2k+1 of the step) of the wave's rows.
+        uint32_t sv[NMAT][NTT][SU / 2], bv[NMAT][NTT][SU / 2];
+#pragma unroll
+        for (int p = 0; p < NMAT; ++p)
+#pragma unroll
+          for (int t = 0; t < NTT; ++t)
+#pragma unroll
+            for (int k = 0; k < SU / 2; ++k) {
+              const int row = 16 * t + c16;
+              const int hi = (64 / ROWS == 2) ? 0 : k / (SPL / 2);
+              const int idx = (64 / ROWS == 2) ? k : k % (SPL / 2);
+              sv[p][t][k] = (uint32_t)__shfl((int)mine[p][idx], (2 * hi) * ROWS + row, 64);
+              bv[p][t][k] = (uint32_t)__shfl((int)mine[p][idx], (2 * hi + 1) * ROWS + row, 64);
+            }
+#pragma unroll
+        for (int j = 0; j < SU; ++j) {
+          const int xd = (e * SU + j) % XD;
+          bf16x8 A[MT][2];
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            A[mt][0] = xfrag4(xv[xd][mt][0]);
+            A[mt][1] = xfrag4(xv[xd][mt][1]);
+          }
+          load_x(xd, stp * SU + j + XD);
+          f32x4 xs[MT];
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            xs[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mt][0], ones, f32x4{}, 0, 0, 0);
+            xs[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mt][1], ones, xs[mt], 0, 0, 0);
+          }
+#pragma unroll
+          for (int p = 0; p < NMAT; ++p) {
+            u32x2 wv[NTT];
+#pragma unroll
+            for (int t = 0; t < NTT; ++t)
+              wv[t] = *reinterpret_cast<const u32x2*>(stage + p * G::STAGE + wr[t][j]);
+            f32x4 P[MT][NTT];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+              for (int t = 0; t < NTT; ++t) {
+                P[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mt][0], wfrag<4>(wv[t][0]),
+                                                                   f32x4{}, 0, 0, 0);
+                P[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mt][1], wfrag<4>(wv[t][1]),
+                                                                   P[mt][t], 0, 0, 0);
+              }
+#pragma unroll
+            for (int t = 0; t < NTT; ++t) {
+              const float s = (j & 1) ? bf16_hi(sv[p][t][j >> 1]) : bf16_lo(sv[p][t][j >> 1]);
+              const float b = (j & 1) ? bf16_hi(bv[p][t][j >> 1]) : bf16_lo(bv[p][t][j >> 1]);
+              const float bo = __builtin_fmaf(-128.f, s, b);
+#pragma unroll
+              for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                  acc[p][mt][t][r] = __builtin_fmaf(s, P[mt][t][r],
+                                                    __builtin_fmaf(bo, xs[mt][r], acc[p][mt][t][r]));
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+}  // namespace fmxq

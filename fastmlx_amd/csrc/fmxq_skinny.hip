@@ -41,6 +41,7 @@
 #include "fmxq_common.hpp"
 #include "fmxq_internal.hpp"
 #include "fmxq_mfma_frag.hpp"
+#include "fmxq_qmvs.hpp"
 
 namespace fmxq {
 
@@ -221,177 +222,41 @@ hipError_t launch_qmv_mfma(const QmmArgs& a, hipStream_t stream) {
 
 // ---------------------------------------------------------------------------
 // qmvs_kernel.  Block: KS waves over the same 16 NTT rows, each wave a
-// contiguous run of SU-unit steps; per step a wave stages 16 NTT rows x 32 SU
-// bytes of packed weights through its own LDS slot (no barrier: a wave reads
-// only what it wrote, and LDS operations of one wave complete in order).
+// contiguous run of SU-unit steps walked by qmvs_slice (fmxq_qmvs.hpp); the
+// slices meet in LDS.
 
 namespace {
 
 constexpr int kQmvsKS = 4;  // waves (K slices) per block
-constexpr int kQmvsXD = 4;  // x units in flight per wave
-
-// Stage position of 16-byte chunk c of row r: 128-byte rows (SU = 4) use the
-// 8-chunk XOR pattern, 256-byte rows (SU = 8) XOR with the row's low 4 bits, so
-// the 16 rows a B-fragment read touches at one chunk land on distinct banks.
-template <int SU>
-__device__ __forceinline__ int qmvs_pos(int c, int r) {
-  if constexpr (SU == 4) return c ^ ((r & 7) ^ ((r >> 3) & 1));
-  else return c ^ (r & 15);
-}
 
 template <int MT, int NTT, int SU>
 __global__ __launch_bounds__(kQmvsKS * 64) void qmvs_kernel(QmmArgs a) {
-  constexpr int KS = kQmvsKS, XD = kQmvsXD, U = 64;
-  constexpr int ROWS = 16 * NTT;
-  constexpr int RB = SU * 32;             // bytes of one row per step
-  constexpr int LPR = RB / 16;            // lanes per row in one load instruction
-  constexpr int NI = ROWS * RB / 1024;    // load instructions per step
-  constexpr int SPL = (64 / ROWS == 2) ? SU : SU / 2;  // groups per scale load
-  typedef uint32_t sbv_t __attribute__((ext_vector_type(SPL / 2)));
-  __shared__ __attribute__((aligned(16))) uint8_t stage[KS][ROWS * RB];
+  constexpr int KS = kQmvsKS;
+  using G = QmvsGeom<NTT, SU>;
+  __shared__ __attribute__((aligned(16))) uint8_t stage[KS][G::STAGE];
   __shared__ float red[KS - 1][MT][NTT][4][64];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c16 = lane & 15, q = lane >> 4;
-  const int64_t nb = (int64_t)blockIdx.x * ROWS;
-  const int64_t nst = a.K / (SU * U);
-  const int64_t s0 = wave * nst / KS, s1 = (wave + 1) * nst / KS;
-  const int64_t wpr = a.K / 8, gpr = a.K / 64;
-  uint8_t* wst = stage[wave];
-
-  // Coalesced weight loads: instruction i, lane L -> row i * (64 / LPR) + L / LPR,
-  // 16-byte chunk L % LPR of the row's step segment; rows past N re-read row N-1.
-  const uint32_t* wq[NI];
-  int wo[NI];
-#pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    const int r = i * (64 / LPR) + lane / LPR;
-    int64_t n = nb + r;
-    n = n < a.N ? n : a.N - 1;
-    wq[i] = a.w + n * wpr + (lane % LPR) * 4;
-    wo[i] = r * RB + (qmvs_pos<SU>(lane % LPR, r) << 4);
-  }
-  // B-fragment reads: tile t row 16 t + c16, unit j -> chunk 2 j + q / 2, 8-byte
-  // half q % 2.
-  int wr[NTT][SU];
-#pragma unroll
-  for (int t = 0; t < NTT; ++t)
-#pragma unroll
-    for (int j = 0; j < SU; ++j) {
-      const int r = 16 * t + c16;
-      wr[t][j] = r * RB + (qmvs_pos<SU>(2 * j + (q >> 1), r) << 4) + (q & 1) * 8;
-    }
-  // Scale loads: lane -> row l % ROWS, kind (l / ROWS) & 1 (0 scales, 1 biases)
-  // and, for 16-row blocks, which half of the step's groups (l / ROWS / 2).
-  const int sh = lane / ROWS;
-  int64_t nrow = nb + lane % ROWS;
-  nrow = nrow < a.N ? nrow : a.N - 1;
-  const uint16_t* sbrow =
-      ((sh & 1) ? a.biases : a.scales) + nrow * gpr + ((64 / ROWS == 2) ? 0 : (sh >> 1) * SPL);
+  const int64_t nb = (int64_t)blockIdx.x * G::ROWS;
+  const int64_t nst = a.K / (SU * 64);
   const uint16_t* xrow[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = 16 * mt + c16;
     xrow[mt] = a.x + (int64_t)(m < a.M ? m : (int)a.M - 1) * a.ldx + q * 16;
   }
-
-  u32x4 wbuf[2][NI];
-  sbv_t sbuf[2];
-  u32x4 xv[XD][MT][2];
-  auto load_w = [&](int d, int64_t st) {
-    st = st < s1 ? st : s1 - 1;  // past the slice: re-read the last step, unused
-#pragma unroll
-    for (int i = 0; i < NI; ++i)
-      wbuf[d][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wq[i] + st * SU * 8));
-    sbuf[d] = *reinterpret_cast<const sbv_t*>(sbrow + st * SU);
-  };
-  const int64_t u_end = s1 * SU;
-  auto load_x = [&](int d, int64_t u) {
-    u = u < u_end ? u : u_end - 1;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const u32x4* xs = reinterpret_cast<const u32x4*>(xrow[mt] + u * U);
-      xv[d][mt][0] = xs[0];
-      xv[d][mt][1] = xs[1];
-    }
-  };
-
-  f32x4 acc[MT][NTT];
+  f32x4 acc[1][MT][NTT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int t = 0; t < NTT; ++t) acc[mt][t] = f32x4{};
-  const bf16x8 ones = as_bf16x8(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
-
-  if (s1 > s0) {
-    load_w(0, s0);
-    load_w(1, s0 + 1);
-#pragma unroll
-    for (int d = 0; d < XD; ++d) load_x(d, s0 * SU + d);
-    for (int64_t st = s0; st < s1; st += 2) {
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int64_t stp = st + e;
-        if (stp < s1) {
-#pragma unroll
-          for (int i = 0; i < NI; ++i) *reinterpret_cast<u32x4*>(wst + wo[i]) = wbuf[e][i];
-          const sbv_t mine = sbuf[e];
-          load_w(e, stp + 2);
-          // Scale and bias pairs (groups 2p, 2p+1 of the step) of the wave's rows.
-          uint32_t sv[NTT][SU / 2], bv[NTT][SU / 2];
-#pragma unroll
-          for (int t = 0; t < NTT; ++t)
-#pragma unroll
-            for (int p = 0; p < SU / 2; ++p) {
-              const int row = 16 * t + c16;
-              const int hi = (64 / ROWS == 2) ? 0 : p / (SPL / 2);
-              const int idx = (64 / ROWS == 2) ? p : p % (SPL / 2);
-              sv[t][p] = (uint32_t)__shfl((int)mine[idx], (2 * hi) * ROWS + row, 64);
-              bv[t][p] = (uint32_t)__shfl((int)mine[idx], (2 * hi + 1) * ROWS + row, 64);
-            }
-#pragma unroll
-          for (int j = 0; j < SU; ++j) {
-            const int xd = (e * SU + j) % XD;
-            bf16x8 A[MT][2];
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-              A[mt][0] = xfrag4(xv[xd][mt][0]);
-              A[mt][1] = xfrag4(xv[xd][mt][1]);
-            }
-            load_x(xd, stp * SU + j + XD);
-            u32x2 wv[NTT];
-#pragma unroll
-            for (int t = 0; t < NTT; ++t) wv[t] = *reinterpret_cast<const u32x2*>(wst + wr[t][j]);
-            f32x4 xs[MT], P[MT][NTT];
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-              xs[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mt][0], ones, f32x4{}, 0, 0, 0);
-              xs[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mt][1], ones, xs[mt], 0, 0, 0);
-#pragma unroll
-              for (int t = 0; t < NTT; ++t) {
-                P[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mt][0], wfrag<4>(wv[t][0]),
-                                                                   f32x4{}, 0, 0, 0);
-                P[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mt][1], wfrag<4>(wv[t][1]),
-                                                                   P[mt][t], 0, 0, 0);
-              }
-            }
-#pragma unroll
-            for (int t = 0; t < NTT; ++t) {
-              const float s = (j & 1) ? bf16_hi(sv[t][j >> 1]) : bf16_lo(sv[t][j >> 1]);
-              const float b = (j & 1) ? bf16_hi(bv[t][j >> 1]) : bf16_lo(bv[t][j >> 1]);
-              const float bo = __builtin_fmaf(-128.f, s, b);
-#pragma unroll
-              for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                  acc[mt][t][r] = __builtin_fmaf(s, P[mt][t][r], __builtin_fmaf(bo, xs[mt][r], acc[mt][t][r]));
-            }
-          }
-        }
-      }
-    }
-  }
+    for (int t = 0; t < NTT; ++t) acc[0][mt][t] = f32x4{};
+  const uint32_t* const w[1] = {a.w};
+  const uint16_t* const sc[1] = {a.scales};
+  const uint16_t* const bi[1] = {a.biases};
+  qmvs_slice<MT, NTT, SU, 1>(stage[wave], w, sc, bi, nb, a.N, a.K, xrow, wave * nst / KS,
+                             (wave + 1) * nst / KS, acc);
 
   if (wave > 0) {
 #pragma unroll
@@ -399,7 +264,7 @@ __global__ __launch_bounds__(kQmvsKS * 64) void qmvs_kernel(QmmArgs a) {
 #pragma unroll
       for (int t = 0; t < NTT; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) red[wave - 1][mt][t][r][lane] = acc[mt][t][r];
+        for (int r = 0; r < 4; ++r) red[wave - 1][mt][t][r][lane] = acc[0][mt][t][r];
   }
   __syncthreads();
   if (wave > 0) return;
@@ -412,9 +277,9 @@ __global__ __launch_bounds__(kQmvsKS * 64) void qmvs_kernel(QmmArgs a) {
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        float v = acc[mt][t][r];
+        float v = acc[0][mt][t][r];
 #pragma unroll
-        for (int w = 0; w < KS - 1; ++w) v += red[w][mt][t][r][lane];
+        for (int k = 0; k < KS - 1; ++k) v += red[k][mt][t][r][lane];
         const int64_t m = 16 * mt + 4 * q + r;
         if (m < a.M && n < a.N) a.y[m * a.ldy + n] = finish_out(v, a.bias, n);
       }

@@ -144,3 +144,97 @@ def test_moe_combine_op_chain(gpu, oracle):
     want_g = r16(base + r16(sig[:, None] * oracle.bf16_to_f32(sh)))
     assert rel_err(oracle.bf16_to_f32(plain), base) <= 1e-2
     assert rel_err(oracle.bf16_to_f32(gated), want_g) <= 1e-2
+
+
+# --- the segmented grouped product (int4 group 64, D and I multiples of 256) ---
+
+@pytest.mark.parametrize("E,T,k", [
+    (64, 5, 4),     # 20 slots over 64 experts: 16-slot windows, mostly one slot per segment
+    (4, 40, 2),     # 80 slots over 4 experts: 32-slot windows, runs crossing windows
+    (1, 37, 1),     # one expert: every segment a full window but the last
+    (16, 64, 3),    # 192 slots, uniform
+])
+def test_switch_glu_segments(gpu, oracle, E, T, k):
+    """Sorted slots cut into expert segments, gate and up fused with silu * up, down
+    stored to each slot's own row: every slot equals the oracle's SwitchGLU row."""
+    rng = np.random.default_rng(E * 31 + T * 7 + k)
+    D, I = 256, 512
+    gate, up, down = _stack(rng, E, D, I)
+    x = make_x(rng, T, D)
+    inds = topk_uniform(rng, T, E, k)
+    announce(f"switch_glu segments E={E} T={T} k={k}")
+    got = _run(gpu, x, inds, gate, up, down)
+    ref = oracle.switch_glu(x, inds, gate, up, down)
+    assert rel_err(oracle.bf16_to_f32(got), oracle.bf16_to_f32(ref)) <= TOL
+
+
+def test_switch_glu_segments_hot_expert(gpu, oracle):
+    """Zipf routing: one expert takes a large share of the slots (runs of many
+    windows) while most experts get one or two."""
+    from synth import topk_zipf
+
+    rng = np.random.default_rng(77)
+    E, T, k, D, I = 32, 96, 4, 512, 256
+    gate, up, down = _stack(rng, E, D, I)
+    x = make_x(rng, T, D)
+    inds = topk_zipf(rng, T, E, k)
+    announce("switch_glu segments zipf")
+    got = _run(gpu, x, inds, gate, up, down)
+    ref = oracle.switch_glu(x, inds, gate, up, down)
+    assert rel_err(oracle.bf16_to_f32(got), oracle.bf16_to_f32(ref)) <= TOL
+
+
+def test_switch_glu_segments_bad_expert_id(gpu, oracle):
+    from fastmlx_amd import FmxqError, ops
+
+    rng = np.random.default_rng(13)
+    E, D, I = 6, 256, 256
+    gate, up, down = _stack(rng, E, D, I)
+    x = make_x(rng, 30, D)
+    inds = topk_uniform(rng, 30, E, 2)
+    inds[3, 0] = 6
+    inds[20, 1] = 1000
+    announce("switch_glu segments out-of-range ids")
+    got = _run(gpu, x, inds, gate, up, down)
+    assert np.all(got[3, 0] == 0) and np.all(got[20, 1] == 0)
+    with pytest.raises(FmxqError):
+        ops.device_error()
+    ok = np.ones(30, dtype=bool)
+    ok[[3, 20]] = False
+    safe = np.where(inds >= E, 0, inds)
+    ref = oracle.switch_glu(x, safe, gate, up, down, token_sel=np.nonzero(ok)[0])
+    assert rel_err(oracle.bf16_to_f32(got[ok]), oracle.bf16_to_f32(ref)) <= TOL
+    # the good slot of each bad token is unaffected
+    ref3 = oracle.switch_glu(x, safe, gate, up, down, token_sel=np.array([3, 20]))
+    assert rel_err(oracle.bf16_to_f32(got[3, 1]), oracle.bf16_to_f32(ref3[0, 1])) <= TOL
+    assert rel_err(oracle.bf16_to_f32(got[20, 0]), oracle.bf16_to_f32(ref3[1, 0])) <= TOL
+
+
+def test_gather_qmm_segments_unsorted_lhs_and_bad_rows(gpu, oracle):
+    """gather_qmm with one x row per item takes the sorted segment path whatever the
+    order of rhs: explicit lhs, unsorted ids, a bad id and a bad x row (both give a
+    zero row and a device error)."""
+    from fastmlx_amd import FmxqError, ops
+
+    rng = np.random.default_rng(23)
+    E, N, K, xb = 7, 200, 768, 11
+    w, s, b = make_quant(rng, (E, N), K, 4, 64)
+    x = make_x(rng, xb, 1, K)
+    S = 90
+    rhs = rng.integers(0, E, size=S).astype(np.uint32)
+    lhs = rng.integers(0, xb, size=S).astype(np.uint32)
+    rhs[17] = 9
+    lhs[40] = xb + 3
+    announce("gather_qmm segments, unsorted, lhs, bad id and row")
+    y = ops.gather_qmm(to_dev(x, gpu), to_dev(w, gpu), to_dev(s, gpu), to_dev(b, gpu),
+                       to_dev(rhs, gpu), to_dev(lhs, gpu), 1, True, 64, 4, False)
+    torch.cuda.synchronize()
+    got = to_np(y).reshape(S, N)
+    bad = np.zeros(S, dtype=bool)
+    bad[[17, 40]] = True
+    assert np.all(got[bad] == 0)
+    with pytest.raises(FmxqError):
+        ops.device_error()
+    ref = oracle.gather_qmm(x.reshape(xb, K), w, s, b, lhs[~bad].astype(np.int32),
+                            rhs[~bad].astype(np.int32))
+    assert rel_err(oracle.bf16_to_f32(got[~bad]), oracle.bf16_to_f32(ref)) <= TOL
