@@ -52,6 +52,8 @@ _A = FmxArray
 _S = FmxStream
 _Ap = ctypes.POINTER(FmxArray)
 _sz = ctypes.c_size_t
+_u64 = ctypes.c_uint64
+_cs = ctypes.c_char_p
 
 # the array-handle layer of include/fmx.h (mlx-c calling convention)
 FMX_SYMBOLS = {
@@ -84,6 +86,24 @@ FMX_SYMBOLS = {
     "fmx_route_softmax_topk": (_int, [_Ap, _Ap, _A, _int, _bool, _S]),
     "fmx_route_group_topk": (_int, [_Ap, _Ap, _A, _A, _int, _int, _int, ctypes.c_float, _bool,
                                     _S]),
+    # weight ingest
+    "fmx_safetensors_parse": (_int, [_p, _u64, ctypes.POINTER(_p)]),
+    "fmx_safetensors_free": (None, [_p]),
+    "fmx_safetensors_header_size": (_u64, [_p]),
+    "fmx_safetensors_data_start": (_u64, [_p]),
+    "fmx_safetensors_count": (_i64, [_p]),
+    "fmx_safetensors_tensor": (_int, [_p, _i64, ctypes.POINTER(_cs), ctypes.POINTER(_cs),
+                                      ctypes.POINTER(_int), ctypes.POINTER(ctypes.POINTER(_i64)),
+                                      ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
+    "fmx_safetensors_find": (_i64, [_p, _cs]),
+    "fmx_safetensors_metadata_count": (_i64, [_p]),
+    "fmx_safetensors_metadata": (_int, [_p, _i64, ctypes.POINTER(_cs), ctypes.POINTER(_cs)]),
+    "fmx_safetensors_dtype": (_int, [_cs, ctypes.POINTER(_int)]),
+    "fmx_safetensors_slice": (_int, [_u64, _u64, _u64, _u64, ctypes.POINTER(_u64)]),
+    "fmx_safetensors_load": (_int, [_Ap, _p, _u64, _p, _i64]),
+    "fmx_view": (_int, [_Ap, _A, _int, _S]),
+    "fmx_stack": (_int, [_Ap, ctypes.POINTER(_A), _sz, _int, _S]),
+    "fmx_scale_neg8": (_int, [_Ap, _A, _S]),
 }
 
 STATUS = {

@@ -253,7 +253,7 @@ struct Launch {
   std::vector<std::pair<void*, size_t>> temps;  // cached index buffers, returned after enqueue
 };
 
-int begin(Launch& L, const fmx_stream s, std::initializer_list<Array*> inputs) {
+int begin(Launch& L, const fmx_stream s, const std::vector<Array*>& inputs) {
   if (int rc = resolve_stream(s, &L.s)) return rc;
   if (int rc = hip_status(hipGetDevice(&L.dev), "fmx: hipGetDevice")) return rc;
   for (Array* a : inputs) {
@@ -1061,6 +1061,94 @@ int fmx_switch_glu(fmx_array* res, const fmx_array x, const fmx_array inds,
           static_cast<const uint16_t*>(Sd->data), static_cast<const uint16_t*>(Bd->data),
           static_cast<uint16_t*>(r->data), T, topk, E, D, I, group_size, bits, L.s);
   }
+  finish(L);
+  return commit(res, r, rc);
+}
+
+// ---- weight-ingest array ops (mlxgo View / Stack and the int4 bias of
+// deepseekv3.go remapInt4) ----
+
+// The bytes of a reinterpreted as dtype: the last axis scales by the ratio of
+// the element sizes (mlxgo.View as remapInt4 uses it, deepseekv3.go:513: packed
+// u8 [..., K/2] -> u32 [..., K/8]).  The result is a copy on stream s.
+int fmx_view(fmx_array* res, const fmx_array a, fmx_dtype dtype, const fmx_stream s) {
+  const char* op = "view";
+  if (!res) return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: null result", op);
+  Array* A;
+  if (int rc = need(a, op, "a", &A)) return rc;
+  const size_t from = dtype_size(A->dtype), to = dtype_size(dtype);
+  if (!to) return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: invalid dtype %d", op, (int)dtype);
+  std::vector<int64_t> shape = A->shape;
+  if (from != to) {
+    if (shape.empty())
+      return fail(FMXQ_ERR_SHAPE, "%s: a scalar of %s cannot be viewed as %s", op,
+                  dtype_name(A->dtype), dtype_name(dtype));
+    const int64_t bytes = shape.back() * (int64_t)from;
+    if (bytes % (int64_t)to)
+      return fail(FMXQ_ERR_SHAPE, "%s: last axis of %s (%lld bytes) is not a multiple of %s", op,
+                  shape_str(A->shape).c_str(), (long long)bytes, dtype_name(dtype));
+    shape.back() = bytes / (int64_t)to;
+  }
+  Launch L;
+  if (int rc = begin(L, s, {A})) return rc;
+  Array* r = nullptr;
+  if (int rc = new_result(L, shape, dtype, &r)) return rc;
+  int rc = FMXQ_OK;
+  if (r->nbytes())
+    rc = hip_status(hipMemcpyAsync(r->data, A->data, r->nbytes(), hipMemcpyDeviceToDevice, L.s),
+                    "view: copy");
+  finish(L);
+  return commit(res, r, rc);
+}
+
+// n arrays of one shape and dtype joined along a new leading axis (mlxgo.Stack
+// with axis 0, as stackExperts calls it, deepseekv3.go:564-592).
+int fmx_stack(fmx_array* res, const fmx_array* arrays, size_t n, int axis, const fmx_stream s) {
+  const char* op = "stack";
+  if (!res) return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: null result", op);
+  if (!arrays || n == 0) return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: no arrays", op);
+  if (axis != 0) return fail(FMXQ_ERR_UNSUPPORTED, "%s: only axis 0 is supported", op);
+  std::vector<Array*> parts(n);
+  for (size_t i = 0; i < n; ++i) {
+    if (int rc = need(arrays[i], op, "part", &parts[i])) return rc;
+    if (parts[i]->dtype != parts[0]->dtype || parts[i]->shape != parts[0]->shape)
+      return fail(FMXQ_ERR_SHAPE, "%s: part %zu is %s %s, part 0 is %s %s", op, i,
+                  dtype_name(parts[i]->dtype), shape_str(parts[i]->shape).c_str(),
+                  dtype_name(parts[0]->dtype), shape_str(parts[0]->shape).c_str());
+  }
+  std::vector<int64_t> shape = parts[0]->shape;
+  shape.insert(shape.begin(), (int64_t)n);
+  Launch L;
+  if (int rc = begin(L, s, parts)) return rc;
+  Array* r = nullptr;
+  if (int rc = new_result(L, shape, parts[0]->dtype, &r)) return rc;
+  const size_t each = parts[0]->nbytes();
+  int rc = FMXQ_OK;
+  for (size_t i = 0; i < n && !rc && each; ++i)
+    rc = hip_status(hipMemcpyAsync(static_cast<char*>(r->data) + i * each, parts[i]->data, each,
+                                   hipMemcpyDeviceToDevice, L.s),
+                    "stack: copy");
+  finish(L);
+  return commit(res, r, rc);
+}
+
+// -8 * scale in the scale's dtype (bf16, f16 or f32): the affine bias of an int4
+// checkpoint whose zero point is 8 (scaleNeg8, deepseekv3.go:539-551).
+int fmx_scale_neg8(fmx_array* res, const fmx_array scale, const fmx_stream s) {
+  const char* op = "scale_neg8";
+  if (!res) return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: null result", op);
+  Array* S;
+  if (int rc = need(scale, op, "scale", &S)) return rc;
+  const int kind = S->dtype == FMX_BFLOAT16 ? 0 : S->dtype == FMX_FLOAT16 ? 1
+                   : S->dtype == FMX_FLOAT32 ? 2 : -1;
+  if (kind < 0)
+    return fail(FMXQ_ERR_UNSUPPORTED, "%s: scale has dtype %s (bfloat16, float16 or float32)",
+                op, dtype_name(S->dtype));
+  Launch L;
+  if (int rc = begin(L, s, {S})) return rc;
+  Array* r = nullptr;
+  if (int rc = new_result(L, S->shape, S->dtype, &r)) return rc;
+  int rc = hip_status(fmxq::launch_scale_neg8(S->data, r->data, S->numel(), kind, L.s), op);
   finish(L);
   return commit(res, r, rc);
 }

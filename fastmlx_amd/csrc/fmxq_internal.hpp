@@ -132,6 +132,10 @@ struct RouteArgs {
 };
 hipError_t launch_route(const RouteArgs& a, bool group, hipStream_t stream);
 
+// Weight ingest (fmx_ingest.hip): dst = -8 * src elementwise in the source dtype
+// (kind 0 bf16, 1 f16, 2 f32).
+hipError_t launch_scale_neg8(const void* src, void* dst, int64_t n, int kind, hipStream_t stream);
+
 // Grouped int4 (group 64, K a multiple of 256) product over expert segments of
 // a sorted slot order (fmxq_moe_gemm.hip).  w/s/b hold NMAT stacks [E, N, .]
 // (gate and up for NMAT = 2, which writes silu(gate) * up); slot s reads x row

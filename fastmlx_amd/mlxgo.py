@@ -383,3 +383,21 @@ def moe_combine(y: Array, weights: Array, shared: Optional[Array] = None,
     """sum over top-k of y * weights (+ shared, sigmoid-gated when shared_gate)."""
     return _op(load().fmx_moe_combine, _ah(y), _ah(weights), _ah(shared), _ah(shared_gate),
                _sh(s))
+
+
+def view(a: Array, dtype: Dtype, s: Optional[Stream] = None) -> Array:
+    """View (as remapInt4 calls it, compute/models/deepseekv3.go:513): a's bytes as
+    dtype, the last axis scaled by the element-size ratio (a copy here)."""
+    return _op(load().fmx_view, _ah(a), int(Dtype(dtype)), _sh(s))
+
+
+def stack(parts: Sequence[Array], axis: int = 0, s: Optional[Stream] = None) -> Array:
+    """Stack along a new leading axis (stackExperts, deepseekv3.go:564-592)."""
+    hs = (FmxArray * max(len(parts), 1))(*[_ah(p) for p in parts])
+    return _op(load().fmx_stack, hs, len(parts), int(axis), _sh(s))
+
+
+def scale_neg8(scale: Array, s: Optional[Stream] = None) -> Array:
+    """-8 * scale in the scale's dtype: Mul by the float32 scalar then Astype back
+    (scaleNeg8, deepseekv3.go:539-551)."""
+    return _op(load().fmx_scale_neg8, _ah(scale), _sh(s))

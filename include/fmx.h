@@ -156,6 +156,53 @@ int fmx_route_group_topk(fmx_array* inds, fmx_array* weights, const fmx_array ga
                          const fmx_array bias, int top_k, int n_group, int topk_group,
                          float routed_scaling_factor, bool norm_topk_prob, const fmx_stream s);
 
+/* ---- weight ingest ---- */
+
+/* A parsed safetensors container header (compute/safetensors.go:101-165,
+ * ParseSafetensorsHeader): tensors in (begin, name) order with their dtype tag,
+ * shape and [begin, end) range in the data buffer, the optional __metadata__
+ * string map, the header length and the data start (8 + header length).
+ * Validation as the reference: known dtype, begin <= end, end within the data,
+ * end - begin = numel * dtype size.  Statuses: FMXQ_ERR_SHAPE for a buffer
+ * shorter than 8 bytes (ErrShortBuffer) or a declared header longer than the
+ * buffer (ErrHeaderTooLarge); FMXQ_ERR_INVALID_ARGUMENT for the rest. */
+typedef struct fmx_st_header_ fmx_st_header;
+int fmx_safetensors_parse(const uint8_t* blob, uint64_t len, fmx_st_header** out);
+void fmx_safetensors_free(fmx_st_header* h);
+uint64_t fmx_safetensors_header_size(const fmx_st_header* h);
+uint64_t fmx_safetensors_data_start(const fmx_st_header* h);
+int64_t fmx_safetensors_count(const fmx_st_header* h);
+/* Tensor i (SafetensorsHeader.Tensors[i]); pointers stay valid until free. */
+int fmx_safetensors_tensor(const fmx_st_header* h, int64_t i, const char** name,
+                           const char** dtype, int* ndim, const int64_t** shape,
+                           uint64_t* begin, uint64_t* end);
+/* Index of the named tensor or -1 (SafetensorsHeader.Tensor, safetensors.go:77-83). */
+int64_t fmx_safetensors_find(const fmx_st_header* h, const char* name);
+/* Entries of __metadata__, or -1 when the header has none (a nil map). */
+int64_t fmx_safetensors_metadata_count(const fmx_st_header* h);
+int fmx_safetensors_metadata(const fmx_st_header* h, int64_t i, const char** key,
+                             const char** value);
+/* The array dtype of a safetensors tag; the float8 tags have none
+ * (mlxgoDtype, compute/loader.go:13-42). */
+int fmx_safetensors_dtype(const char* tag, fmx_dtype* out);
+/* Offset in the blob of the data range [begin, end) after data_start,
+ * bounds-checked against the blob length (TensorBytes, compute/loader.go:47-55). */
+int fmx_safetensors_slice(uint64_t blob_len, uint64_t data_start, uint64_t begin,
+                          uint64_t end, uint64_t* offset);
+/* Upload tensor i's bytes unchanged into a new device array of its dtype
+ * (the per-tensor step of LoadTensors, compute/loader.go:61-84). */
+int fmx_safetensors_load(fmx_array* res, const uint8_t* blob, uint64_t len,
+                         const fmx_st_header* h, int64_t i);
+/* a's bytes as dtype, the last axis scaled by the element-size ratio (mlxgo.View
+ * as remapInt4 uses it, compute/models/deepseekv3.go:513). */
+int fmx_view(fmx_array* res, const fmx_array a, fmx_dtype dtype, const fmx_stream s);
+/* n arrays of one shape and dtype joined on a new axis; axis 0 only (mlxgo.Stack
+ * as stackExperts uses it, compute/models/deepseekv3.go:564-592). */
+int fmx_stack(fmx_array* res, const fmx_array* arrays, size_t n, int axis, const fmx_stream s);
+/* -8 * scale in the scale's dtype (bf16, f16, f32): the affine bias of an int4
+ * checkpoint (scaleNeg8, compute/models/deepseekv3.go:539-551). */
+int fmx_scale_neg8(fmx_array* res, const fmx_array scale, const fmx_stream s);
+
 #ifdef __cplusplus
 }
 #endif
