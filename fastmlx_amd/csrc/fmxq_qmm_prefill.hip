@@ -10,8 +10,8 @@
 //     lds (no VGPR staging), two steps ahead, into one of three x stages;
 //   - loads the packed weight tile two steps ahead into registers and, one step
 //     later, dequantizes it into one of two bf16 weight stages in LDS:
-//     w = bf16(s * q + b), for 4-bit one v_dot2_f32_bf16 per value on
-//     (128 + q, exponent trick) x (s, 0) plus (b - 128 s), products exact;
+//     w = bf16(s * q + b), for 4-bit one v_cvt_f32_ubyteN and one fma per value
+//     (the exact s*q + b rounded once to fp32);
 //   - runs its MFMAs from LDS in four k16 sub-steps, fragments read one
 //     sub-step ahead.
 // One barrier per step.  Before it each wave waits only for the loads issued one
@@ -42,18 +42,27 @@ __device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
   __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4))
 
 // One 4-bit word (values q0..q7, least significant first) -> bf16 pairs
-// (w0,w1) (w2,w3) (w4,w5) (w6,w7) of w = s*q + b.  p_i holds bf16(128 + q_i)
-// and bf16(128 + q_{i+4}); s_lo / s_hi are the pairs (s, 0) / (0, s) and
-// c = b - 128 s.
-__device__ __forceinline__ void dequant_word4(uint32_t w, uint32_t s_lo, uint32_t s_hi, float c,
-                                              uint32_t magic, uint32_t* out) {
-  constexpr uint32_t K = 0x000F000Fu;
-  const uint32_t p0 = (w & K) | magic, p1 = ((w >> 4) & K) | magic;
-  const uint32_t p2 = ((w >> 8) & K) | magic, p3 = ((w >> 12) & K) | magic;
-  out[0] = pack_bf16x2(dot2_bf16(p0, s_lo, c), dot2_bf16(p1, s_lo, c));
-  out[1] = pack_bf16x2(dot2_bf16(p2, s_lo, c), dot2_bf16(p3, s_lo, c));
-  out[2] = pack_bf16x2(dot2_bf16(p0, s_hi, c), dot2_bf16(p1, s_hi, c));
-  out[3] = pack_bf16x2(dot2_bf16(p2, s_hi, c), dot2_bf16(p3, s_hi, c));
+// (w0,w1) (w2,w3) (w4,w5) (w6,w7) of w = bf16(fma(s, q, b)): the exact s*q + b
+// rounded once to fp32, then to bf16.  The nibbles are split into two byte
+// vectors (q0 q2 q4 q6 and q1 q3 q5 q7) and converted with v_cvt_f32_ubyteN
+// (written out: the compiler turns the byte extracts into bfe + ubyte0);
+// each fma writes a fresh register, where v_dot2c (which accumulates into its
+// destination) would need a copy of the shared addend before every use.
+template <int K>
+__device__ __forceinline__ float ubyte_to_f32(uint32_t v) {
+  float f;
+  if constexpr (K == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f) : "v"(v));
+  else if constexpr (K == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(f) : "v"(v));
+  else if constexpr (K == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f) : "v"(v));
+  else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f) : "v"(v));
+  return f;
+}
+__device__ __forceinline__ void dequant_word4(uint32_t w, float s, float b, uint32_t* out) {
+  const uint32_t e = w & 0x0F0F0F0Fu, o = (w >> 4) & 0x0F0F0F0Fu;
+  out[0] = pack_bf16x2(__builtin_fmaf(s, ubyte_to_f32<0>(e), b), __builtin_fmaf(s, ubyte_to_f32<0>(o), b));
+  out[1] = pack_bf16x2(__builtin_fmaf(s, ubyte_to_f32<1>(e), b), __builtin_fmaf(s, ubyte_to_f32<1>(o), b));
+  out[2] = pack_bf16x2(__builtin_fmaf(s, ubyte_to_f32<2>(e), b), __builtin_fmaf(s, ubyte_to_f32<2>(o), b));
+  out[3] = pack_bf16x2(__builtin_fmaf(s, ubyte_to_f32<3>(e), b), __builtin_fmaf(s, ubyte_to_f32<3>(o), b));
 }
 // Two 8-bit words (values e0..e7) -> 4 bf16 pairs of w = s*q + b.
 __device__ __forceinline__ void dequant_words8(uint32_t w0, uint32_t w1, float s, float b,
@@ -170,14 +179,12 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void qmm_prefill_kernel(QmmArgs a)
   };
   // Dequantize chunk v of every unit of this thread into weight stage ws.
   auto store_chunk = [&](uint8_t* ws, const uvec* wq, const uint32_t* sq, const uint32_t* bq, int v) {
-    const uint32_t magic = vgpr_const(0x43004300u);
 #pragma unroll
     for (int i = 0; i < BU; ++i) {
       const int r = u_row[i];
       uint32_t d[4];
       if constexpr (BITS == 4) {
-        const float c = __builtin_fmaf(-128.f, bf16_bits_to_f32(sq[i]), bf16_bits_to_f32(bq[i]));
-        dequant_word4(wq[i][v], sq[i], sq[i] << 16, c, magic, d);
+        dequant_word4(wq[i][v], bf16_bits_to_f32(sq[i]), bf16_bits_to_f32(bq[i]), d);
       } else {
         dequant_words8(wq[i][2 * v], wq[i][2 * v + 1], bf16_bits_to_f32(sq[i]),
                        bf16_bits_to_f32(bq[i]), d);
