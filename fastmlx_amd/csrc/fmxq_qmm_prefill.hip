@@ -143,8 +143,16 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void qmm_prefill_kernel(QmmArgs a)
     aoff[j] = (uint32_t)((row * a.ldx + c * 8) * 2);
   }
 
-  const uint32_t* wrow[BU];
-  int64_t srow[BU];
+  // Weights, scales and biases through buffer resources: a thread's offset is
+  // fixed and each step adds one wave-uniform offset (no per-step 64-bit address
+  // arithmetic).  qmm_prefill_supported keeps every byte offset below 2^31.
+  const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)a.w, (short)0, (int)(a.N * wpr * 4), 0x00020000);
+  const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)a.scales, (short)0, (int)(a.N * gpr * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t bres = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)a.biases, (short)0, (int)(a.N * gpr * 2), 0x00020000);
+  uint32_t wvo[BU], svo[BU];
   int u_row[BU], u_idx[BU];
 #pragma unroll
   for (int i = 0; i < BU; ++i) {
@@ -153,8 +161,11 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void qmm_prefill_kernel(QmmArgs a)
     u_idx[i] = q % P::UPR;
     int64_t n = n0 + u_row[i];
     if (n > a.N - 1) n = a.N - 1;  // rows past N load row N-1; their outputs are not stored
-    wrow[i] = a.w + n * wpr + u_idx[i] * UW;
-    srow[i] = n * gpr;
+    wvo[i] = (uint32_t)((n * wpr + u_idx[i] * UW) * 4);
+    // Group of the unit: (64 kt + u_idx CHU) >> gshift.  A 64-deep step lies in one
+    // group when group_size >= 64; with group_size 32 the unit's half is fixed.
+    const int gadd = a.group_size == 32 ? (u_idx[i] * P::CHU) >> 5 : 0;
+    svo[i] = (uint32_t)((n * gpr + gadd) * 2);
   }
 
   typedef uint32_t uvec __attribute__((ext_vector_type(UW)));
@@ -168,13 +179,18 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void qmm_prefill_kernel(QmmArgs a)
   };
   auto load_w = [&](int kt, uvec* wq, uint32_t* sq, uint32_t* bq) {
     kt = kt < nk ? kt : nk - 1;
-    const int64_t k0 = (int64_t)kt * kStepK;
+    const int wso = kt * (kStepK * BITS / 8);          // bytes of packed words per step
+    const int sso = ((kt * kStepK) >> gshift) * 2;     // first group of the step
 #pragma unroll
     for (int i = 0; i < BU; ++i) {
-      wq[i] = __builtin_nontemporal_load(reinterpret_cast<const uvec*>(wrow[i] + k0 * BITS / 32));
-      const int64_t g = (k0 + u_idx[i] * P::CHU) >> gshift;
-      sq[i] = a.scales[srow[i] + g];
-      bq[i] = a.biases[srow[i] + g];
+      if constexpr (UW == 2)
+        wq[i] = __builtin_bit_cast(uvec, __builtin_amdgcn_raw_buffer_load_b64(wres, (int)wvo[i],
+                                                                              wso, 2 /* nt */));
+      else
+        wq[i] = __builtin_bit_cast(uvec, __builtin_amdgcn_raw_buffer_load_b128(wres, (int)wvo[i],
+                                                                               wso, 2 /* nt */));
+      sq[i] = __builtin_amdgcn_raw_buffer_load_b16(sres, (int)svo[i], sso, 0);
+      bq[i] = __builtin_amdgcn_raw_buffer_load_b16(bres, (int)svo[i], sso, 0);
     }
   };
   // Dequantize chunk v of every unit of this thread into weight stage ws.
@@ -368,8 +384,11 @@ bool qmm_prefill_supported(const QmmArgs& a) {
          (a.bits == 4 || a.bits == 8) && a.group_size >= 32 && a.splits == 1 &&
          (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
          (reinterpret_cast<uintptr_t>(a.w) & 15) == 0 &&
-         // the per-block x buffer resource counts bytes in 32 bits
-         256 * a.ldx * 2 < ((int64_t)1 << 31) && a.N < ((int64_t)1 << 31) / 256;
+         // the buffer resources (x per block; w, scales, biases whole) count bytes
+         // in 32 bits
+         256 * a.ldx * 2 < ((int64_t)1 << 31) && a.N < ((int64_t)1 << 31) / 256 &&
+         a.N * (a.K * a.bits / 8) < ((int64_t)1 << 31) &&
+         a.N * (a.K / a.group_size) * 2 < ((int64_t)1 << 31);
 }
 
 hipError_t launch_qmm_prefill(const QmmArgs& a, hipStream_t stream) {
