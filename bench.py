@@ -10,7 +10,7 @@ the 256 MB MALL cannot hold them); x ~ N(0,1) bf16.
 value = algorithmic HBM bytes of the step / measured step time (GB/s).
 Also reported, as extra fields: the same stack at M in {4, 8, 16, 32}, the
 north-star qmv points (4-bit 14336x4096 and 4096x14336 at M=1, rotating over
-distinct weight copies), the qmm points (4-bit, M=2048) and one MoE layer of
+distinct weight copies), the qmm points (4-bit, M=2048 and M=512) and one MoE layer of
 configs 3 and 4 (moe_c3_M*, moe_c4_M*).
 
 The CPU baseline times the oracle's OpenMP routine (oracle/, kind "port") on a
@@ -326,20 +326,21 @@ def main():
                 "timing": "HIP events over a graph of %d back-to-back launches on distinct "
                           "weight copies; per-launch = total / launches" % n_up}
 
-        # qmm point: M = 2048
-        for (N, K) in ((14336, 4096), (4096, 14336)):
-            w, s, b = stack[0]["gate" if N == 14336 else "down"]
-            x = torch.randn(2048, K, device=dev, generator=gen).to(torch.bfloat16)
-            y = torch.empty(2048, N, device=dev, dtype=torch.bfloat16)
+        # qmm points: M = 2048 (north star) and 512 (config 2)
+        for Mq in (2048, 512):
+            for (N, K) in ((14336, 4096), (4096, 14336)):
+                w, s, b = stack[0]["gate" if N == 14336 else "down"]
+                x = torch.randn(Mq, K, device=dev, generator=gen).to(torch.bfloat16)
+                y = torch.empty(Mq, N, device=dev, dtype=torch.bfloat16)
 
-            def fn():
-                for _ in range(5):
-                    ops.quantized_matmul(x, w, s, b, True, GROUP, bits, out=y)
-            g = capture(torch, fn)
-            per = time_graph(torch, g, 4, 1) / 5
-            tf = qmm_flops(2048, N, K) / (per * 1e-3) / 1e12
-            extra[f"qmm_{N}x{K}_M2048"] = {"us": round(per * 1e3, 2), "TFLOPs": round(tf, 1),
-                                           "frac_mfma": round(tf / BF16_MFMA_PEAK_TFLOPS, 4)}
+                def fn():
+                    for _ in range(5):
+                        ops.quantized_matmul(x, w, s, b, True, GROUP, bits, out=y)
+                g = capture(torch, fn)
+                per = time_graph(torch, g, 4, 1) / 5
+                tf = qmm_flops(Mq, N, K) / (per * 1e-3) / 1e12
+                extra[f"qmm_{N}x{K}_M{Mq}"] = {"us": round(per * 1e3, 2), "TFLOPs": round(tf, 1),
+                                               "frac_mfma": round(tf / BF16_MFMA_PEAK_TFLOPS, 4)}
 
         if not args.no_moe:
             extra.update(moe_points(torch, ops, gen, dev))

@@ -107,6 +107,8 @@ struct SplitWs {
   int64_t ws_floats = 0;
   uint32_t* counters = nullptr;
   int64_t n_counters = 0;
+  float* pf = nullptr;  // prefill K-split partials (overwritten by every call, no zero state)
+  int64_t pf_floats = 0;
 };
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, SplitWs> g_ws;
@@ -149,6 +151,49 @@ int split_workspace(hipStream_t s, const fmxq::QmmPlan& plan, float** ws, uint32
   }
   *ws = w.ws;
   *cnt = w.counters;
+  return FMXQ_OK;
+}
+
+int prefill_workspace(hipStream_t s, int64_t floats, float** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(FMXQ_ERR_DEVICE, "hipGetDevice failed");
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  SplitWs& w = g_ws[{dev, s}];
+  if (w.pf_floats < floats) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
+      return fail(FMXQ_ERR_INVALID_ARGUMENT,
+                  "quantized_matmul: prefill workspace must grow to %lld floats during graph "
+                  "capture; run the same shape once outside capture first",
+                  (long long)floats);
+    if (int rc = hip_status(hipStreamSynchronize(s), "prefill workspace: synchronize")) return rc;
+    float* p = nullptr;
+    if (int rc = hip_status(hipMalloc(&p, floats * sizeof(float)), "prefill workspace: hipMalloc"))
+      return rc;
+    if (w.pf) g_retired.push_back(w.pf);
+    w.pf = p;
+    w.pf_floats = floats;
+  }
+  *out = w.pf;
+  return FMXQ_OK;
+}
+
+// Compute units of the current device (blocks of the prefill GEMM resident at once).
+int device_cus(int* out) {
+  static std::mutex mu;
+  static std::map<int, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(FMXQ_ERR_DEVICE, "hipGetDevice failed");
+  std::lock_guard<std::mutex> lk(mu);
+  auto it = cache.find(dev);
+  if (it == cache.end()) {
+    int n = 0;
+    if (int rc = hip_status(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev),
+                            "hipDeviceGetAttribute"))
+      return rc;
+    it = cache.emplace(dev, n > 0 ? n : 1).first;
+  }
+  *out = it->second;
   return FMXQ_OK;
 }
 
@@ -231,7 +276,17 @@ int qmm_common(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
   if (fmxq::qmv_supported(a)) return hip_status(fmxq::launch_qmv(a, s), op);
   if (M <= fmxq::kSkinnyMaxM && fmxq::qmv_mfma_supported(a))
     return hip_status(fmxq::launch_qmv_mfma(a, s), op);
-  if (fmxq::qmm_prefill_supported(a)) return hip_status(fmxq::launch_qmm_prefill(a, s), op);
+  if (fmxq::qmm_prefill_supported(a)) {
+    int cus = 0;
+    if (int rc = device_cus(&cus)) return rc;
+    const fmxq::PrefillPlan pp = fmxq::qmm_prefill_plan(a, cus);
+    if (pp.splits > 1) {
+      if (int rc = prefill_workspace(s, pp.ws_floats, &a.ws)) return rc;
+      a.splits = pp.splits;
+      a.split_tail = pp.tail;
+    }
+    return hip_status(fmxq::launch_qmm_prefill(a, s), op);
+  }
   const fmxq::QmmPlan plan = fmxq::qmm_plan(M, N, K);
   if (plan.splits > 1) {
     if (int rc = split_workspace(s, plan, &a.ws, &a.tile_count)) return rc;

@@ -23,6 +23,10 @@ struct QmmArgs {
   float* ws = nullptr;
   uint32_t* tile_count = nullptr;
   int splits = 1;
+  // Prefill GEMM only: the last split_tail output tiles are computed in `splits`
+  // K ranges whose fp32 partials go to ws (no zero state) and are summed by a
+  // second kernel.
+  int64_t split_tail = 0;
 };
 
 // Gathered product over `batch` items of Mx rows:
@@ -96,6 +100,14 @@ hipError_t launch_qmm(const QmmArgs& a, hipStream_t stream);
 // x rows 16-byte aligned, 4- or 8-bit with group_size >= 32, no split-K.
 constexpr int64_t kPrefillMinM = 64;
 bool qmm_prefill_supported(const QmmArgs& a);
+// K split of the tiles of a part-full last wave on `cus` compute units (one block
+// per CU): splits 1 means none; otherwise ws_floats of workspace for split_tail.
+struct PrefillPlan {
+  int splits;
+  int64_t tail;
+  int64_t ws_floats;
+};
+PrefillPlan qmm_prefill_plan(const QmmArgs& a, int cus);
 hipError_t launch_qmm_prefill(const QmmArgs& a, hipStream_t stream);
 
 hipError_t launch_gather_qmv(const GatherArgs& a, hipStream_t stream);

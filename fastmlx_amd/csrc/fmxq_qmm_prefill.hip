@@ -115,19 +115,33 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void qmm_prefill_kernel(QmmArgs a)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
 
-  // Blocks are dealt to the 8 XCDs round robin; consecutive tiles (M fastest)
-  // go to one XCD so its resident blocks share weight rows through its L2.
+  // Block -> tile and K range.  Blocks [0, full) take whole tiles; they are dealt
+  // to the 8 XCDs round robin, so consecutive tiles (M fastest) go to one XCD and
+  // its resident blocks share weight rows through its L2.  With a.splits > 1 the
+  // last a.split_tail tiles are cut into a.splits K ranges, one block each, which
+  // write fp32 partials to a.ws for prefill_fixup_kernel (they are dispatched
+  // last, so a part-full last wave of whole tiles becomes a full wave of parts).
   const int nt_m = (int)((a.M + BM - 1) / BM);
-  const int nblk = gridDim.x;
-  int t = blockIdx.x;
-  if ((nblk & 7) == 0) t = (t & 7) * (nblk >> 3) + (t >> 3);
+  const int64_t tiles = (int64_t)nt_m * ((a.N + BN - 1) / BN);
+  const int64_t full = tiles - (a.splits > 1 ? a.split_tail : 0);
+  int64_t t = blockIdx.x;
+  int part = -1;
+  if (t < full) {
+    if ((full & 7) == 0) t = (t & 7) * (full >> 3) + (t >> 3);
+  } else {
+    const int64_t r = t - full;
+    t = full + r / a.splits;
+    part = (int)(r % a.splits);
+  }
   const int64_t m0 = (int64_t)(t % nt_m) * BM;
   const int64_t n0 = (int64_t)(t / nt_m) * BN;
 
   const int64_t wpr = a.K * BITS / 32;
   const int gshift = __builtin_ctz((unsigned)a.group_size);
   const int64_t gpr = a.K >> gshift;
-  const int nk = (int)(a.K / kStepK);
+  const int nk_all = (int)(a.K / kStepK);
+  const int kb = part < 0 ? 0 : (int)((int64_t)part * nk_all / a.splits);  // first step
+  const int nk = part < 0 ? nk_all : (int)((int64_t)(part + 1) * nk_all / a.splits) - kb;
 
   // x rows of this block through a buffer resource: rows past M read as zero.
   const int64_t rows_here = a.M - m0 < BM ? a.M - m0 : BM;
@@ -170,7 +184,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void qmm_prefill_kernel(QmmArgs a)
 
   typedef uint32_t uvec __attribute__((ext_vector_type(UW)));
   auto issue_x = [&](int kt, uint8_t* xs) {
-    kt = kt < nk ? kt : nk - 1;
+    kt = kb + (kt < nk ? kt : nk - 1);
     const int soff = kt * kStepK * 2;
 #pragma unroll
     for (int j = 0; j < AI; ++j)
@@ -178,7 +192,7 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void qmm_prefill_kernel(QmmArgs a)
                                                (int)aoff[j], soff, 0, 0);
   };
   auto load_w = [&](int kt, uvec* wq, uint32_t* sq, uint32_t* bq) {
-    kt = kt < nk ? kt : nk - 1;
+    kt = kb + (kt < nk ? kt : nk - 1);
     const int wso = kt * (kStepK * BITS / 8);          // bytes of packed words per step
     const int sso = ((kt * kStepK) >> gshift) * 2;     // first group of the step
 #pragma unroll
@@ -333,6 +347,25 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void qmm_prefill_kernel(QmmArgs a)
 #undef FMXQ_STEP
   mfmas(xf1, wf1);
 
+  if (part >= 0) {
+    // fp32 partial of this K range into slot ((t - full) * splits + part) of the
+    // workspace, BM x BN row-major; the fixup kernel sums the parts of a tile.
+    float* wsp = a.ws + ((t - full) * a.splits + part) * (int64_t)(BM * BN);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int r = wm * P::WTM + fr + 32 * i;
+          const int c = wn * P::WTN + j * 32 + 8 * g + 4 * fh;
+          *reinterpret_cast<f32x4*>(wsp + r * BN + c) =
+              f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                    acc[i][j][4 * g + 3]};
+        }
+    return;
+  }
+
   // Epilogue: bf16 (round to nearest even), then the optional additive bias as a
   // second bf16 add (the qlinear-then-add chain, compute/models/quant.go:105-111).
   const bool fast = ((a.ldy & 3) == 0) && ((reinterpret_cast<uintptr_t>(a.y) & 7) == 0);
@@ -370,18 +403,85 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void qmm_prefill_kernel(QmmArgs a)
   }
 }
 
+// Sums the a.splits fp32 partials of each split tile and stores it like the
+// main epilogue (bf16, then the optional bias add rounded again).  One thread per
+// 4 consecutive columns of a tile row.
+template <int BM, int BN>
+__global__ __launch_bounds__(256) void prefill_fixup_kernel(QmmArgs a) {
+  const int nt_m = (int)((a.M + BM - 1) / BM);
+  const int64_t tiles = (int64_t)nt_m * ((a.N + BN - 1) / BN);
+  const int64_t full = tiles - a.split_tail;
+  constexpr int Q = BM * BN / 4;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= a.split_tail * Q) return;
+  const int64_t tt = idx / Q;
+  const int e = (int)(idx % Q) * 4;
+  const int64_t t = full + tt;
+  const int64_t m = (t % nt_m) * BM + e / BN, n = (t / nt_m) * BN + e % BN;
+  if (m >= a.M || n >= a.N) return;
+  f32x4 v = {};
+  for (int sp = 0; sp < a.splits; ++sp)
+    v += *reinterpret_cast<const f32x4*>(a.ws + (tt * a.splits + sp) * (int64_t)(BM * BN) + e);
+  uint32_t p0 = pack_bf16x2(v[0], v[1]), p1 = pack_bf16x2(v[2], v[3]);
+  if (a.bias) {
+    float bv[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) bv[k] = n + k < a.N ? bf16_bits_to_f32(a.bias[n + k]) : 0.f;
+    p0 = pack_bf16x2(bf16_lo(p0) + bv[0], bf16_hi(p0) + bv[1]);
+    p1 = pack_bf16x2(bf16_lo(p1) + bv[2], bf16_hi(p1) + bv[3]);
+  }
+  uint16_t* dst = a.y + m * a.ldy + n;
+  const bool fast = ((a.ldy & 3) == 0) && ((reinterpret_cast<uintptr_t>(a.y) & 7) == 0);
+  if (fast && n + 3 < a.N) {
+    *reinterpret_cast<u32x2*>(dst) = u32x2{p0, p1};
+  } else {
+    const uint16_t w[4] = {(uint16_t)p0, (uint16_t)(p0 >> 16), (uint16_t)p1, (uint16_t)(p1 >> 16)};
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (n + k < a.N) dst[k] = w[k];
+  }
+}
+
 template <int BITS, int BM, int BN, int WM, int WN>
 hipError_t launch_tile(const QmmArgs& a, hipStream_t stream) {
   const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-  qmm_prefill_kernel<BITS, BM, BN, WM, WN><<<(unsigned)tiles, WM * WN * 64, 0, stream>>>(a);
+  const int64_t blocks = a.splits > 1 ? tiles + a.split_tail * (a.splits - 1) : tiles;
+  qmm_prefill_kernel<BITS, BM, BN, WM, WN><<<(unsigned)blocks, WM * WN * 64, 0, stream>>>(a);
+  if (a.splits > 1) {
+    const int64_t threads = a.split_tail * (BM * BN / 4);
+    prefill_fixup_kernel<BM, BN><<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(a);
+  }
   return hipGetLastError();
+}
+
+struct TileShape {
+  int bm, bn;
+};
+TileShape prefill_tile(const QmmArgs& a) {
+  if (a.bits == 8 || a.M > 128) return {256, 128};
+  return {128, 256};
 }
 
 }  // namespace
 
+PrefillPlan qmm_prefill_plan(const QmmArgs& a, int cus) {
+  const TileShape ts = prefill_tile(a);
+  const int64_t tiles = ((a.M + ts.bm - 1) / ts.bm) * ((a.N + ts.bn - 1) / ts.bn);
+  const int64_t nk = a.K / kStepK;
+  // Tiles of a part-full last wave (or all tiles, when they do not fill the chip
+  // once) are split along K while the parts still fill at most one wave and keep
+  // at least 8 steps each.
+  const int64_t tail = tiles < cus ? tiles : tiles % cus;
+  int splits = 1;
+  if (tail > 0 && tail * 2 <= cus)
+    while (splits < 8 && tail * splits * 2 <= cus && nk / (splits * 2) >= 8) splits *= 2;
+  if (splits == 1) return {1, 0, 0};
+  return {splits, tail, tail * splits * ts.bm * ts.bn};
+}
+
 bool qmm_prefill_supported(const QmmArgs& a) {
   return a.M > kPrefillMinM && a.K % kStepK == 0 && a.K > 0 && a.ldx % 8 == 0 &&
-         (a.bits == 4 || a.bits == 8) && a.group_size >= 32 && a.splits == 1 &&
+         (a.bits == 4 || a.bits == 8) && a.group_size >= 32 &&
          (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
          (reinterpret_cast<uintptr_t>(a.w) & 15) == 0 &&
          // the buffer resources (x per block; w, scales, biases whole) count bytes
@@ -393,9 +493,11 @@ bool qmm_prefill_supported(const QmmArgs& a) {
 
 hipError_t launch_qmm_prefill(const QmmArgs& a, hipStream_t stream) {
   if (!qmm_prefill_supported(a)) return hipErrorInvalidValue;
+  if (a.splits > 1 && (!a.ws || a.split_tail < 1 || a.splits > 8)) return hipErrorInvalidValue;
   // 128 x 256 tiles for M <= 128 (4-bit; the 8-bit form of that tile spills).
+  const TileShape ts = prefill_tile(a);
   if (a.bits == 8) return launch_tile<8, 256, 128, 4, 2>(a, stream);
-  if (a.M > 128) return launch_tile<4, 256, 128, 4, 2>(a, stream);
+  if (ts.bm == 256) return launch_tile<4, 256, 128, 4, 2>(a, stream);
   return launch_tile<4, 128, 256, 2, 4>(a, stream);
 }
 

@@ -138,6 +138,24 @@ def test_qmm_prefill_tiles(gpu, oracle, M, N, K, bits, group):
     _qmm_case(gpu, oracle, M, N, K, bits, group, seed=7000 + M + N + K + bits + group)
 
 
+@pytest.mark.parametrize("M,N,K,bits,group,bias", [
+    (300, 512, 2048, 4, 64, True),     # 8 tiles -> 4 K parts each (fixup adds the bias)
+    (130, 700, 4096, 8, 32, False),    # 8-bit, group 32, ragged M and N, parts only
+    (1000, 2048, 8192, 4, 128, False), # 64 tiles x 4 parts
+    (512, 16640, 1024, 4, 64, True),   # 260 tiles: 256 whole, the last 4 in 2 parts each
+])
+def test_qmm_prefill_k_split(gpu, oracle, M, N, K, bits, group, bias):
+    """Prefill tiles of a part-full last wave are computed in K parts summed by a
+    fixup kernel; whole and split tiles must both match the oracle, twice in a row
+    (the partial workspace is overwritten, never accumulated)."""
+    rows = None if M <= 130 else np.unique(np.concatenate([[0, M - 1], np.arange(0, M, 37)]))
+    e1 = _qmm_case(gpu, oracle, M, N, K, bits, group, seed=8800 + M + K + bits, rows_checked=rows,
+                   bias=bias)
+    e2 = _qmm_case(gpu, oracle, M, N, K, bits, group, seed=8800 + M + K + bits, rows_checked=rows,
+                   bias=bias)
+    assert e1 == e2
+
+
 @pytest.mark.parametrize("M", [5, 7, 8, 9, 13, 16, 17, 24, 25, 31, 32])
 @pytest.mark.parametrize("bits,group,K", [(4, 64, 192), (4, 128, 1024), (8, 32, 96),
                                           (8, 64, 2048)])
