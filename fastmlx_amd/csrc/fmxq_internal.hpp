@@ -98,7 +98,7 @@ hipError_t launch_qmm(const QmmArgs& a, hipStream_t stream);
 
 // Prefill GEMM for M > kPrefillMinM (fmxq_qmm_prefill.hip): K a multiple of 64,
 // x rows 16-byte aligned, 4- or 8-bit with group_size >= 32, no split-K.
-constexpr int64_t kPrefillMinM = 64;
+constexpr int64_t kPrefillMinM = 32;
 bool qmm_prefill_supported(const QmmArgs& a);
 // K split of the tiles of a part-full last wave on `cus` compute units (one block
 // per CU): splits 1 means none; otherwise ws_floats of workspace for split_tail.

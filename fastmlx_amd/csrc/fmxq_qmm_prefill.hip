@@ -1,4 +1,4 @@
-// fmxq_qmm_prefill.hip -- MFMA GEMM for quantized_matmul at prefill sizes (M > 64).
+// fmxq_qmm_prefill.hip -- MFMA GEMM for quantized_matmul at verify and prefill sizes (M > 32).
 //
 // Replaces the GEMM side of mlx_quantized_matmul (mlxgo/binding_cgo.go:636-643)
 // for x [M, K] with M = batch * seq rows (prefill at batch_generator.go:258).

@@ -131,9 +131,11 @@ def test_qmm_ragged_n(gpu, oracle):
     (100, 384, 1024, 8, 32),     # 8-bit at M <= 128 takes the 256x128 tile
     (512, 128, 2048, 8, 128),
     (1000, 2048, 768, 4, 64),
+    (33, 1000, 1024, 4, 64),     # the smallest M on this kernel
+    (64, 520, 3072, 8, 128),
 ])
 def test_qmm_prefill_tiles(gpu, oracle, M, N, K, bits, group):
-    """The M > 64 prefill GEMM: every step-count remainder of its six-step loop,
+    """The M > 32 prefill GEMM: every step-count remainder of its six-step loop,
     both tiles, ragged M and N, both bit widths and every group size."""
     _qmm_case(gpu, oracle, M, N, K, bits, group, seed=7000 + M + N + K + bits + group)
 
