@@ -305,6 +305,148 @@ static hipError_t launch_qmv1(const QmmArgs& a, hipStream_t stream) {
   return hipErrorNotSupported;
 }
 
+// ---------------------------------------------------------------------------
+// Decode GEMV for one x row, int4 group 64, K a multiple of 2048: a wave owns a
+// 64-chunk (2048-value) K slice of RW rows, lane l chunk l of the slice.  All RW
+// weight loads of a wave are in flight at once, and the lane's x chunk serves all
+// RW rows.  Loads are issued x, scales and biases, then weights, so the x pairs
+// and the scale/bias table are built while the weights are on their way:
+//   - scales and biases of the wave's rows come as 16-byte pieces (lane L -> row
+//     L / 4, groups 8 (L % 4) .. +7 of the slice), are interleaved into
+//     (scale | bias << 16) words and written to a wave-private LDS table
+//     [RW][32 groups], from which lane l reads group l / 2 of each row;
+//   - a block is RG row groups x KS slices; the slices meet in LDS.
+// Arithmetic as in qmv1_kernel.
+template <int RW, int KS, int RG>
+__global__ __launch_bounds__(KS * RG * 64) void qmv1_slice_kernel(QmmArgs a) {
+  constexpr int NP = (RW * 4 + 63) / 64;  // piece loads per lane (scales and biases each)
+  constexpr int LV = __builtin_ctz(RW);
+  __shared__ float part[RG][KS][RW];
+  __shared__ __attribute__((aligned(16))) uint32_t sbl[KS * RG][RW][32];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rg = wave / KS, ks = wave % KS;
+  const int c = ks * 64 + lane;
+  const int64_t wpr = a.K / 8, gpr = a.K / 64;
+  const int64_t nbase = ((int64_t)blockIdx.x * RG + rg) * RW;
+  u32x4 xr[4];
+  {
+    const u32x4* xs = reinterpret_cast<const u32x4*>(a.x + (int64_t)c * 32);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xr[j] = xs[j];
+  }
+  u32x4 ps[NP], pb[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int L = lane + 64 * p;
+    const int r = L >> 2, pc = L & 3;
+    int64_t n = nbase + (r < RW ? r : 0);
+    n = n < a.N ? n : a.N - 1;
+    const int64_t off = n * gpr + ks * 32 + pc * 8;
+    ps[p] = *reinterpret_cast<const u32x4*>(a.scales + off);
+    pb[p] = *reinterpret_cast<const u32x4*>(a.biases + off);
+  }
+  // Keep the weight loads behind x and the pieces: the wait for those then does
+  // not hold on the weights.
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 wv[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    int64_t n = nbase + r;
+    n = n < a.N ? n : a.N - 1;  // rows past N load row N-1; their outputs are not stored
+    wv[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.w + n * wpr) + c);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  XChunk<4> xc;
+  {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      x_pairs_q4(xr[j], xc.p + 4 * j);
+      s = dot2_bf16(xr[j][0], kOnes, s);
+      s = dot2_bf16(xr[j][1], kOnes, s);
+      s = dot2_bf16(xr[j][2], kOnes, s);
+      s = dot2_bf16(xr[j][3], kOnes, s);
+    }
+    xc.sum = s;
+  }
+  // The table is written and read by this wave only: LDS operations of one wave
+  // complete in order, so no barrier is needed.
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int L = lane + 64 * p;
+    const int r = L >> 2, pc = L & 3;
+    if (r < RW) {
+      u32x4 o0, o1;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        o0[2 * h] = __builtin_amdgcn_perm(pb[p][h], ps[p][h], 0x05040100u);
+        o0[2 * h + 1] = __builtin_amdgcn_perm(pb[p][h], ps[p][h], 0x07060302u);
+        o1[2 * h] = __builtin_amdgcn_perm(pb[p][2 + h], ps[p][2 + h], 0x05040100u);
+        o1[2 * h + 1] = __builtin_amdgcn_perm(pb[p][2 + h], ps[p][2 + h], 0x07060302u);
+      }
+      *reinterpret_cast<u32x4*>(&sbl[wave][r][pc * 8]) = o0;
+      *reinterpret_cast<u32x4*>(&sbl[wave][r][pc * 8 + 4]) = o1;
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const int gl = lane >> 1;
+  float res[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const uint32_t sb = sbl[wave][r][gl];
+    const float s = bf16_lo(sb);
+    const float bo = __builtin_fmaf(-magic_offset<4>(), s, bf16_hi(sb));
+    res[r] = __builtin_fmaf(s, chunk_dot<4>(wv[r], xc), bo * xc.sum);
+  }
+  const float tot = wave_sum_multi<RW>(res, lane);
+  const int idx = lane >> (6 - LV);
+  const bool writer = (lane & ((64 >> LV) - 1)) == 0;
+  const int64_t n = nbase + idx;
+  if constexpr (KS > 1) {
+    if (writer) part[rg][ks][idx] = tot;
+    __syncthreads();
+    if (ks == 0 && writer) {
+      float v = 0.f;
+#pragma unroll
+      for (int k = 0; k < KS; ++k) v += part[rg][k][idx];
+      if (n < a.N) a.y[n] = finish_out(v, a.bias, n);
+    }
+  } else {
+    if (writer && n < a.N) a.y[n] = finish_out(tot, a.bias, n);
+  }
+}
+
+template <int RW, int KS, int RG>
+static hipError_t launch_qmv1_slice_cfg(const QmmArgs& a, hipStream_t stream) {
+  constexpr int64_t rows = RW * RG;
+  qmv1_slice_kernel<RW, KS, RG><<<(unsigned)((a.N + rows - 1) / rows), KS * RG * 64, 0, stream>>>(a);
+  return hipGetLastError();
+}
+
+// Shapes where the slice kernel beats qmv1_kernel (graphs of launches over
+// distinct weight copies): 14336-deep rows (8.2 -> 7.7 us for 4096 x 14336) and
+// K = 4096 with N <= 4096 (4.2 -> 3.9 us for 4096 x 4096).  The 14336-row,
+// 4096-deep projections stay on qmv1_kernel (equal times).
+static hipError_t launch_qmv1_slice(const QmmArgs& a, hipStream_t stream) {
+  if (a.M != 1 || a.bits != 4 || a.group_size != 64 || a.K % 2048 != 0) return hipErrorNotSupported;
+  if ((reinterpret_cast<uintptr_t>(a.scales) & 15u) || (reinterpret_cast<uintptr_t>(a.biases) & 15u) ||
+      (reinterpret_cast<uintptr_t>(a.x) & 15u) || (reinterpret_cast<uintptr_t>(a.w) & 15u))
+    return hipErrorNotSupported;
+  switch (a.K / 2048) {
+    case 4: return launch_qmv1_slice_cfg<8, 4, 1>(a, stream);
+    case 5: return launch_qmv1_slice_cfg<8, 5, 1>(a, stream);
+    case 6: return launch_qmv1_slice_cfg<8, 6, 1>(a, stream);
+    case 7: return launch_qmv1_slice_cfg<8, 7, 1>(a, stream);
+    case 8: return launch_qmv1_slice_cfg<8, 8, 1>(a, stream);
+    case 2:
+      if (a.N > 4096) return hipErrorNotSupported;
+      return a.N >= 2048 ? launch_qmv1_slice_cfg<8, 2, 2>(a, stream)
+                         : launch_qmv1_slice_cfg<2, 2, 2>(a, stream);
+    default: return hipErrorNotSupported;
+  }
+}
+
 struct QmvxShape {
   int ks, cpl, rpw, waves;
   int r = 2;  // rows per load group (all rpw rows at once when r == rpw)
@@ -535,6 +677,8 @@ bool qmv_supported(const QmmArgs& a) {
 
 hipError_t launch_qmv(const QmmArgs& a, hipStream_t stream) {
   if (a.M <= 0 || a.N <= 0) return hipSuccess;
+  const hipError_t e0 = launch_qmv1_slice(a, stream);
+  if (e0 != hipErrorNotSupported) return e0;
   const hipError_t e1 = launch_qmv1(a, stream);
   if (e1 != hipErrorNotSupported) return e1;
   if (qmvx_supported(a, a.bits))

@@ -181,6 +181,20 @@ def test_qmvs_blocks_and_steps(gpu, oracle, M, N, K):
     _qmm_case(gpu, oracle, M, N, K, 4, 64, seed=9100 + M * 7 + N + K)
 
 
+@pytest.mark.parametrize("N,K,bias", [
+    (1001, 8192, False),   # four 2048-deep slices, rows not a multiple of the 8-row wave
+    (77, 16384, True),     # eight slices (the largest block), bias epilogue
+    (77, 32768, False),    # sixteen slices: not taken by the slice kernel
+    (264, 14336, False),   # the down-projection depth
+    (2056, 4096, True),    # two slices x two 8-row groups per block, ragged
+    (1001, 4096, False),   # two slices x two 2-row groups per block
+    (520, 6144, False),    # three slices: not taken by the slice kernel
+])
+def test_qmv1_slice_shapes(gpu, oracle, N, K, bias):
+    """M = 1 GEMV over 2048-deep K slices (qmv1_slice_kernel) and its neighbours."""
+    _qmm_case(gpu, oracle, 1, N, K, 4, 64, seed=9300 + N + K, bias=bias)
+
+
 def test_qmvs_bias(gpu, oracle):
     _qmm_case(gpu, oracle, 12, 8256, 512, 4, 64, seed=9201, bias=True)
     _qmm_case(gpu, oracle, 30, 2080, 1024, 4, 64, seed=9202, bias=True)
