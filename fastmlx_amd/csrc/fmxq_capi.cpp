@@ -391,6 +391,13 @@ int fmxq_gather_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* scales
       aligned16(scales) && aligned16(biases)) {
     // Items sorted by expert, then one grouped product per expert segment; the
     // sort's order maps each sorted item back to its output row.
+    if (batch <= fmxq::kMoeUnsortedMaxSlots) {
+      // A few items: each is its own segment, written to its own output row.
+      fmxq::MoeArgs a{x, lhs_indices, {w, nullptr}, {scales, nullptr}, {biases, nullptr},
+                      rhs_indices, nullptr, nullptr, y, nullptr, batch, N, K, E, x_batch, flag,
+                      lhs_div};
+      return hip_status(fmxq::launch_moe_qmvs(a, 1, 16, batch, s), op);
+    }
     const int window = fmxq::moe_window(batch, E);
     const int64_t max_seg = fmxq::moe_max_segments(batch, E, window);
     if (max_seg <= kMaxSegmentsGrid) {
@@ -478,8 +485,19 @@ extern "C" int fmxq_switch_glu(const uint16_t* x, const uint32_t* inds, const ui
       aligned16(b_down)) {
     // Sorted slots (for every slot count: the order cannot change a value, each
     // slot being its own product row), then gate and up fused with silu * up into
-    // h in sorted order, then down written to each slot's own output row.
+    // h in sorted order, then down written to each slot's own output row.  A few
+    // slots skip the sort: each is its own segment, h stays in slot order.
     MoeScratch m;
+    if (S <= fmxq::kMoeUnsortedMaxSlots) {
+      if (int rc = moe_scratch(s, S, I, 1, &m, op)) return rc;
+      fmxq::MoeArgs gu{x, nullptr, {w_gate, w_up}, {s_gate, s_up}, {b_gate, b_up}, inds, nullptr,
+                       nullptr, m.h, nullptr, S, I, D, E, T, flag, topk};
+      if (int rc = hip_status(fmxq::launch_moe_qmvs(gu, 2, 16, S, s), "switch_glu: gate/up"))
+        return rc;
+      fmxq::MoeArgs dn{m.h, nullptr, {w_down, nullptr}, {s_down, nullptr}, {b_down, nullptr},
+                       inds, nullptr, nullptr, out, nullptr, S, D, I, E, S, flag, 1};
+      return hip_status(fmxq::launch_moe_qmvs(dn, 1, 16, S, s), "switch_glu: down");
+    }
     if (int rc = moe_scratch(s, S, I, max_seg, &m, op)) return rc;
     if (int rc = hip_status(fmxq::launch_sort_slots(inds, S, topk, E, m.order, m.rhs, m.lhs, s,
                                                     nullptr, m.seg, m.nseg, window),

@@ -158,14 +158,18 @@ struct MoeArgs {
   const uint32_t* w[2];
   const uint16_t* s[2];
   const uint16_t* b[2];
-  const uint32_t* rhs;      // [S] expert of each slot, sorted
-  const uint32_t* seg;      // (start, len) pairs
-  const uint32_t* nseg;     // segment count (device)
+  const uint32_t* rhs;      // [S] expert of each slot (sorted when seg is set)
+  const uint32_t* seg;      // (start, len) pairs, or null: segment i is slot i alone
+  const uint32_t* nseg;     // segment count (device); S when seg is null
   uint16_t* y;              // [rows, N]
   const uint32_t* yrow;     // [S] or null
   int64_t S, N, K, E, x_rows;
   uint32_t* err_flag;
+  int64_t lhs_div = 1;      // x row of slot s is lhs[s], or s / lhs_div without lhs
 };
+// Slot counts up to which the MoE products skip the sort: every slot is its own
+// segment (a sort saves weight reads only when slots share an expert).
+constexpr int64_t kMoeUnsortedMaxSlots = 16;
 bool moe_qmvs_supported(int64_t N, int64_t K, int bits, int group_size);
 int moe_window(int64_t S, int64_t E);
 int64_t moe_max_segments(int64_t S, int64_t E, int window);

@@ -151,11 +151,25 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
        i += (int64_t)gridDim.x * 256) {
     const int64_t t = i / pairs, d = (i - t * pairs) * 2;
     float a0 = 0.f, a1 = 0.f;
-    for (int64_t j = 0; j < topk; ++j) {
-      const float wj = bf16_bits_to_f32(w[t * topk + j]);
-      const uint32_t v = *reinterpret_cast<const uint32_t*>(y + (t * topk + j) * D + d);
-      a0 += r16(bf16_lo(v) * wj);
-      a1 += r16(bf16_hi(v) * wj);
+    // Up to 16 expert rows are requested before any is summed (the sum still runs
+    // in j order).
+    for (int64_t j0 = 0; j0 < topk; j0 += 16) {
+      uint32_t v[16];
+      uint16_t wb[16];
+#pragma unroll
+      for (int jj = 0; jj < 16; ++jj) {
+        const int64_t j = j0 + jj < topk ? j0 + jj : topk - 1;
+        v[jj] = *reinterpret_cast<const uint32_t*>(y + (t * topk + j) * D + d);
+        wb[jj] = w[t * topk + j];
+      }
+#pragma unroll
+      for (int jj = 0; jj < 16; ++jj) {
+        if (j0 + jj < topk) {
+          const float wj = bf16_bits_to_f32(wb[jj]);
+          a0 += r16(bf16_lo(v[jj]) * wj);
+          a1 += r16(bf16_hi(v[jj]) * wj);
+        }
+      }
     }
     a0 = r16(a0);
     a1 = r16(a1);

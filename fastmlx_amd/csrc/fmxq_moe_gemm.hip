@@ -20,6 +20,9 @@
 // rounded, times u rounded.  NMAT = 1 writes bf16(acc) to output row yrow[slot]
 // (the unsort of switch_glu.go:150-152) or to row slot.
 //
+// Without a segment table (a.seg null, few slots) segment i is slot i alone, in
+// the caller's slot order.
+//
 // A slot whose expert id is >= E or whose x row is >= x_rows gets a zero output
 // row and raises err_flag.
 #include "fmxq_common.hpp"
@@ -40,12 +43,13 @@ __global__ __launch_bounds__(256) void moe_qmvs_kernel(MoeArgs a) {
   __shared__ float red[KS > 1 ? KS - 1 : 1][WC][NMAT][MT][NTT][4][64];
 
   const int64_t sg = blockIdx.y;
-  if (sg >= (int64_t)*a.nseg) return;
+  if (sg >= (a.seg ? (int64_t)*a.nseg : a.S)) return;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wc = wave % WC, ks = wave / WC;
   const int c16 = lane & 15, q = lane >> 4;
-  const int64_t start = a.seg[2 * sg], len = a.seg[2 * sg + 1];
+  const int64_t start = a.seg ? (int64_t)a.seg[2 * sg] : sg;
+  const int64_t len = a.seg ? (int64_t)a.seg[2 * sg + 1] : 1;
   const uint32_t e = a.rhs[start];
   const int64_t nb = (int64_t)blockIdx.x * (16 * NTT * WC) + wc * (16 * NTT);
   const bool bad_e = (int64_t)e >= a.E;
@@ -57,7 +61,7 @@ __global__ __launch_bounds__(256) void moe_qmvs_kernel(MoeArgs a) {
   for (int mt = 0; mt < MT; ++mt) {
     const int m = 16 * mt + c16;
     const int64_t slot = start + (m < len ? m : 0);
-    int64_t xr = a.lhs ? (int64_t)a.lhs[slot] : slot;
+    int64_t xr = a.lhs ? (int64_t)a.lhs[slot] : slot / a.lhs_div;
     if (xr >= a.x_rows) xr = 0;
     xrow[mt] = a.x + xr * a.K + q * 16;
   }
@@ -136,7 +140,7 @@ __global__ __launch_bounds__(256) void moe_qmvs_kernel(MoeArgs a) {
       const int m = 16 * mt + 4 * q + r;
       if (m >= len) continue;
       const int64_t slot = start + m;
-      const int64_t xr = a.lhs ? (int64_t)a.lhs[slot] : slot;
+      const int64_t xr = a.lhs ? (int64_t)a.lhs[slot] : slot / a.lhs_div;
       const bool bad = bad_e || xr >= a.x_rows;
       raise |= bad;
       const int64_t orow = a.yrow ? (int64_t)a.yrow[slot] : slot;
@@ -192,13 +196,27 @@ hipError_t launch_moe_qmvs(const MoeArgs& a, int nmat, int window, int64_t max_s
       (nmat != 1 && nmat != 2))
     return hipErrorInvalidValue;
   // K slices per block: about four 4-unit steps per wave, at most 4 slices; the
-  // remaining waves of the block take further column groups.
+  // remaining waves of the block take further column groups.  With few segments
+  // (decode) the column tiles narrow (one 16-column tile per wave, then more K
+  // slices while every slice keeps a step) until the grid has about two blocks
+  // per CU.
   const int64_t nst = a.K / 256;
-  const int ks = nst >= 16 ? 4 : (nst >= 8 ? 2 : 1);
+  int ks = nst >= 16 ? 4 : (nst >= 8 ? 2 : 1);
+  int ntt = nmat == 2 ? 1 : 2;
+  auto blocks = [&](int ks_, int ntt_) {
+    const int64_t cols = 16 * ntt_ * (4 / ks_);
+    return (a.N + cols - 1) / cols * max_seg;
+  };
+  constexpr int64_t kMinBlocks = 512;
+  if (blocks(ks, ntt) < kMinBlocks) ntt = 1;
+  while (blocks(ks, ntt) < kMinBlocks && ks < 4 && 2 * ks <= nst) ks *= 2;
   const int wc = 4 / ks;
   if (nmat == 2)
     return window == 16 ? launch_wc<1, 1, 2>(a, wc, max_seg, stream)
                         : launch_wc<2, 1, 2>(a, wc, max_seg, stream);
+  if (ntt == 1)
+    return window == 16 ? launch_wc<1, 1, 1>(a, wc, max_seg, stream)
+                        : launch_wc<2, 1, 1>(a, wc, max_seg, stream);
   return window == 16 ? launch_wc<1, 2, 1>(a, wc, max_seg, stream)
                       : launch_wc<2, 2, 1>(a, wc, max_seg, stream);
 }

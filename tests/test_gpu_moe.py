@@ -238,3 +238,81 @@ def test_gather_qmm_segments_unsorted_lhs_and_bad_rows(gpu, oracle):
     ref = oracle.gather_qmm(x.reshape(xb, K), w, s, b, lhs[~bad].astype(np.int32),
                             rhs[~bad].astype(np.int32))
     assert rel_err(oracle.bf16_to_f32(got[~bad]), oracle.bf16_to_f32(ref)) <= TOL
+
+
+# --- few slots: no sort, every slot its own segment ---
+
+@pytest.mark.parametrize("E,T,k", [
+    (64, 1, 10),    # one decode token (configuration 3's top-10)
+    (8, 2, 8),      # 16 slots, every expert twice
+    (3, 5, 3),      # 15 slots over 3 experts: repeated experts in slot order
+    (5, 17, 1),     # 17 slots: the sorted path, just past the limit
+])
+def test_switch_glu_few_slots(gpu, oracle, E, T, k):
+    rng = np.random.default_rng(E * 13 + T * 5 + k)
+    D, I = 256, 512
+    gate, up, down = _stack(rng, E, D, I)
+    x = make_x(rng, T, D)
+    inds = topk_uniform(rng, T, E, k)
+    announce(f"switch_glu few slots E={E} T={T} k={k}")
+    got = _run(gpu, x, inds, gate, up, down)
+    ref = oracle.switch_glu(x, inds, gate, up, down)
+    assert rel_err(oracle.bf16_to_f32(got), oracle.bf16_to_f32(ref)) <= TOL
+
+
+def test_switch_glu_few_slots_bad_expert_id(gpu, oracle):
+    from fastmlx_amd import FmxqError, ops
+
+    rng = np.random.default_rng(29)
+    E, D, I, T, k = 9, 256, 256, 2, 4
+    gate, up, down = _stack(rng, E, D, I)
+    x = make_x(rng, T, D)
+    inds = topk_uniform(rng, T, E, k)
+    inds[1, 2] = 77
+    announce("switch_glu few slots, out-of-range id")
+    got = _run(gpu, x, inds, gate, up, down)
+    assert np.all(got[1, 2] == 0)
+    with pytest.raises(FmxqError):
+        ops.device_error()
+    ref = oracle.switch_glu(x, np.where(inds >= E, 0, inds), gate, up, down)
+    keep = np.ones((T, k), dtype=bool)
+    keep[1, 2] = False
+    assert rel_err(oracle.bf16_to_f32(got[keep]), oracle.bf16_to_f32(ref[keep])) <= TOL
+
+
+@pytest.mark.parametrize("with_lhs", [True, False])
+def test_gather_qmm_few_items(gpu, oracle, with_lhs):
+    """Up to 16 items: one segment per item in item order, with explicit lhs (one bad
+    row) or the implicit item // lhs_div rows, and one bad expert id."""
+    from fastmlx_amd import FmxqError, ops
+
+    rng = np.random.default_rng(31 + with_lhs)
+    E, N, K, xb, S = 6, 300, 512, 5, 12
+    w, s, b = make_quant(rng, (E, N), K, 4, 64)
+    x = make_x(rng, xb, 1, K)
+    rhs = rng.integers(0, E, size=S).astype(np.uint32)
+    rhs[4] = 40
+    if with_lhs:
+        lhs = rng.integers(0, xb, size=S).astype(np.uint32)
+        lhs[9] = xb
+        lhs_div = 1
+    else:
+        lhs = None
+        lhs_div = 3  # items 0..11 read rows 0..3
+    announce(f"gather_qmm few items lhs={with_lhs}")
+    y = ops.gather_qmm(to_dev(x, gpu), to_dev(w, gpu), to_dev(s, gpu), to_dev(b, gpu),
+                       to_dev(rhs, gpu), None if lhs is None else to_dev(lhs, gpu), lhs_div,
+                       True, 64, 4, False)
+    torch.cuda.synchronize()
+    got = to_np(y).reshape(S, N)
+    bad = np.zeros(S, dtype=bool)
+    bad[4] = True
+    if with_lhs:
+        bad[9] = True
+    assert np.all(got[bad] == 0)
+    with pytest.raises(FmxqError):
+        ops.device_error()
+    rows = lhs if with_lhs else (np.arange(S) // lhs_div).astype(np.uint32)
+    ref = oracle.gather_qmm(x.reshape(xb, K), w, s, b, rows[~bad].astype(np.int32),
+                            rhs[~bad].astype(np.int32))
+    assert rel_err(oracle.bf16_to_f32(got[~bad]), oracle.bf16_to_f32(ref)) <= TOL
