@@ -28,6 +28,7 @@
 #include "fmxq_common.hpp"
 #include "fmxq_internal.hpp"
 #include "fmxq_qmvs.hpp"
+#include "fmxq_qmv_impl.hpp"
 
 namespace fmxq {
 namespace {
@@ -175,6 +176,108 @@ static hipError_t launch_wc(const MoeArgs& a, int wc, int64_t max_seg, hipStream
   return hipGetLastError();
 }
 
+
+// One-row segments (the unsorted few-slot path) with K >= 2048: the decode GEMV
+// form of the same product.  Grid (row blocks of RW, slots); a block is KS waves
+// splitting K, lane l owning 16-byte chunk c0 + l of its slice for all RW rows of
+// each of the NMAT matrices; the slices meet in LDS and wave 0 stores RW output
+// columns (silu(g) * u with the op chain's roundings for NMAT = 2).  Arithmetic as
+// in the dense GEMV (fmxq_qmv.hip): exponent-trick pairs dotted with v_dot2, then
+// s d + (b - 128 s) sum(x) per chunk.
+template <int NMAT, int RW, int KS>
+__global__ __launch_bounds__(KS * 64) void moe_qmv1_kernel(MoeArgs a) {
+  constexpr int V = NMAT * RW;
+  constexpr int LV = __builtin_ctz(V);
+  __shared__ float part[KS][V];
+  const int lane = threadIdx.x & 63;
+  const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t slot = blockIdx.y;
+  const int64_t nbase = (int64_t)blockIdx.x * RW;
+  const uint32_t e = a.rhs[slot];
+  const int64_t xr = a.lhs ? (int64_t)a.lhs[slot] : slot / a.lhs_div;
+  const int64_t orow = a.yrow ? (int64_t)a.yrow[slot] : slot;
+  if ((int64_t)e >= a.E || xr >= a.x_rows) {
+    if (ks == 0 && lane < RW && nbase + lane < a.N) a.y[orow * a.N + nbase + lane] = 0;
+    if (ks == 0 && lane == 0) atomicOr(a.err_flag, 1u);
+    return;
+  }
+  const int nch = (int)(a.K / 32);
+  const int c0 = ks * nch / KS, c1 = (ks + 1) * nch / KS;
+  const int c = c0 + lane;
+  const bool live = c < c1;
+  const int cc = live ? c : c0;
+  const int g = cc >> 1;  // group of the chunk (64 values = 2 chunks)
+  const int64_t wpr = a.K / 8, gpr = a.K / 64;
+  u32x4 wv[NMAT][RW];
+  uint32_t sv[NMAT][RW], bv[NMAT][RW];
+#pragma unroll
+  for (int p = 0; p < NMAT; ++p)
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      int64_t n = nbase + r;
+      n = n < a.N ? n : a.N - 1;  // rows past N re-read row N-1; not stored
+      const int64_t row = (int64_t)e * a.N + n;
+      wv[p][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.w[p] + row * wpr) + cc);
+      sv[p][r] = a.s[p][row * gpr + g];
+      bv[p][r] = a.b[p][row * gpr + g];
+    }
+  // The weight requests go out before x is read and paired.
+  __builtin_amdgcn_sched_barrier(0);
+  XChunk<4> xc;
+  xc.load(a.x + xr * a.K, (int64_t)cc * 32);
+  float res[V];
+#pragma unroll
+  for (int p = 0; p < NMAT; ++p)
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const float sc = bf16_bits_to_f32(sv[p][r]);
+      const float bo = __builtin_fmaf(-magic_offset<4>(), sc, bf16_bits_to_f32(bv[p][r]));
+      const float t = __builtin_fmaf(sc, chunk_dot<4>(wv[p][r], xc), bo * xc.sum);
+      res[p * RW + r] = live ? t : 0.f;
+    }
+  const float tot = wave_sum_multi<V>(res, lane);
+  if ((lane & ((64 >> LV) - 1)) == 0) part[ks][lane >> (6 - LV)] = tot;
+  __syncthreads();
+  if (ks == 0 && lane < RW) {
+    const int64_t n = nbase + lane;
+    if (n < a.N) {
+      float acc[NMAT];
+#pragma unroll
+      for (int p = 0; p < NMAT; ++p) {
+        acc[p] = 0.f;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) acc[p] += part[k][p * RW + lane];
+      }
+      uint16_t v;
+      if constexpr (NMAT == 2) {
+        const float gg = r16(acc[0]), u = r16(acc[1]);
+        const float sg_ = r16(1.f / (1.f + __expf(-gg)));
+        v = (uint16_t)f32_to_bf16_rne(r16(r16(gg * sg_) * u));
+      } else {
+        v = (uint16_t)f32_to_bf16_rne(acc[0]);
+      }
+      a.y[orow * a.N + n] = v;
+    }
+  }
+}
+
+template <int NMAT, int KS>
+static hipError_t launch_qmv1_ks(const MoeArgs& a, hipStream_t stream) {
+  constexpr int RW = 4;
+  dim3 grid((unsigned)((a.N + RW - 1) / RW), (unsigned)a.S);
+  moe_qmv1_kernel<NMAT, RW, KS><<<grid, KS * 64, 0, stream>>>(a);
+  return hipGetLastError();
+}
+
+template <int NMAT>
+static hipError_t launch_qmv1_nmat(const MoeArgs& a, hipStream_t stream) {
+  const int64_t nch = a.K / 32;
+  if (nch <= 64) return launch_qmv1_ks<NMAT, 1>(a, stream);
+  if (nch <= 128) return launch_qmv1_ks<NMAT, 2>(a, stream);
+  if (nch <= 256) return launch_qmv1_ks<NMAT, 4>(a, stream);
+  return launch_qmv1_ks<NMAT, 8>(a, stream);
+}
+
 }  // namespace
 
 bool moe_qmvs_supported(int64_t N, int64_t K, int bits, int group_size) {
@@ -195,6 +298,10 @@ hipError_t launch_moe_qmvs(const MoeArgs& a, int nmat, int window, int64_t max_s
   if (!moe_qmvs_supported(a.N, a.K, 4, 64) || (window != 16 && window != 32) ||
       (nmat != 1 && nmat != 2))
     return hipErrorInvalidValue;
+  // One-row segments over rows of 2048..16384 values: the GEMV form (all lanes
+  // busy with 64-chunk slices; shorter rows stay on the MFMA walk).
+  if (!a.seg && a.K >= 2048 && a.K <= 16384)
+    return nmat == 2 ? launch_qmv1_nmat<2>(a, stream) : launch_qmv1_nmat<1>(a, stream);
   // K slices per block: about four 4-unit steps per wave, at most 4 slices; the
   // remaining waves of the block take further column groups.  With few segments
   // (decode) the column tiles narrow (one 16-column tile per wave, then more K

@@ -242,15 +242,16 @@ def test_gather_qmm_segments_unsorted_lhs_and_bad_rows(gpu, oracle):
 
 # --- few slots: no sort, every slot its own segment ---
 
-@pytest.mark.parametrize("E,T,k", [
-    (64, 1, 10),    # one decode token (configuration 3's top-10)
-    (8, 2, 8),      # 16 slots, every expert twice
-    (3, 5, 3),      # 15 slots over 3 experts: repeated experts in slot order
-    (5, 17, 1),     # 17 slots: the sorted path, just past the limit
+@pytest.mark.parametrize("E,T,k,D,I", [
+    (64, 1, 10, 256, 512),    # one decode token (configuration 3's top-10), MFMA walk
+    (8, 2, 8, 256, 512),      # 16 slots, every expert twice
+    (3, 5, 3, 256, 512),      # 15 slots over 3 experts: repeated experts in slot order
+    (5, 17, 1, 256, 512),     # 17 slots: the sorted path, just past the limit
+    (12, 1, 8, 2048, 2304),   # GEMV form: gate/up one 2048-deep slice, down two slices
+    (6, 2, 3, 4608, 2048),    # GEMV form: gate/up four slices of 36 chunks
 ])
-def test_switch_glu_few_slots(gpu, oracle, E, T, k):
+def test_switch_glu_few_slots(gpu, oracle, E, T, k, D, I):
     rng = np.random.default_rng(E * 13 + T * 5 + k)
-    D, I = 256, 512
     gate, up, down = _stack(rng, E, D, I)
     x = make_x(rng, T, D)
     inds = topk_uniform(rng, T, E, k)
@@ -280,14 +281,15 @@ def test_switch_glu_few_slots_bad_expert_id(gpu, oracle):
     assert rel_err(oracle.bf16_to_f32(got[keep]), oracle.bf16_to_f32(ref[keep])) <= TOL
 
 
-@pytest.mark.parametrize("with_lhs", [True, False])
-def test_gather_qmm_few_items(gpu, oracle, with_lhs):
+@pytest.mark.parametrize("with_lhs,K", [(True, 512), (False, 512), (True, 4096), (False, 6144)])
+def test_gather_qmm_few_items(gpu, oracle, with_lhs, K):
     """Up to 16 items: one segment per item in item order, with explicit lhs (one bad
-    row) or the implicit item // lhs_div rows, and one bad expert id."""
+    row) or the implicit item // lhs_div rows, and one bad expert id; K of 512 (MFMA
+    walk) and of 4096 / 6144 (GEMV form with two and four K slices)."""
     from fastmlx_amd import FmxqError, ops
 
-    rng = np.random.default_rng(31 + with_lhs)
-    E, N, K, xb, S = 6, 300, 512, 5, 12
+    rng = np.random.default_rng(31 + with_lhs + K)
+    E, N, xb, S = 6, 300, 5, 12
     w, s, b = make_quant(rng, (E, N), K, 4, 64)
     x = make_x(rng, xb, 1, K)
     rhs = rng.integers(0, E, size=S).astype(np.uint32)
@@ -299,7 +301,7 @@ def test_gather_qmm_few_items(gpu, oracle, with_lhs):
     else:
         lhs = None
         lhs_div = 3  # items 0..11 read rows 0..3
-    announce(f"gather_qmm few items lhs={with_lhs}")
+    announce(f"gather_qmm few items lhs={with_lhs} K={K}")
     y = ops.gather_qmm(to_dev(x, gpu), to_dev(w, gpu), to_dev(s, gpu), to_dev(b, gpu),
                        to_dev(rhs, gpu), None if lhs is None else to_dev(lhs, gpu), lhs_div,
                        True, 64, 4, False)
