@@ -51,6 +51,7 @@ __global__ __launch_bounds__(256) void moe_qmvs_kernel(MoeArgs a) {
   const int c16 = lane & 15, q = lane >> 4;
   const int64_t start = a.seg ? (int64_t)a.seg[2 * sg] : sg;
   const int64_t len = a.seg ? (int64_t)a.seg[2 * sg + 1] : 1;
+  if (len < a.min_len) return;  // taken by the GEMV form
   const uint32_t e = a.rhs[start];
   const int64_t nb = (int64_t)blockIdx.x * (16 * NTT * WC) + wc * (16 * NTT);
   const bool bad_e = (int64_t)e >= a.E;
@@ -177,28 +178,50 @@ static hipError_t launch_wc(const MoeArgs& a, int wc, int64_t max_seg, hipStream
 }
 
 
-// One-row segments (the unsorted few-slot path) with K >= 2048: the decode GEMV
-// form of the same product.  Grid (row blocks of RW, slots); a block is KS waves
-// splitting K, lane l owning 16-byte chunk c0 + l of its slice for all RW rows of
-// each of the NMAT matrices; the slices meet in LDS and wave 0 stores RW output
-// columns (silu(g) * u with the op chain's roundings for NMAT = 2).  Arithmetic as
-// in the dense GEMV (fmxq_qmv.hip): exponent-trick pairs dotted with v_dot2, then
-// s d + (b - 128 s) sum(x) per chunk.
-template <int NMAT, int RW, int KS>
+// Short segments (up to MM slots; every slot is its own segment on the unsorted
+// few-slot path) with K >= 2048: the decode GEMV form of the same product.  Grid
+// (row blocks of RW, segments); a block is KS waves splitting K, lane l owning
+// 16-byte chunk c0 + l of its slice for all RW rows of each of the NMAT matrices.
+// Each packed word is unpacked once and dotted with the segment's x rows (v_dot2
+// on exponent-trick pairs, then s d + (b - 128 s) sum(x) per chunk, as in the
+// dense GEMV, fmxq_qmv.hip).  The slices meet in LDS and wave 0 stores RW output
+// columns per slot (silu(g) * u with the op chain's roundings for NMAT = 2).
+// Segments longer than MM are left to the MFMA walk above.
+template <int NMAT, int RW, int KS, int MM>
 __global__ __launch_bounds__(KS * 64) void moe_qmv1_kernel(MoeArgs a) {
-  constexpr int V = NMAT * RW;
+  constexpr int V = NMAT * RW * MM;  // partials per lane: index (p RW + r) MM + m
   constexpr int LV = __builtin_ctz(V);
+  static_assert((V & (V - 1)) == 0 && V <= 64, "partials per lane");
   __shared__ float part[KS][V];
   const int lane = threadIdx.x & 63;
   const int ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t slot = blockIdx.y;
+  const int64_t sg = blockIdx.y;
+  int64_t start = sg, len = 1;
+  if (a.seg) {
+    if (sg >= (int64_t)*a.nseg) return;
+    start = a.seg[2 * sg];
+    len = a.seg[2 * sg + 1];
+    if (len > MM) return;
+  }
   const int64_t nbase = (int64_t)blockIdx.x * RW;
-  const uint32_t e = a.rhs[slot];
-  const int64_t xr = a.lhs ? (int64_t)a.lhs[slot] : slot / a.lhs_div;
-  const int64_t orow = a.yrow ? (int64_t)a.yrow[slot] : slot;
-  if ((int64_t)e >= a.E || xr >= a.x_rows) {
-    if (ks == 0 && lane < RW && nbase + lane < a.N) a.y[orow * a.N + nbase + lane] = 0;
-    if (ks == 0 && lane == 0) atomicOr(a.err_flag, 1u);
+  const uint32_t e = a.rhs[start];
+  int64_t xr[MM], orow[MM];
+  bool rbad[MM];
+#pragma unroll
+  for (int m = 0; m < MM; ++m) {
+    const int64_t slot = start + (m < len ? m : 0);
+    const int64_t r = a.lhs ? (int64_t)a.lhs[slot] : slot / a.lhs_div;
+    rbad[m] = r >= a.x_rows;
+    xr[m] = rbad[m] ? 0 : r;
+    orow[m] = a.yrow ? (int64_t)a.yrow[slot] : slot;
+  }
+  if ((int64_t)e >= a.E) {
+    if (ks == 0) {
+#pragma unroll
+      for (int m = 0; m < MM; ++m)
+        if (m < len && lane < RW && nbase + lane < a.N) a.y[orow[m] * a.N + nbase + lane] = 0;
+      if (lane == 0) atomicOr(a.err_flag, 1u);
+    }
     return;
   }
   const int nch = (int)(a.K / 32);
@@ -223,8 +246,12 @@ __global__ __launch_bounds__(KS * 64) void moe_qmv1_kernel(MoeArgs a) {
     }
   // The weight requests go out before x is read and paired.
   __builtin_amdgcn_sched_barrier(0);
-  XChunk<4> xc;
-  xc.load(a.x + xr * a.K, (int64_t)cc * 32);
+  XChunk<4> xc[MM];
+#pragma unroll
+  for (int m = 0; m < MM; ++m) {
+    xc[m].load(a.x + xr[m] * a.K, (int64_t)cc * 32);
+    if (!live) xc[m].sum = 0.f;
+  }
   float res[V];
 #pragma unroll
   for (int p = 0; p < NMAT; ++p)
@@ -232,50 +259,72 @@ __global__ __launch_bounds__(KS * 64) void moe_qmv1_kernel(MoeArgs a) {
     for (int r = 0; r < RW; ++r) {
       const float sc = bf16_bits_to_f32(sv[p][r]);
       const float bo = __builtin_fmaf(-magic_offset<4>(), sc, bf16_bits_to_f32(bv[p][r]));
-      const float t = __builtin_fmaf(sc, chunk_dot<4>(wv[p][r], xc), bo * xc.sum);
-      res[p * RW + r] = live ? t : 0.f;
+      if constexpr (MM == 1) {
+        const float t = __builtin_fmaf(sc, chunk_dot<4>(wv[p][r], xc[0]), bo * xc[0].sum);
+        res[p * RW + r] = live ? t : 0.f;
+      } else {
+        uint32_t pk[16];
+        unpack_chunk(wv[p][r], pk);
+#pragma unroll
+        for (int m = 0; m < MM; ++m) {
+          const float t = __builtin_fmaf(sc, dot_pairs<4>(pk, xc[m]), bo * xc[m].sum);
+          res[(p * RW + r) * MM + m] = live ? t : 0.f;
+        }
+      }
     }
   const float tot = wave_sum_multi<V>(res, lane);
   if ((lane & ((64 >> LV) - 1)) == 0) part[ks][lane >> (6 - LV)] = tot;
   __syncthreads();
-  if (ks == 0 && lane < RW) {
-    const int64_t n = nbase + lane;
-    if (n < a.N) {
+  if (ks == 0 && lane < RW * MM) {
+    const int r = lane / MM, m = lane % MM;
+    const int64_t n = nbase + r;
+    int64_t o = orow[0];
+    bool bad = rbad[0];
+#pragma unroll
+    for (int mm = 1; mm < MM; ++mm)
+      if (m == mm) {
+        o = orow[mm];
+        bad = rbad[mm];
+      }
+    if (m < len && n < a.N) {
       float acc[NMAT];
 #pragma unroll
       for (int p = 0; p < NMAT; ++p) {
         acc[p] = 0.f;
 #pragma unroll
-        for (int k = 0; k < KS; ++k) acc[p] += part[k][p * RW + lane];
+        for (int k = 0; k < KS; ++k) acc[p] += part[k][(p * RW + r) * MM + m];
       }
       uint16_t v;
-      if constexpr (NMAT == 2) {
+      if (bad) {
+        v = 0;
+      } else if constexpr (NMAT == 2) {
         const float gg = r16(acc[0]), u = r16(acc[1]);
         const float sg_ = r16(1.f / (1.f + __expf(-gg)));
         v = (uint16_t)f32_to_bf16_rne(r16(r16(gg * sg_) * u));
       } else {
         v = (uint16_t)f32_to_bf16_rne(acc[0]);
       }
-      a.y[orow * a.N + n] = v;
+      a.y[o * a.N + n] = v;
+      if (bad) atomicOr(a.err_flag, 1u);
     }
   }
 }
 
-template <int NMAT, int KS>
-static hipError_t launch_qmv1_ks(const MoeArgs& a, hipStream_t stream) {
+template <int NMAT, int KS, int MM>
+static hipError_t launch_qmv1_ks(const MoeArgs& a, int64_t segs, hipStream_t stream) {
   constexpr int RW = 4;
-  dim3 grid((unsigned)((a.N + RW - 1) / RW), (unsigned)a.S);
-  moe_qmv1_kernel<NMAT, RW, KS><<<grid, KS * 64, 0, stream>>>(a);
+  dim3 grid((unsigned)((a.N + RW - 1) / RW), (unsigned)segs);
+  moe_qmv1_kernel<NMAT, RW, KS, MM><<<grid, KS * 64, 0, stream>>>(a);
   return hipGetLastError();
 }
 
-template <int NMAT>
-static hipError_t launch_qmv1_nmat(const MoeArgs& a, hipStream_t stream) {
+template <int NMAT, int MM>
+static hipError_t launch_qmv1_nmat(const MoeArgs& a, int64_t segs, hipStream_t stream) {
   const int64_t nch = a.K / 32;
-  if (nch <= 64) return launch_qmv1_ks<NMAT, 1>(a, stream);
-  if (nch <= 128) return launch_qmv1_ks<NMAT, 2>(a, stream);
-  if (nch <= 256) return launch_qmv1_ks<NMAT, 4>(a, stream);
-  return launch_qmv1_ks<NMAT, 8>(a, stream);
+  if (nch <= 64) return launch_qmv1_ks<NMAT, 1, MM>(a, segs, stream);
+  if (nch <= 128) return launch_qmv1_ks<NMAT, 2, MM>(a, segs, stream);
+  if (nch <= 256) return launch_qmv1_ks<NMAT, 4, MM>(a, segs, stream);
+  return launch_qmv1_ks<NMAT, 8, MM>(a, segs, stream);
 }
 
 }  // namespace
@@ -298,10 +347,24 @@ hipError_t launch_moe_qmvs(const MoeArgs& a, int nmat, int window, int64_t max_s
   if (!moe_qmvs_supported(a.N, a.K, 4, 64) || (window != 16 && window != 32) ||
       (nmat != 1 && nmat != 2))
     return hipErrorInvalidValue;
-  // One-row segments over rows of 2048..16384 values: the GEMV form (all lanes
-  // busy with 64-chunk slices; shorter rows stay on the MFMA walk).
-  if (!a.seg && a.K >= 2048 && a.K <= 16384)
-    return nmat == 2 ? launch_qmv1_nmat<2>(a, stream) : launch_qmv1_nmat<1>(a, stream);
+  // Rows of 2048..16384 values (all lanes busy with 64-chunk slices; shorter rows
+  // stay on the MFMA walk): without a segment table every slot takes the GEMV form;
+  // with one, segments of up to kMoeGemvMaxLen slots take it (a launch of its own)
+  // and the MFMA walk below skips them.
+  MoeArgs b = a;
+  if (a.K >= 2048 && a.K <= 16384) {
+    if (!a.seg)
+      return nmat == 2 ? launch_qmv1_nmat<2, 1>(a, a.S, stream)
+                       : launch_qmv1_nmat<1, 1>(a, a.S, stream);
+    // One-slot segments are common while slots are at most 8 per expert on
+    // average (uniform routings beyond that leave few).
+    if (a.S <= 8 * a.E) {
+      const hipError_t e = nmat == 2 ? launch_qmv1_nmat<2, kMoeGemvMaxLen>(a, max_seg, stream)
+                                     : launch_qmv1_nmat<1, kMoeGemvMaxLen>(a, max_seg, stream);
+      if (e != hipSuccess) return e;
+      b.min_len = kMoeGemvMaxLen + 1;
+    }
+  }
   // K slices per block: about four 4-unit steps per wave, at most 4 slices; the
   // remaining waves of the block take further column groups.  With few segments
   // (decode) the column tiles narrow (one 16-column tile per wave, then more K
@@ -319,13 +382,13 @@ hipError_t launch_moe_qmvs(const MoeArgs& a, int nmat, int window, int64_t max_s
   while (blocks(ks, ntt) < kMinBlocks && ks < 4 && 2 * ks <= nst) ks *= 2;
   const int wc = 4 / ks;
   if (nmat == 2)
-    return window == 16 ? launch_wc<1, 1, 2>(a, wc, max_seg, stream)
-                        : launch_wc<2, 1, 2>(a, wc, max_seg, stream);
+    return window == 16 ? launch_wc<1, 1, 2>(b, wc, max_seg, stream)
+                        : launch_wc<2, 1, 2>(b, wc, max_seg, stream);
   if (ntt == 1)
-    return window == 16 ? launch_wc<1, 1, 1>(a, wc, max_seg, stream)
-                        : launch_wc<2, 1, 1>(a, wc, max_seg, stream);
-  return window == 16 ? launch_wc<1, 2, 1>(a, wc, max_seg, stream)
-                      : launch_wc<2, 2, 1>(a, wc, max_seg, stream);
+    return window == 16 ? launch_wc<1, 1, 1>(b, wc, max_seg, stream)
+                        : launch_wc<2, 1, 1>(b, wc, max_seg, stream);
+  return window == 16 ? launch_wc<1, 2, 1>(b, wc, max_seg, stream)
+                      : launch_wc<2, 2, 1>(b, wc, max_seg, stream);
 }
 
 }  // namespace fmxq

@@ -318,3 +318,71 @@ def test_gather_qmm_few_items(gpu, oracle, with_lhs, K):
     ref = oracle.gather_qmm(x.reshape(xb, K), w, s, b, rows[~bad].astype(np.int32),
                             rhs[~bad].astype(np.int32))
     assert rel_err(oracle.bf16_to_f32(got[~bad]), oracle.bf16_to_f32(ref)) <= TOL
+
+
+def test_switch_glu_segments_short_and_long(gpu, oracle):
+    """Sorted slots with K >= 2048: one-slot segments take the GEMV form, longer
+    ones the MFMA walk; Zipf routing gives both, plus one out-of-range id."""
+    from fastmlx_amd import FmxqError, ops
+
+    rng = np.random.default_rng(41)
+    E, T, k, D, I = 24, 40, 4, 2048, 2304
+    gate, up, down = _stack(rng, E, D, I)
+    x = make_x(rng, T, D)
+    inds = topk_zipf(rng, T, E, k)
+    inds[7, 1] = E + 5
+    counts = np.bincount(inds[inds < E].ravel(), minlength=E)
+    assert counts.max() > 4 and ((counts > 0) & (counts <= 4)).any()
+    announce("switch_glu segments, short and long, K >= 2048")
+    got = _run(gpu, x, inds, gate, up, down)
+    assert np.all(got[7, 1] == 0)
+    with pytest.raises(FmxqError):
+        ops.device_error()
+    keep = np.ones((T, k), dtype=bool)
+    keep[7, 1] = False
+    ref = oracle.switch_glu(x, np.where(inds >= E, 0, inds), gate, up, down)
+    assert rel_err(oracle.bf16_to_f32(got[keep]), oracle.bf16_to_f32(ref[keep])) <= TOL
+
+
+def test_gather_qmm_segments_short_and_long(gpu, oracle):
+    """gather_qmm over 70 items, K = 4096: runs of one item (GEMV form) and of 2 to
+    20 (MFMA walk), explicit lhs with a bad row, one bad id."""
+    from fastmlx_amd import FmxqError, ops
+
+    rng = np.random.default_rng(43)
+    E, N, K, xb = 10, 260, 4096, 9
+    w, s, b = make_quant(rng, (E, N), K, 4, 64)
+    x = make_x(rng, xb, 1, K)
+    lens = [20, 1, 2, 3, 4, 5, 1, 14, 2, 18]
+    rhs = np.concatenate([np.full(n, e, dtype=np.uint32) for e, n in enumerate(lens)])
+    rng.shuffle(rhs)
+    S = rhs.size
+    lhs = rng.integers(0, xb, size=S).astype(np.uint32)
+    rhs[11] = E
+    lhs[50] = xb + 1
+    announce("gather_qmm segments, short and long, K = 4096")
+    y = ops.gather_qmm(to_dev(x, gpu), to_dev(w, gpu), to_dev(s, gpu), to_dev(b, gpu),
+                       to_dev(rhs, gpu), to_dev(lhs, gpu), 1, True, 64, 4, False)
+    torch.cuda.synchronize()
+    got = to_np(y).reshape(S, N)
+    bad = np.zeros(S, dtype=bool)
+    bad[[11, 50]] = True
+    assert np.all(got[bad] == 0)
+    with pytest.raises(FmxqError):
+        ops.device_error()
+    ref = oracle.gather_qmm(x.reshape(xb, K), w, s, b, lhs[~bad].astype(np.int32),
+                            rhs[~bad].astype(np.int32))
+    assert rel_err(oracle.bf16_to_f32(got[~bad]), oracle.bf16_to_f32(ref)) <= TOL
+
+
+def test_switch_glu_many_slots_per_expert_long_rows(gpu, oracle):
+    """More than 8 slots per expert on average with K >= 2048: the MFMA walk alone."""
+    rng = np.random.default_rng(47)
+    E, T, k, D, I = 4, 40, 2, 2048, 2048
+    gate, up, down = _stack(rng, E, D, I)
+    x = make_x(rng, T, D)
+    inds = topk_uniform(rng, T, E, k)
+    announce("switch_glu 80 slots over 4 experts, K = 2048")
+    got = _run(gpu, x, inds, gate, up, down)
+    ref = oracle.switch_glu(x, inds, gate, up, down)
+    assert rel_err(oracle.bf16_to_f32(got), oracle.bf16_to_f32(ref)) <= TOL
