@@ -233,17 +233,23 @@ constexpr int64_t kMaxSegmentsGrid = 65535;
 // Scratch of the segmented MoE product in the stream arena: the sorted order,
 // ids and x rows of S slots, the segment table and count, and (SwitchGLU) the
 // h rows of the sorted slots.
+// With max_tiles > 0 also the grouped GEMM's work list and count and (gu_cols > 0)
+// the gate and up rows of its tiles.
 struct MoeScratch {
   uint32_t *order, *rhs, *lhs, *seg, *nseg;
   uint16_t* h;
+  uint32_t *tiles = nullptr, *ntile = nullptr;
+  uint16_t *g = nullptr, *u = nullptr;
 };
 int moe_scratch(hipStream_t s, int64_t S, int64_t h_cols, int64_t max_seg, MoeScratch* m,
-                const char* op) {
+                const char* op, int64_t max_tiles = 0, int64_t gu_cols = 0) {
   const size_t ib = align_up((size_t)S * sizeof(uint32_t));
   const size_t sb = align_up((size_t)max_seg * 2 * sizeof(uint32_t));
   const size_t hb = align_up((size_t)S * h_cols * sizeof(uint16_t));
+  const size_t tb = align_up((size_t)max_tiles * 2 * sizeof(uint32_t));
+  const size_t gb = align_up((size_t)S * gu_cols * sizeof(uint16_t));
   void* arena = nullptr;
-  if (int rc = stream_arena(s, 3 * ib + sb + 256 + hb, &arena, op)) return rc;
+  if (int rc = stream_arena(s, 3 * ib + sb + 256 + hb + tb + 256 + 2 * gb, &arena, op)) return rc;
   char* p = static_cast<char*>(arena);
   m->order = reinterpret_cast<uint32_t*>(p);
   m->rhs = reinterpret_cast<uint32_t*>(p + ib);
@@ -251,7 +257,39 @@ int moe_scratch(hipStream_t s, int64_t S, int64_t h_cols, int64_t max_seg, MoeSc
   m->seg = reinterpret_cast<uint32_t*>(p + 3 * ib);
   m->nseg = reinterpret_cast<uint32_t*>(p + 3 * ib + sb);
   m->h = h_cols ? reinterpret_cast<uint16_t*>(p + 3 * ib + sb + 256) : nullptr;
+  char* q = p + 3 * ib + sb + 256 + hb;
+  if (max_tiles > 0) {
+    m->tiles = reinterpret_cast<uint32_t*>(q);
+    m->ntile = reinterpret_cast<uint32_t*>(q + tb);
+    if (gu_cols > 0) {
+      m->g = reinterpret_cast<uint16_t*>(q + tb + 256);
+      m->u = reinterpret_cast<uint16_t*>(q + tb + 256 + gb);
+    }
+  }
   return FMXQ_OK;
+}
+
+// Expert runs of at least this many slots go to the grouped GEMM (tiles of
+// kGroupedTileRows slots); shorter runs stay on the segment kernels.
+constexpr int64_t kGroupedMinRun = 256;
+int64_t grouped_max_tiles(int64_t S, int64_t E) {
+  const int64_t runs = S / kGroupedMinRun < E ? S / kGroupedMinRun : E;
+  return runs == 0 ? 0 : runs + S / fmxq::kGroupedTileRows + 1;
+}
+// A grouped-GEMM pass over the work list of sorted slots (see QmmArgs::g_*).
+fmxq::QmmArgs grouped_args(const uint16_t* x, const uint32_t* w, const uint16_t* sc,
+                           const uint16_t* bi, uint16_t* y, int64_t N, int64_t K, int bits,
+                           int group_size, const MoeScratch& m, const uint32_t* rows,
+                           const uint32_t* yrow, int64_t x_rows, uint32_t* flag) {
+  fmxq::QmmArgs a{x, w, sc, bi, nullptr, y, 0, N, K, K, N, group_size, bits};
+  a.g_tiles = m.tiles;
+  a.g_ntile = m.ntile;
+  a.g_rhs = m.rhs;
+  a.g_rows = rows;
+  a.g_yrow = yrow;
+  a.g_xrows = x_rows;
+  a.g_flag = flag;
+  return a;
 }
 
 int qmm_common(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
@@ -402,15 +440,24 @@ int fmxq_gather_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* scales
     const int64_t max_seg = fmxq::moe_max_segments(batch, E, window);
     if (max_seg <= kMaxSegmentsGrid) {
       MoeScratch m;
-      if (int rc = moe_scratch(s, batch, 0, max_seg, &m, op)) return rc;
+      const int64_t max_tiles = fmxq::qmm_grouped_supported(N, K, x_batch, bits, group_size)
+                                    ? grouped_max_tiles(batch, E)
+                                    : 0;
+      if (int rc = moe_scratch(s, batch, 0, max_seg, &m, op, max_tiles)) return rc;
       if (int rc = hip_status(fmxq::launch_sort_slots(rhs_indices, batch, lhs_div, E, m.order,
                                                       m.rhs, m.lhs, s, lhs_indices, m.seg,
-                                                      m.nseg, window),
+                                                      m.nseg, window, m.tiles, m.ntile,
+                                                      (int)kGroupedMinRun,
+                                                      fmxq::kGroupedTileRows),
                               "gather_qmm: sort"))
         return rc;
       fmxq::MoeArgs a{x, m.lhs, {w, nullptr}, {scales, nullptr}, {biases, nullptr}, m.rhs,
                       m.seg, m.nseg, y, m.order, batch, N, K, E, x_batch, flag};
-      return hip_status(fmxq::launch_moe_qmvs(a, 1, window, max_seg, s), op);
+      if (int rc = hip_status(fmxq::launch_moe_qmvs(a, 1, window, max_seg, s), op)) return rc;
+      if (!max_tiles) return FMXQ_OK;
+      const fmxq::QmmArgs gq = grouped_args(x, w, scales, biases, y, N, K, bits, group_size, m,
+                                            m.lhs, m.order, x_batch, flag);
+      return hip_status(fmxq::launch_qmm_grouped(gq, max_tiles, s), op);
     }
   }
   fmxq::GatherArgs a{x,      w,     scales,  biases, lhs_indices, rhs_indices, y,
@@ -498,9 +545,18 @@ extern "C" int fmxq_switch_glu(const uint16_t* x, const uint32_t* inds, const ui
                        inds, nullptr, nullptr, out, nullptr, S, D, I, E, S, flag, 1};
       return hip_status(fmxq::launch_moe_qmvs(dn, 1, 16, S, s), "switch_glu: down");
     }
-    if (int rc = moe_scratch(s, S, I, max_seg, &m, op)) return rc;
+    // Long expert runs (>= kGroupedMinRun slots) go to the grouped GEMM: gate and
+    // up into g and u, silu * up into their h rows, then down.
+    const int64_t max_tiles =
+        fmxq::qmm_grouped_supported(I, D, T, bits, group_size) &&
+                fmxq::qmm_grouped_supported(D, I, S, bits, group_size)
+            ? grouped_max_tiles(S, E)
+            : 0;
+    if (int rc = moe_scratch(s, S, I, max_seg, &m, op, max_tiles, max_tiles ? I : 0)) return rc;
     if (int rc = hip_status(fmxq::launch_sort_slots(inds, S, topk, E, m.order, m.rhs, m.lhs, s,
-                                                    nullptr, m.seg, m.nseg, window),
+                                                    nullptr, m.seg, m.nseg, window, m.tiles,
+                                                    m.ntile, (int)kGroupedMinRun,
+                                                    fmxq::kGroupedTileRows),
                             "switch_glu: sort"))
       return rc;
     fmxq::MoeArgs gu{x, m.lhs, {w_gate, w_up}, {s_gate, s_up}, {b_gate, b_up}, m.rhs, m.seg,
@@ -508,9 +564,29 @@ extern "C" int fmxq_switch_glu(const uint16_t* x, const uint32_t* inds, const ui
     if (int rc = hip_status(fmxq::launch_moe_qmvs(gu, 2, window, max_seg, s),
                             "switch_glu: gate/up"))
       return rc;
+    if (max_tiles) {
+      const fmxq::QmmArgs gg = grouped_args(x, w_gate, s_gate, b_gate, m.g, I, D, bits,
+                                            group_size, m, m.lhs, nullptr, T, flag);
+      if (int rc = hip_status(fmxq::launch_qmm_grouped(gg, max_tiles, s), "switch_glu: gate"))
+        return rc;
+      const fmxq::QmmArgs gup = grouped_args(x, w_up, s_up, b_up, m.u, I, D, bits, group_size,
+                                             m, m.lhs, nullptr, T, flag);
+      if (int rc = hip_status(fmxq::launch_qmm_grouped(gup, max_tiles, s), "switch_glu: up"))
+        return rc;
+      if (int rc = hip_status(fmxq::launch_silu_mul_tiles(m.g, m.u, m.h, m.tiles, m.ntile,
+                                                          max_tiles, fmxq::kGroupedTileRows, I,
+                                                          s),
+                              "switch_glu: silu"))
+        return rc;
+    }
     fmxq::MoeArgs dn{m.h, nullptr, {w_down, nullptr}, {s_down, nullptr}, {b_down, nullptr},
                      m.rhs, m.seg, m.nseg, out, m.order, S, D, I, E, S, flag};
-    return hip_status(fmxq::launch_moe_qmvs(dn, 1, window, max_seg, s), "switch_glu: down");
+    if (int rc = hip_status(fmxq::launch_moe_qmvs(dn, 1, window, max_seg, s), "switch_glu: down"))
+      return rc;
+    if (!max_tiles) return FMXQ_OK;
+    const fmxq::QmmArgs gd = grouped_args(m.h, w_down, s_down, b_down, out, D, I, bits,
+                                          group_size, m, nullptr, m.order, S, flag);
+    return hip_status(fmxq::launch_qmm_grouped(gd, max_tiles, s), "switch_glu: down");
   }
   // The reference sorts once routing reaches 64 slots (switch_glu.go:119-124).
   const bool sort = S >= 64 && E <= kSortMaxExperts;

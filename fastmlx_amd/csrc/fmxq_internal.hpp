@@ -27,6 +27,18 @@ struct QmmArgs {
   // K ranges whose fp32 partials go to ws (no zero state) and are summed by a
   // second kernel.
   int64_t split_tail = 0;
+  // Grouped prefill GEMM only (expert-sorted slots): tile t of the work list is
+  // slots [g_tiles[2t], + g_tiles[2t+1]) of one expert g_rhs[start] (its weights at
+  // w/scales/biases + expert * N rows); slot s reads x row g_rows[s] (s itself
+  // without g_rows) and writes y row g_yrow[s] (s itself without g_yrow).  x has
+  // g_xrows rows; a slot whose x row is past them gets a zero row and raises g_flag.
+  const uint32_t* g_tiles = nullptr;
+  const uint32_t* g_ntile = nullptr;
+  const uint32_t* g_rhs = nullptr;
+  const uint32_t* g_rows = nullptr;
+  const uint32_t* g_yrow = nullptr;
+  int64_t g_xrows = 0;
+  uint32_t* g_flag = nullptr;
 };
 
 // Gathered product over `batch` items of Mx rows:
@@ -109,6 +121,10 @@ struct PrefillPlan {
 };
 PrefillPlan qmm_prefill_plan(const QmmArgs& a, int cus);
 hipError_t launch_qmm_prefill(const QmmArgs& a, hipStream_t stream);
+// Grouped form (QmmArgs::g_*): grid = N tiles x max_tiles work-list entries.
+constexpr int kGroupedTileRows = 128;
+bool qmm_grouped_supported(int64_t N, int64_t K, int64_t x_rows, int bits, int group_size);
+hipError_t launch_qmm_grouped(const QmmArgs& a, int64_t max_tiles, hipStream_t stream);
 
 hipError_t launch_gather_qmv(const GatherArgs& a, hipStream_t stream);
 
@@ -120,7 +136,12 @@ hipError_t launch_gather_qmv(const GatherArgs& a, hipStream_t stream);
 hipError_t launch_sort_slots(const uint32_t* inds, int64_t S, int64_t lhs_div, int64_t E,
                              uint32_t* order, uint32_t* rhs_sorted, uint32_t* lhs_sorted,
                              hipStream_t stream, const uint32_t* lhs = nullptr,
-                             uint32_t* seg = nullptr, uint32_t* nseg = nullptr, int window = 16);
+                             uint32_t* seg = nullptr, uint32_t* nseg = nullptr, int window = 16,
+                             uint32_t* tiles = nullptr, uint32_t* ntile = nullptr,
+                             int long_min = 0, int tile_rows = 0);
+hipError_t launch_silu_mul_tiles(const uint16_t* g, const uint16_t* u, uint16_t* h,
+                                 const uint32_t* tiles, const uint32_t* ntile, int64_t max_tiles,
+                                 int64_t tile_rows, int64_t n, hipStream_t stream);
 hipError_t launch_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* h, int64_t n,
                            hipStream_t stream);
 hipError_t launch_moe_combine(const uint16_t* y, const uint16_t* w, const uint16_t* shared,

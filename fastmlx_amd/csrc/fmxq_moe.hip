@@ -57,7 +57,10 @@ __device__ __forceinline__ uint32_t range_pieces(uint32_t off, uint32_t c, uint3
 // Each thread owns a run of consecutive buckets for the scans.  With seg
 // non-null, before the scatter: the pieces of every bucket's range
 // [off, off + count) cut at multiples of `window`, as (start, len) pairs in
-// bucket order, and their number in *nseg.
+// bucket order, and their number in *nseg.  With tiles non-null as well, the
+// runs of an expert (id < E) with at least long_min slots are not cut into
+// window pieces but into tiles of tile_rows slots, written as (start, len) pairs
+// to tiles with their number in *ntile (the grouped GEMM's work list).
 __global__ __launch_bounds__(1024) void sort_slots_kernel(const uint32_t* __restrict__ inds,
                                                           int64_t S, int64_t lhs_div, int64_t E,
                                                           uint32_t* __restrict__ order,
@@ -66,7 +69,9 @@ __global__ __launch_bounds__(1024) void sort_slots_kernel(const uint32_t* __rest
                                                           const uint32_t* __restrict__ lhs,
                                                           uint32_t* __restrict__ seg,
                                                           uint32_t* __restrict__ nseg,
-                                                          int window) {
+                                                          int window, uint32_t* __restrict__ tiles,
+                                                          uint32_t* __restrict__ ntile,
+                                                          uint32_t long_min, uint32_t tile_rows) {
   extern __shared__ uint32_t cnt[];  // E + 1 counters, then E + 1 cursors
   __shared__ uint32_t wsum[16], total;
   const int64_t nb = E + 1;
@@ -90,12 +95,28 @@ __global__ __launch_bounds__(1024) void sort_slots_kernel(const uint32_t* __rest
   }
   __syncthreads();
   if (seg) {
-    uint32_t lp = 0;
-    for (int64_t i = b0; i < b1; ++i) lp += range_pieces(cur[i], cnt[i], (uint32_t)window);
+    auto is_long = [&](int64_t i) { return tiles && i < E && cnt[i] >= long_min; };
+    uint32_t lp = 0, lt = 0;
+    for (int64_t i = b0; i < b1; ++i) {
+      if (is_long(i)) lt += (cnt[i] + tile_rows - 1) / tile_rows;
+      else lp += range_pieces(cur[i], cnt[i], (uint32_t)window);
+    }
     uint32_t k = block_exclusive_scan(lp, wsum, &total);
     if (threadIdx.x == 0) *nseg = total;
+    uint32_t kt = 0;
+    if (tiles) {
+      kt = block_exclusive_scan(lt, wsum, &total);
+      if (threadIdx.x == 0) *ntile = total;
+    }
     for (int64_t i = b0; i < b1; ++i) {
       const uint32_t end = cur[i] + cnt[i];
+      if (is_long(i)) {
+        for (uint32_t p = cur[i]; p < end; p += tile_rows, ++kt) {
+          tiles[2 * kt] = p;
+          tiles[2 * kt + 1] = end - p < tile_rows ? end - p : tile_rows;
+        }
+        continue;
+      }
       for (uint32_t p = cur[i]; p < end; ++k) {
         const uint32_t wend = (p / window + 1) * window;
         const uint32_t q = wend < end ? wend : end;
@@ -197,11 +218,57 @@ static unsigned grid_for(int64_t items, int64_t per_block) {
 hipError_t launch_sort_slots(const uint32_t* inds, int64_t S, int64_t lhs_div, int64_t E,
                              uint32_t* order, uint32_t* rhs_sorted, uint32_t* lhs_sorted,
                              hipStream_t stream, const uint32_t* lhs, uint32_t* seg,
-                             uint32_t* nseg, int window) {
+                             uint32_t* nseg, int window, uint32_t* tiles, uint32_t* ntile,
+                             int long_min, int tile_rows) {
   if (seg && (!nseg || window < 1)) return hipErrorInvalidValue;
+  if (tiles && (!seg || !ntile || long_min < 1 || tile_rows < 1)) return hipErrorInvalidValue;
   const size_t lds = (size_t)(E + 1) * 2 * sizeof(uint32_t);
   sort_slots_kernel<<<1, 1024, lds, stream>>>(inds, S, lhs_div, E, order, rhs_sorted, lhs_sorted,
-                                              lhs, seg, nseg, window);
+                                              lhs, seg, nseg, window, tiles, ntile,
+                                              (uint32_t)long_min, (uint32_t)tile_rows);
+  return hipGetLastError();
+}
+
+// h rows of the grouped-GEMM tiles: h = silu(g) * u with the op chain's roundings
+// (silu_mul_kernel's arithmetic).  Grid (column blocks, tile bound); a block
+// covers 256 x 8 values of one tile: rows start .. start + len, n cols.
+__global__ __launch_bounds__(256) void silu_mul_tiles_kernel(const uint16_t* __restrict__ g,
+                                                             const uint16_t* __restrict__ u,
+                                                             uint16_t* __restrict__ h,
+                                                             const uint32_t* __restrict__ tiles,
+                                                             const uint32_t* __restrict__ ntile,
+                                                             int64_t n) {
+  const int64_t t = blockIdx.y;
+  if (t >= (int64_t)*ntile) return;
+  const int64_t start = tiles[2 * t], len = tiles[2 * t + 1];
+  const int64_t n8 = n / 8, items = len * n8;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < items;
+       i += (int64_t)gridDim.x * 256) {
+    const int64_t r = start + i / n8, c = i % n8;
+    const u32x4 gv = reinterpret_cast<const u32x4*>(g + r * n)[c];
+    const u32x4 uv = reinterpret_cast<const u32x4*>(u + r * n)[c];
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float g0 = bf16_lo(gv[j]), g1 = bf16_hi(gv[j]);
+      const float s0 = r16(1.f / (1.f + __expf(-g0))), s1 = r16(1.f / (1.f + __expf(-g1)));
+      const float h0 = r16(r16(g0 * s0) * bf16_lo(uv[j]));
+      const float h1 = r16(r16(g1 * s1) * bf16_hi(uv[j]));
+      o[j] = f32_to_bf16_rne(h0) | (f32_to_bf16_rne(h1) << 16);
+    }
+    reinterpret_cast<u32x4*>(h + r * n)[c] = o;
+  }
+}
+
+hipError_t launch_silu_mul_tiles(const uint16_t* g, const uint16_t* u, uint16_t* h,
+                                 const uint32_t* tiles, const uint32_t* ntile, int64_t max_tiles,
+                                 int64_t tile_rows, int64_t n, hipStream_t stream) {
+  if (max_tiles <= 0) return hipSuccess;
+  if (n % 8 != 0) return hipErrorInvalidValue;
+  const int64_t per_tile = tile_rows * (n / 8);
+  dim3 grid((unsigned)((per_tile + 255) / 256 < 64 ? (per_tile + 255) / 256 : 64),
+            (unsigned)max_tiles);
+  silu_mul_tiles_kernel<<<grid, 256, 0, stream>>>(g, u, h, tiles, ntile, n);
   return hipGetLastError();
 }
 

@@ -98,7 +98,7 @@ struct PrefillTile {
   static_assert(3 * BM * 128 + 2 * BN * 128 <= 160 * 1024, "LDS budget");
 };
 
-template <int BITS, int BM, int BN, int WM, int WN>
+template <int BITS, int BM, int BN, int WM, int WN, bool GR = false>
 __global__ __launch_bounds__(WM * WN * 64, 1) void qmm_prefill_kernel(QmmArgs a) {
   using P = PrefillTile<BITS, BM, BN, WM, WN>;
   constexpr int T = P::T, TM = P::TM, TN = P::TN, UW = P::UW, BU = P::BU, AI = P::AI;
@@ -121,51 +121,71 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void qmm_prefill_kernel(QmmArgs a)
   // last a.split_tail tiles are cut into a.splits K ranges, one block each, which
   // write fp32 partials to a.ws for prefill_fixup_kernel (they are dispatched
   // last, so a part-full last wave of whole tiles becomes a full wave of parts).
-  const int nt_m = (int)((a.M + BM - 1) / BM);
-  const int64_t tiles = (int64_t)nt_m * ((a.N + BN - 1) / BN);
-  const int64_t full = tiles - (a.splits > 1 ? a.split_tail : 0);
-  int64_t t = blockIdx.x;
-  int part = -1;
-  if (t < full) {
-    if ((full & 7) == 0) t = (t & 7) * (full >> 3) + (t >> 3);
-  } else {
-    const int64_t r = t - full;
-    t = full + r / a.splits;
-    part = (int)(r % a.splits);
-  }
-  const int64_t m0 = (int64_t)(t % nt_m) * BM;
-  const int64_t n0 = (int64_t)(t / nt_m) * BN;
-
   const int64_t wpr = a.K * BITS / 32;
   const int gshift = __builtin_ctz((unsigned)a.group_size);
   const int64_t gpr = a.K >> gshift;
   const int nk_all = (int)(a.K / kStepK);
+  int64_t t = blockIdx.x, full = 0, m0 = 0, n0 = 0;
+  int part = -1;
+  // Grouped form: one work-list tile (slots g_start .. + g_len of expert g_e) by
+  // one N tile.
+  int64_t g_start = 0, g_len = 0, g_e = 0;
+  if constexpr (GR) {
+    const int64_t tile = blockIdx.y;
+    if (tile >= (int64_t)*a.g_ntile) return;
+    g_start = a.g_tiles[2 * tile];
+    g_len = a.g_tiles[2 * tile + 1];
+    g_e = a.g_rhs[g_start];
+    n0 = (int64_t)blockIdx.x * BN;
+  } else {
+    const int nt_m = (int)((a.M + BM - 1) / BM);
+    const int64_t tiles = (int64_t)nt_m * ((a.N + BN - 1) / BN);
+    full = tiles - (a.splits > 1 ? a.split_tail : 0);
+    if (t < full) {
+      if ((full & 7) == 0) t = (t & 7) * (full >> 3) + (t >> 3);
+    } else {
+      const int64_t r = t - full;
+      t = full + r / a.splits;
+      part = (int)(r % a.splits);
+    }
+    m0 = (int64_t)(t % nt_m) * BM;
+    n0 = (int64_t)(t / nt_m) * BN;
+  }
   const int kb = part < 0 ? 0 : (int)((int64_t)part * nk_all / a.splits);  // first step
   const int nk = part < 0 ? nk_all : (int)((int64_t)(part + 1) * nk_all / a.splits) - kb;
 
-  // x rows of this block through a buffer resource: rows past M read as zero.
-  const int64_t rows_here = a.M - m0 < BM ? a.M - m0 : BM;
+  // x rows through a buffer resource: rows past M (or a grouped slot's row past
+  // g_xrows) read as zero.
+  const int64_t rows_here = GR ? a.g_xrows : (a.M - m0 < BM ? a.M - m0 : BM);
   const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(a.x + m0 * a.ldx), (short)0, (int)(rows_here * a.ldx * 2), 0x00020000);
   // DMA instruction j of this wave fills rows 8 (wave AI + j) .. +8 of a stage:
   // lane L lands at row + L/8, position L%8, so it fetches chunk (L%8) ^ swz(row).
+  // Grouped: the row is tile slot g_start + row (slots past the tile repeat its
+  // first), whose x row comes from g_rows.
   uint32_t aoff[AI];
 #pragma unroll
   for (int j = 0; j < AI; ++j) {
     const int row = 8 * (wave * AI + j) + (lane >> 3);
     const int c = (lane & 7) ^ swz(row);
-    aoff[j] = (uint32_t)((row * a.ldx + c * 8) * 2);
+    if constexpr (GR) {
+      const int64_t slot = g_start + (row < g_len ? row : 0);
+      const int64_t xr = a.g_rows ? (int64_t)a.g_rows[slot] : slot;
+      aoff[j] = (uint32_t)((xr < a.g_xrows ? xr : a.g_xrows) * a.ldx * 2 + c * 16);
+    } else {
+      aoff[j] = (uint32_t)((row * a.ldx + c * 8) * 2);
+    }
   }
 
   // Weights, scales and biases through buffer resources: a thread's offset is
   // fixed and each step adds one wave-uniform offset (no per-step 64-bit address
   // arithmetic).  qmm_prefill_supported keeps every byte offset below 2^31.
   const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)a.w, (short)0, (int)(a.N * wpr * 4), 0x00020000);
+      (void*)(a.w + g_e * a.N * wpr), (short)0, (int)(a.N * wpr * 4), 0x00020000);
   const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)a.scales, (short)0, (int)(a.N * gpr * 2), 0x00020000);
+      (void*)(a.scales + g_e * a.N * gpr), (short)0, (int)(a.N * gpr * 2), 0x00020000);
   const __amdgpu_buffer_rsrc_t bres = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)a.biases, (short)0, (int)(a.N * gpr * 2), 0x00020000);
+      (void*)(a.biases + g_e * a.N * gpr), (short)0, (int)(a.N * gpr * 2), 0x00020000);
   uint32_t wvo[BU], svo[BU];
   int u_row[BU], u_idx[BU];
 #pragma unroll
@@ -372,17 +392,27 @@ __global__ __launch_bounds__(WM * WN * 64, 1) void qmm_prefill_kernel(QmmArgs a)
   const int64_t m_l = m0 + wm * P::WTM + fr;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
-    const int64_t m = m_l + i * 32;
-    if (m >= a.M) continue;
+    int64_t m = m_l + i * 32;
+    bool zero = false;
+    if constexpr (GR) {
+      if (m >= g_len) continue;
+      const int64_t slot = g_start + m;
+      const int64_t xr = a.g_rows ? (int64_t)a.g_rows[slot] : slot;
+      zero = xr >= a.g_xrows;
+      if (zero && fh == 0 && n0 + wn * P::WTN == 0) atomicOr(a.g_flag, 1u);
+      m = a.g_yrow ? (int64_t)a.g_yrow[slot] : slot;
+    } else {
+      if (m >= a.M) continue;
+    }
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int64_t n = n0 + wn * P::WTN + j * 32 + 8 * g + 4 * fh;
         if (n >= a.N) continue;
-        uint32_t p0 = pack_bf16x2(acc[i][j][4 * g], acc[i][j][4 * g + 1]);
-        uint32_t p1 = pack_bf16x2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
-        if (a.bias) {
+        uint32_t p0 = zero ? 0u : pack_bf16x2(acc[i][j][4 * g], acc[i][j][4 * g + 1]);
+        uint32_t p1 = zero ? 0u : pack_bf16x2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+        if (a.bias && !zero) {
           float bv[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) bv[e] = n + e < a.N ? bf16_bits_to_f32(a.bias[n + e]) : 0.f;
@@ -489,6 +519,25 @@ bool qmm_prefill_supported(const QmmArgs& a) {
          256 * a.ldx * 2 < ((int64_t)1 << 31) && a.N < ((int64_t)1 << 31) / 256 &&
          a.N * (a.K * a.bits / 8) < ((int64_t)1 << 31) &&
          a.N * (a.K / a.group_size) * 2 < ((int64_t)1 << 31);
+}
+
+bool qmm_grouped_supported(int64_t N, int64_t K, int64_t x_rows, int bits, int group_size) {
+  return bits == 4 && group_size >= 32 && K % kStepK == 0 && K > 0 && N > 0 &&
+         x_rows * K * 2 < ((int64_t)1 << 31) && N * (K / 2) < ((int64_t)1 << 31) &&
+         N * (K / group_size) * 2 < ((int64_t)1 << 31);
+}
+
+hipError_t launch_qmm_grouped(const QmmArgs& a, int64_t max_tiles, hipStream_t stream) {
+  if (max_tiles <= 0) return hipSuccess;
+  if (!qmm_grouped_supported(a.N, a.K, a.g_xrows, a.bits, a.group_size) || !a.g_tiles ||
+      !a.g_ntile || !a.g_rhs || !a.g_flag || a.ldx % 8 != 0 ||
+      (reinterpret_cast<uintptr_t>(a.x) & 15) || (reinterpret_cast<uintptr_t>(a.w) & 15))
+    return hipErrorInvalidValue;
+  static_assert(kGroupedTileRows == 128, "grouped tile height");
+  constexpr int BM = 128, BN = 256;
+  dim3 grid((unsigned)((a.N + BN - 1) / BN), (unsigned)max_tiles);
+  qmm_prefill_kernel<4, BM, BN, 2, 4, true><<<grid, 512, 0, stream>>>(a);
+  return hipGetLastError();
 }
 
 hipError_t launch_qmm_prefill(const QmmArgs& a, hipStream_t stream) {

@@ -386,3 +386,57 @@ def test_switch_glu_many_slots_per_expert_long_rows(gpu, oracle):
     got = _run(gpu, x, inds, gate, up, down)
     ref = oracle.switch_glu(x, inds, gate, up, down)
     assert rel_err(oracle.bf16_to_f32(got), oracle.bf16_to_f32(ref)) <= TOL
+
+
+# --- long expert runs (>= 256 slots): the grouped GEMM over 128-slot tiles ---
+
+@pytest.mark.parametrize("E,T,k,D,I", [
+    (2, 300, 2, 256, 512),     # two runs of 300 slots: tiles of 128, 128 and 44
+    (3, 390, 2, 1024, 512),    # runs of 270, 262 and 248 slots: either side of the threshold
+    (20, 400, 4, 512, 256),    # Zipf: one long run, the rest on the segment kernels
+])
+def test_switch_glu_long_runs(gpu, oracle, E, T, k, D, I):
+    rng = np.random.default_rng(E * 7 + T + k + D)
+    gate, up, down = _stack(rng, E, D, I)
+    x = make_x(rng, T, D)
+    inds = topk_zipf(rng, T, E, k) if E >= 20 else topk_uniform(rng, T, E, k)
+    counts = np.bincount(inds.ravel(), minlength=E)
+    assert counts.max() >= 256
+    announce(f"switch_glu long runs E={E} T={T} k={k} D={D} I={I} max run {counts.max()}")
+    got = _run(gpu, x, inds, gate, up, down)
+    ref = oracle.switch_glu(x, inds, gate, up, down)
+    assert rel_err(oracle.bf16_to_f32(got), oracle.bf16_to_f32(ref)) <= TOL
+
+
+def test_gather_qmm_long_runs_bad_row_and_id(gpu, oracle):
+    """gather_qmm with runs of 300, 260, 100 and 5 items (two grouped-GEMM runs of
+    three tiles each), N not a multiple of the 256-column tile, a bad x row inside a
+    long run and a bad expert id."""
+    from fastmlx_amd import FmxqError, ops
+
+    rng = np.random.default_rng(53)
+    E, N, K, xb = 4, 300, 512, 37
+    w, s, b = make_quant(rng, (E, N), K, 4, 64)
+    x = make_x(rng, xb, 1, K)
+    lens = [300, 260, 100, 5]
+    rhs = np.concatenate([np.full(n, e, dtype=np.uint32) for e, n in enumerate(lens)])
+    rng.shuffle(rhs)
+    S = rhs.size
+    lhs = rng.integers(0, xb, size=S).astype(np.uint32)
+    i_bad_row = int(np.nonzero(rhs == 0)[0][17])
+    lhs[i_bad_row] = xb + 4
+    i_bad_id = int(np.nonzero(rhs == 3)[0][0])
+    rhs[i_bad_id] = 11
+    announce("gather_qmm long runs with bad row and id")
+    y = ops.gather_qmm(to_dev(x, gpu), to_dev(w, gpu), to_dev(s, gpu), to_dev(b, gpu),
+                       to_dev(rhs, gpu), to_dev(lhs, gpu), 1, True, 64, 4, False)
+    torch.cuda.synchronize()
+    got = to_np(y).reshape(S, N)
+    bad = np.zeros(S, dtype=bool)
+    bad[[i_bad_row, i_bad_id]] = True
+    assert np.all(got[bad] == 0)
+    with pytest.raises(FmxqError):
+        ops.device_error()
+    ref = oracle.gather_qmm(x.reshape(xb, K), w, s, b, lhs[~bad].astype(np.int32),
+                            rhs[~bad].astype(np.int32))
+    assert rel_err(oracle.bf16_to_f32(got[~bad]), oracle.bf16_to_f32(ref)) <= TOL
