@@ -274,7 +274,8 @@ int moe_scratch(hipStream_t s, int64_t S, int64_t h_cols, int64_t max_seg, MoeSc
 constexpr int64_t kGroupedMinRun = 256;
 int64_t grouped_max_tiles(int64_t S, int64_t E) {
   const int64_t runs = S / kGroupedMinRun < E ? S / kGroupedMinRun : E;
-  return runs == 0 ? 0 : runs + S / fmxq::kGroupedTileRows + 1;
+  const int64_t bound = runs == 0 ? 0 : runs + S / fmxq::kGroupedTileRows + 1;
+  return bound <= kMaxSegmentsGrid ? bound : 0;  // the work list runs along the grid's y axis
 }
 // A grouped-GEMM pass over the work list of sorted slots (see QmmArgs::g_*).
 fmxq::QmmArgs grouped_args(const uint16_t* x, const uint32_t* w, const uint16_t* sc,
