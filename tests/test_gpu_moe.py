@@ -388,12 +388,12 @@ def test_switch_glu_many_slots_per_expert_long_rows(gpu, oracle):
     assert rel_err(oracle.bf16_to_f32(got), oracle.bf16_to_f32(ref)) <= TOL
 
 
-# --- long expert runs (>= 256 slots): the grouped GEMM over 128-slot tiles ---
+# --- long expert runs (>= 256 slots, batches of >= 4096 slots): the grouped GEMM ---
 
 @pytest.mark.parametrize("E,T,k,D,I", [
-    (2, 300, 2, 256, 512),     # two runs of 300 slots: tiles of 128, 128 and 44
-    (3, 390, 2, 1024, 512),    # runs of 270, 262 and 248 slots: either side of the threshold
-    (20, 400, 4, 512, 256),    # Zipf: one long run, the rest on the segment kernels
+    (2, 2100, 2, 256, 256),    # two runs of 2100 slots: 16 full tiles and a partial each
+    (3, 2100, 2, 256, 512),    # three runs of ~1400
+    (24, 1024, 4, 256, 256),   # Zipf: runs of 838 .. 281 grouped, 239 and below on the walk
 ])
 def test_switch_glu_long_runs(gpu, oracle, E, T, k, D, I):
     rng = np.random.default_rng(E * 7 + T + k + D)
@@ -401,7 +401,7 @@ def test_switch_glu_long_runs(gpu, oracle, E, T, k, D, I):
     x = make_x(rng, T, D)
     inds = topk_zipf(rng, T, E, k) if E >= 20 else topk_uniform(rng, T, E, k)
     counts = np.bincount(inds.ravel(), minlength=E)
-    assert counts.max() >= 256
+    assert counts.max() >= 256 and T * k >= 4096
     announce(f"switch_glu long runs E={E} T={T} k={k} D={D} I={I} max run {counts.max()}")
     got = _run(gpu, x, inds, gate, up, down)
     ref = oracle.switch_glu(x, inds, gate, up, down)
@@ -409,23 +409,23 @@ def test_switch_glu_long_runs(gpu, oracle, E, T, k, D, I):
 
 
 def test_gather_qmm_long_runs_bad_row_and_id(gpu, oracle):
-    """gather_qmm with runs of 300, 260, 100 and 5 items (two grouped-GEMM runs of
-    three tiles each), N not a multiple of the 256-column tile, a bad x row inside a
-    long run and a bad expert id."""
+    """gather_qmm over 4096 items in runs of 2000, 1500, 300, 255 and 41 (three
+    grouped-GEMM runs; 255 just below the threshold), N not a multiple of the
+    256-column tile, a bad x row inside a long run and a bad expert id."""
     from fastmlx_amd import FmxqError, ops
 
     rng = np.random.default_rng(53)
-    E, N, K, xb = 4, 300, 512, 37
+    E, N, K, xb = 5, 300, 512, 37
     w, s, b = make_quant(rng, (E, N), K, 4, 64)
     x = make_x(rng, xb, 1, K)
-    lens = [300, 260, 100, 5]
+    lens = [2000, 1500, 300, 255, 41]
     rhs = np.concatenate([np.full(n, e, dtype=np.uint32) for e, n in enumerate(lens)])
     rng.shuffle(rhs)
     S = rhs.size
     lhs = rng.integers(0, xb, size=S).astype(np.uint32)
     i_bad_row = int(np.nonzero(rhs == 0)[0][17])
     lhs[i_bad_row] = xb + 4
-    i_bad_id = int(np.nonzero(rhs == 3)[0][0])
+    i_bad_id = int(np.nonzero(rhs == 4)[0][0])
     rhs[i_bad_id] = 11
     announce("gather_qmm long runs with bad row and id")
     y = ops.gather_qmm(to_dev(x, gpu), to_dev(w, gpu), to_dev(s, gpu), to_dev(b, gpu),
