@@ -8,6 +8,8 @@ Cases (4-bit, group 64 unless noted):
   qmm_up     M=2048, 14336x4096;  qmm_down  M=2048, 4096x14336
   skinny16   M=16, 14336x4096 over distinct copies
   moe_c3     config-3 MoE layer (512 experts, top-10) at --tokens M
+  moe_c4     config-4 routed experts (256 experts, 7168 -> 2048 -> 7168, top-8
+             Zipf(1.1)) at --tokens M; 8 routings rotate from launch to launch
   copy       a plain device copy of --mib MiB (calibrates byte counters: it
              reads and writes exactly that many bytes per dispatch)
 
@@ -34,7 +36,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--case", required=True,
                     choices=["qmv_up", "qmv_down", "qmm_up", "qmm_down", "skinny16", "moe_c3",
-                             "copy"])
+                             "moe_c4", "copy"])
     ap.add_argument("--launches", type=int, default=64)
     ap.add_argument("--copies", type=int, default=16)
     ap.add_argument("--mib", type=int, default=512)
@@ -72,6 +74,24 @@ def main():
             ops.switch_glu(x, inds, gate, up, down, 64, 4)
         hit = int(torch.unique(inds).numel())
         info.update(algorithmic_bytes=moe_bytes(M, D, I, k, hit, 4, 64), experts_hit=hit)
+    elif args.case == "moe_c4":
+        E, D, I, k, M, R = 256, 7168, 2048, 8, args.tokens, 8
+        gate = [t.view(E, I, -1) for t in _quant(torch, E * I, D, 4, gen, dev)]
+        up = [t.view(E, I, -1) for t in _quant(torch, E * I, D, 4, gen, dev)]
+        down = [t.view(E, D, -1) for t in _quant(torch, E * D, I, 4, gen, dev)]
+        x = torch.randn(M, D, device=dev, generator=gen).to(torch.bfloat16)
+        pz = torch.arange(1, E + 1, device=dev, dtype=torch.float64) ** -1.1
+        routes = []
+        for _ in range(R):
+            ranks = torch.multinomial(pz.expand(M, E), k, replacement=False, generator=gen)
+            routes.append(torch.randperm(E, device=dev, generator=gen)[ranks].to(torch.int32))
+        ys = torch.empty(M, k, D, device=dev, dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        for i in range(args.launches):
+            ops.switch_glu(x, routes[i % R], gate, up, down, 64, 4, out=ys)
+        hit = sum(int(torch.unique(r).numel()) for r in routes) / R
+        info.update(algorithmic_bytes=moe_bytes(M, D, I, k, int(round(hit)), 4, 64),
+                    experts_hit=hit)
     else:
         shapes = {"qmv_up": (1, 14336, 4096), "qmv_down": (1, 4096, 14336),
                   "qmm_up": (2048, 14336, 4096), "qmm_down": (2048, 4096, 14336),
