@@ -35,6 +35,48 @@ namespace {
 
 __device__ __forceinline__ float r16(float v) { return bf16_bits_to_f32(f32_to_bf16_rne(v)); }
 
+// Store a segment's rows.  C layout of a 16x16 tile: register r of lane l is row
+// 4 (l / 16) + r, column l % 16.  Row m of tile mt is slot start + 16 mt + m; nb
+// is the wave's first column.
+template <int MT, int NTT, int NMAT>
+__device__ __forceinline__ void store_segment(const MoeArgs& a, int64_t start, int64_t len,
+                                              bool bad_e, int64_t nb,
+                                              const f32x4 (&acc)[NMAT][MT][NTT]) {
+  const int lane = threadIdx.x & 63;
+  const int c16 = lane & 15, q = lane >> 4;
+  bool raise = false;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 16 * mt + 4 * q + r;
+      if (m >= len) continue;
+      const int64_t slot = start + m;
+      const int64_t xr = a.lhs ? (int64_t)a.lhs[slot] : slot / a.lhs_div;
+      const bool bad = bad_e || xr >= a.x_rows;
+      raise |= bad;
+      const int64_t orow = a.yrow ? (int64_t)a.yrow[slot] : slot;
+      uint16_t* yr = a.y + orow * a.N;
+#pragma unroll
+      for (int t = 0; t < NTT; ++t) {
+        const int64_t n = nb + 16 * t + c16;
+        if (n >= a.N) continue;
+        uint16_t v;
+        if (bad) {
+          v = 0;
+        } else if constexpr (NMAT == 2) {
+          const float g = r16(acc[0][mt][t][r]), u = r16(acc[1][mt][t][r]);
+          const float sg_ = r16(1.f / (1.f + __expf(-g)));
+          v = (uint16_t)f32_to_bf16_rne(r16(r16(g * sg_) * u));
+        } else {
+          v = (uint16_t)f32_to_bf16_rne(acc[0][mt][t][r]);
+        }
+        yr[n] = v;
+      }
+    }
+  if (raise) atomicOr(a.err_flag, 1u);
+}
+
 template <int MT, int NTT, int WC, int NMAT>
 __global__ __launch_bounds__(256) void moe_qmvs_kernel(MoeArgs a) {
   constexpr int SU = 4;
@@ -132,46 +174,96 @@ __global__ __launch_bounds__(256) void moe_qmvs_kernel(MoeArgs a) {
             for (int k = 0; k < KS - 1; ++k) acc[p][mt][t][r] += red[k][wc][p][mt][t][r][lane];
   }
 
-  // C layout of a 16x16 tile: register r of lane l is row 4 (l / 16) + r,
-  // column l % 16.  Row m of tile mt is slot start + 16 mt + m.
-  bool raise = false;
+  store_segment<MT, NTT, NMAT>(a, start, len, bad_e, nb, acc);
+}
+
+// Fixed-length (16 or 32 slot) x-in-LDS form of moe_qmvs_kernel for blocks whose
+// 4 waves walk the whole K range side by side (16 NTT columns each): the
+// segment's x rows go to LDS once per step for all four (qmvs_walk_xlds), so a
+// step's texture-unit traffic is the weights plus a quarter of x instead of the
+// weights plus all of x per wave.
+template <int MT, int NTT, int NMAT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void moe_qmvw_kernel(
+    MoeArgs a) {
+  using G = QmvsGeom<NTT, 4>;
+  __shared__ __attribute__((aligned(1024))) uint8_t xs0[16 * MT * kXStageRow];
+  __shared__ __attribute__((aligned(1024))) uint8_t xs1[16 * MT * kXStageRow];
+  __shared__ __attribute__((aligned(16))) uint8_t stage[4][NMAT * G::STAGE];
+
+  const int64_t sg = blockIdx.y;
+  if (sg >= (a.seg ? (int64_t)*a.nseg : a.S)) return;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t start = a.seg ? (int64_t)a.seg[2 * sg] : sg;
+  const int64_t len = a.seg ? (int64_t)a.seg[2 * sg + 1] : 1;
+  if (len < a.min_len) return;  // taken by the GEMV form
+  const uint32_t e = a.rhs[start];
+  const int64_t nb = (int64_t)blockIdx.x * (64 * NTT) + wave * (16 * NTT);
+  const bool bad_e = (int64_t)e >= a.E;
+
+  f32x4 acc[NMAT][MT][NTT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+  for (int p = 0; p < NMAT; ++p)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = 16 * mt + 4 * q + r;
-      if (m >= len) continue;
-      const int64_t slot = start + m;
-      const int64_t xr = a.lhs ? (int64_t)a.lhs[slot] : slot / a.lhs_div;
-      const bool bad = bad_e || xr >= a.x_rows;
-      raise |= bad;
-      const int64_t orow = a.yrow ? (int64_t)a.yrow[slot] : slot;
-      uint16_t* yr = a.y + orow * a.N;
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int t = 0; t < NTT; ++t) {
-        const int64_t n = nb + 16 * t + c16;
-        if (n >= a.N) continue;
-        uint16_t v;
-        if (bad) {
-          v = 0;
-        } else if constexpr (NMAT == 2) {
-          const float g = r16(acc[0][mt][t][r]), u = r16(acc[1][mt][t][r]);
-          const float sg_ = r16(1.f / (1.f + __expf(-g)));
-          v = (uint16_t)f32_to_bf16_rne(r16(r16(g * sg_) * u));
-        } else {
-          v = (uint16_t)f32_to_bf16_rne(acc[0][mt][t][r]);
-        }
-        yr[n] = v;
-      }
+      for (int t = 0; t < NTT; ++t) acc[p][mt][t] = f32x4{};
+  if (!bad_e) {
+    const int64_t wpr = a.K / 8, gpr = a.K / 64;
+    const uint32_t* w[NMAT];
+    const uint16_t* sc[NMAT];
+    const uint16_t* bi[NMAT];
+#pragma unroll
+    for (int p = 0; p < NMAT; ++p) {
+      w[p] = a.w[p] + (int64_t)e * a.N * wpr;
+      sc[p] = a.s[p] + (int64_t)e * a.N * gpr;
+      bi[p] = a.b[p] + (int64_t)e * a.N * gpr;
     }
-  if (raise) atomicOr(a.err_flag, 1u);
+    // moe_xlds_supported keeps x_rows * K * 2 below 2^31.
+    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)a.x, (short)0, (int)(a.x_rows * a.K * 2), 0x00020000);
+    // Byte offset of the x chunk lane `lane` fetches for DMA instruction j (see
+    // qmvs_walk_xlds): stage row r is slot start + r (the first slot past the
+    // segment), a bad x row reads row 0 (its output is zeroed).
+    auto x_offsets = [&](uint32_t* xo, int ax) {
+      for (int j = 0; j < ax; ++j) {
+        const int r = 2 * (wave * ax + j) + (lane >> 5);
+        const int c = (lane & 31) ^ (r & 15);
+        const int64_t slot = start + (r < len ? r : 0);
+        int64_t xr = a.lhs ? (int64_t)a.lhs[slot] : slot / a.lhs_div;
+        if (xr >= a.x_rows) xr = 0;
+        xo[j] = (uint32_t)(xr * a.K * 2 + c * 16);
+      }
+    };
+    if (MT == 2 && len <= 16) {
+      // Short segment of a 32-slot window: 16 stage rows, one tile walked.
+      uint32_t xo[2];
+      x_offsets(xo, 2);
+      qmvs_walk_xlds<1, MT, NTT, NMAT>(xs0, xs1, stage[wave], xres, xo, wave, w, sc, bi, nb, a.N,
+                                       a.K, acc);
+    } else {
+      uint32_t xo[2 * MT];
+      x_offsets(xo, 2 * MT);
+      qmvs_walk_xlds<MT, MT, NTT, NMAT>(xs0, xs1, stage[wave], xres, xo, wave, w, sc, bi, nb, a.N,
+                                        a.K, acc);
+    }
+  }
+  store_segment<MT, NTT, NMAT>(a, start, len, bad_e, nb, acc);
+}
+
+// x through buffer resources needs every byte offset of x below 2^31, and the
+// 16-byte DMA a 16-byte aligned base.
+static bool moe_xlds_supported(const MoeArgs& a) {
+  return a.x_rows > 0 && a.x_rows * a.K * 2 < (int64_t(1) << 31) &&
+         (reinterpret_cast<uintptr_t>(a.x) & 15) == 0;
 }
 
 template <int MT, int NTT, int NMAT>
 static hipError_t launch_wc(const MoeArgs& a, int wc, int64_t max_seg, hipStream_t stream) {
   const int64_t cols = 16 * NTT * wc;
   dim3 grid((unsigned)((a.N + cols - 1) / cols), (unsigned)max_seg);
-  if (wc == 1) moe_qmvs_kernel<MT, NTT, 1, NMAT><<<grid, 256, 0, stream>>>(a);
+  if (wc == 4 && moe_xlds_supported(a)) moe_qmvw_kernel<MT, NTT, NMAT><<<grid, 256, 0, stream>>>(a);
+  else if (wc == 1) moe_qmvs_kernel<MT, NTT, 1, NMAT><<<grid, 256, 0, stream>>>(a);
   else if (wc == 2) moe_qmvs_kernel<MT, NTT, 2, NMAT><<<grid, 256, 0, stream>>>(a);
   else moe_qmvs_kernel<MT, NTT, 4, NMAT><<<grid, 256, 0, stream>>>(a);
   return hipGetLastError();

@@ -25,6 +25,8 @@
 // operations of one wave complete in order.  Rows past N re-read row N-1 and
 // steps past s1 re-read step s1-1; neither reaches an output.
 #pragma once
+#include <type_traits>
+
 #include "fmxq_common.hpp"
 #include "fmxq_mfma_frag.hpp"
 
@@ -204,6 +206,215 @@ __device__ __forceinline__ void qmvs_slice(uint8_t* stage, const uint32_t* const
       }
     }
   }
+}
+
+typedef __attribute__((address_space(3))) void qmvs_lds_t;
+
+// s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding, expcnt left alone).
+template <int N>
+__device__ __forceinline__ void qmvs_wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+
+// Bytes of one row of the block-shared x stage: one 4-unit step, 256 bf16 values.
+constexpr int kXStageRow = 512;
+
+// The walk of qmvs_slice for a block of 4 waves that all walk the same K range
+// (each wave its own 16 NTT columns from nb), with the segment's x rows shared
+// through LDS instead of loaded by every wave.
+//
+// x stage (xs0 / xs1, one step each, alternating): 16 MTW rows of kXStageRow
+// bytes; 16-byte chunk c of row r sits at position c ^ (r & 15), so the 16 rows
+// an A-fragment read touches at one chunk fall on distinct banks.  The block
+// fills a stage with buffer_load ... lds (no VGPR staging): instruction j of wave
+// wave covers rows 2 (2 MTW wave + j) and the next, lane L landing at row + L / 32,
+// position L % 32; xo[j] is that lane's byte offset (its x row and swizzled
+// chunk) in xres, and a step adds kXStageRow bytes.
+//
+// Step st waits for its x stage (vmcnt then s_barrier: each wave's DMA has
+// landed and every wave has left step st - 1, whose stage the next DMA
+// overwrites), DMAs the x of step st + 1, stages its weights (loaded two steps
+// ahead, as in qmvs_slice) and runs the MFMAs.  Rows of the stage past the
+// segment hold its first slot's x; their accumulators are not stored.
+// Only acc[.][0, MTW) is touched.
+template <int MTW, int MT, int NTT, int NMAT>
+__device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8_t* stage,
+                                               __amdgpu_buffer_rsrc_t xres,
+                                               const uint32_t (&xo)[2 * MTW], int wave,
+                                               const uint32_t* const (&w)[NMAT],
+                                               const uint16_t* const (&sc)[NMAT],
+                                               const uint16_t* const (&bi)[NMAT], int64_t nb,
+                                               int64_t N, int64_t K,
+                                               f32x4 (&acc)[NMAT][MT][NTT]) {
+  constexpr int SU = 4;
+  using G = QmvsGeom<NTT, SU>;
+  constexpr int NI = G::NI, LPR = G::LPR, RB = G::RB, ROWS = G::ROWS, SPL = G::SPL;
+  constexpr int AX = 2 * MTW;
+  static_assert(MTW <= MT, "walked tiles");
+  typedef uint32_t sbv_t __attribute__((ext_vector_type(SPL / 2)));
+  const int lane = threadIdx.x & 63;
+  const int c16 = lane & 15, q = lane >> 4;
+  const int64_t wpr = K / 8, gpr = K / 64, nst = K / (SU * 64);
+
+  int64_t wq[NI];
+  int wo[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int r = i * (64 / LPR) + lane / LPR;
+    int64_t n = nb + r;
+    n = n < N ? n : N - 1;
+    wq[i] = n * wpr + (lane % LPR) * 4;
+    wo[i] = r * RB + (qmvs_pos<SU>(lane % LPR, r) << 4);
+  }
+  int wr[NTT][SU];
+#pragma unroll
+  for (int t = 0; t < NTT; ++t)
+#pragma unroll
+    for (int j = 0; j < SU; ++j) {
+      const int r = 16 * t + c16;
+      wr[t][j] = r * RB + (qmvs_pos<SU>(2 * j + (q >> 1), r) << 4) + (q & 1) * 8;
+    }
+  const int sh = lane / ROWS;
+  int64_t nrow = nb + lane % ROWS;
+  nrow = nrow < N ? nrow : N - 1;
+  const int64_t soff = nrow * gpr + ((64 / ROWS == 2) ? 0 : (sh >> 1) * SPL);
+  const uint16_t* sbrow[NMAT];
+#pragma unroll
+  for (int p = 0; p < NMAT; ++p) sbrow[p] = ((sh & 1) ? bi[p] : sc[p]) + soff;
+  // A-fragment byte offsets in a stage: row 16 mt + c16, chunk 8 j + 2 q (+1).
+  int xa[SU][2];
+#pragma unroll
+  for (int j = 0; j < SU; ++j)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) xa[j][h] = c16 * kXStageRow + (((8 * j + 2 * q + h) ^ c16) << 4);
+
+  u32x4 wbuf[2][NMAT][NI];
+  sbv_t sbuf[2][NMAT];
+  auto load_w = [&](int d, int64_t st) {
+    st = st < nst ? st : nst - 1;
+#pragma unroll
+    for (int p = 0; p < NMAT; ++p) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+        wbuf[d][p][i] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(w[p] + wq[i] + st * SU * 8));
+      sbuf[d][p] = *reinterpret_cast<const sbv_t*>(sbrow[p] + st * SU);
+    }
+  };
+  auto issue_x = [&](int64_t st, uint8_t* xs) {
+#pragma unroll
+    for (int j = 0; j < AX; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (qmvs_lds_t*)(xs + (wave * AX + j) * 1024),
+                                               16, (int)xo[j], (int)(st * kXStageRow), 0, 0);
+  };
+  const bf16x8 ones = as_bf16x8(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+
+  if (nst <= 0) return;
+  issue_x(0, xs0);
+  __builtin_amdgcn_sched_barrier(0);
+  load_w(0, 0);
+  load_w(1, 1);
+  __builtin_amdgcn_sched_barrier(0);
+  // One step; e (0 or 1) picks the stage and register set.  Pairs of steps run
+  // unconditionally inside the loop and an odd last step after it, so every path
+  // into a step has issued the same loads (the compiler then waits for no more
+  // than the explicit wait does).
+  auto step = [&](auto ec, int64_t stp) {
+    constexpr int e = decltype(ec)::value;
+    uint8_t* xc = e ? xs1 : xs0;
+    uint8_t* xn = e ? xs0 : xs1;
+    // Issued after this step's x: the loads of step stp + 1's weights.
+    qmvs_wait_vm_lgkm0<NMAT * (NI + 1)>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    // The weight stage is written and read back (B words of all SU units), and
+    // the scale and bias pairs shuffled, before the next x DMA goes out: LDS
+    // accesses after it that the compiler cannot tell apart from its target
+    // would wait for it.
+#pragma unroll
+    for (int p = 0; p < NMAT; ++p)
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+        *reinterpret_cast<u32x4*>(stage + p * G::STAGE + wo[i]) = wbuf[e][p][i];
+    u32x2 wv[SU][NMAT][NTT];
+#pragma unroll
+    for (int j = 0; j < SU; ++j)
+#pragma unroll
+      for (int p = 0; p < NMAT; ++p)
+#pragma unroll
+        for (int t = 0; t < NTT; ++t)
+          wv[j][p][t] = *reinterpret_cast<const u32x2*>(stage + p * G::STAGE + wr[t][j]);
+    sbv_t mine[NMAT];
+#pragma unroll
+    for (int p = 0; p < NMAT; ++p) mine[p] = sbuf[e][p];
+    uint32_t sv[NMAT][NTT][SU / 2], bv[NMAT][NTT][SU / 2];
+#pragma unroll
+    for (int p = 0; p < NMAT; ++p)
+#pragma unroll
+      for (int t = 0; t < NTT; ++t)
+#pragma unroll
+        for (int k = 0; k < SU / 2; ++k) {
+          const int row = 16 * t + c16;
+          const int hi = (64 / ROWS == 2) ? 0 : k / (SPL / 2);
+          const int idx = (64 / ROWS == 2) ? k : k % (SPL / 2);
+          sv[p][t][k] = (uint32_t)__shfl((int)mine[p][idx], (2 * hi) * ROWS + row, 64);
+          bv[p][t][k] = (uint32_t)__shfl((int)mine[p][idx], (2 * hi + 1) * ROWS + row, 64);
+        }
+    __builtin_amdgcn_sched_barrier(0);
+    if (stp + 1 < nst) issue_x(stp + 1, xn);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(e, stp + 2);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < SU; ++j) {
+      bf16x8 A[MTW][2];
+#pragma unroll
+      for (int mt = 0; mt < MTW; ++mt) {
+        A[mt][0] = xfrag4(*reinterpret_cast<const u32x4*>(xc + mt * 16 * kXStageRow + xa[j][0]));
+        A[mt][1] = xfrag4(*reinterpret_cast<const u32x4*>(xc + mt * 16 * kXStageRow + xa[j][1]));
+      }
+      f32x4 xsum[MTW];
+#pragma unroll
+      for (int mt = 0; mt < MTW; ++mt) {
+        xsum[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mt][0], ones, f32x4{}, 0, 0, 0);
+        xsum[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mt][1], ones, xsum[mt], 0, 0, 0);
+      }
+#pragma unroll
+      for (int p = 0; p < NMAT; ++p) {
+        f32x4 P[MTW][NTT];
+#pragma unroll
+        for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+          for (int t = 0; t < NTT; ++t) {
+            P[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                A[mt][0], wfrag<4>(wv[j][p][t][0]), f32x4{}, 0, 0, 0);
+            P[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                A[mt][1], wfrag<4>(wv[j][p][t][1]), P[mt][t], 0, 0, 0);
+          }
+#pragma unroll
+        for (int t = 0; t < NTT; ++t) {
+          const float s = (j & 1) ? bf16_hi(sv[p][t][j >> 1]) : bf16_lo(sv[p][t][j >> 1]);
+          const float b = (j & 1) ? bf16_hi(bv[p][t][j >> 1]) : bf16_lo(bv[p][t][j >> 1]);
+          const float bo = __builtin_fmaf(-128.f, s, b);
+#pragma unroll
+          for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              acc[p][mt][t][r] = __builtin_fmaf(s, P[mt][t][r],
+                                                __builtin_fmaf(bo, xsum[mt][r], acc[p][mt][t][r]));
+        }
+      }
+    }
+  };
+  int64_t st = 0;
+#pragma clang loop unroll(disable)
+  for (; st + 1 < nst; st += 2) {
+    step(std::integral_constant<int, 0>{}, st);
+    step(std::integral_constant<int, 1>{}, st + 1);
+  }
+  if (st < nst) step(std::integral_constant<int, 0>{}, st);
+  qmvs_wait_vm_lgkm0<0>();
 }
 
 }  // namespace fmxq
