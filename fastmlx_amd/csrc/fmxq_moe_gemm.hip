@@ -182,13 +182,13 @@ __global__ __launch_bounds__(256) void moe_qmvs_kernel(MoeArgs a) {
 // segment's x rows go to LDS once per step for all four (qmvs_walk_xlds), so a
 // step's texture-unit traffic is the weights plus a quarter of x instead of the
 // weights plus all of x per wave.
-template <int MT, int NTT, int NMAT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void moe_qmvw_kernel(
+template <int MT, int NTT, int NMAT, int WV>
+__global__ __launch_bounds__(WV * 64) __attribute__((amdgpu_waves_per_eu(2))) void moe_qmvw_kernel(
     MoeArgs a) {
   using G = QmvsGeom<NTT, 4>;
   __shared__ __attribute__((aligned(1024))) uint8_t xs0[16 * MT * kXStageRow];
   __shared__ __attribute__((aligned(1024))) uint8_t xs1[16 * MT * kXStageRow];
-  __shared__ __attribute__((aligned(16))) uint8_t stage[4][NMAT * G::STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t stage[WV][NMAT * G::STAGE];
 
   const int64_t sg = blockIdx.y;
   if (sg >= (a.seg ? (int64_t)*a.nseg : a.S)) return;
@@ -198,7 +198,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
   const int64_t len = a.seg ? (int64_t)a.seg[2 * sg + 1] : 1;
   if (len < a.min_len) return;  // taken by the GEMV form
   const uint32_t e = a.rhs[start];
-  const int64_t nb = (int64_t)blockIdx.x * (64 * NTT) + wave * (16 * NTT);
+  const int64_t nb = (int64_t)blockIdx.x * (16 * NTT * WV) + wave * (16 * NTT);
   const bool bad_e = (int64_t)e >= a.E;
 
   f32x4 acc[NMAT][MT][NTT];
@@ -223,8 +223,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
         (void*)a.x, (short)0, (int)(a.x_rows * a.K * 2), 0x00020000);
     // Byte offset of the x chunk lane `lane` fetches for DMA instruction j (see
-    // qmvs_walk_xlds): stage row r is slot start + r (the first slot past the
-    // segment), a bad x row reads row 0 (its output is zeroed).
+    // qmvs_walk_xlds): stage row r is slot start + r (the first slot for a row past
+    // the segment that shares an issued instruction), a bad x row reads row 0 (its
+    // output is zeroed).
     auto x_offsets = [&](uint32_t* xo, int ax) {
       for (int j = 0; j < ax; ++j) {
         const int r = 2 * (wave * ax + j) + (lane >> 5);
@@ -237,15 +238,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     };
     if (MT == 2 && len <= 16) {
       // Short segment of a 32-slot window: 16 stage rows, one tile walked.
-      uint32_t xo[2];
-      x_offsets(xo, 2);
-      qmvs_walk_xlds<1, MT, NTT, NMAT>(xs0, xs1, stage[wave], xres, xo, wave, w, sc, bi, nb, a.N,
-                                       a.K, acc);
+      uint32_t xo[8 / WV];
+      x_offsets(xo, 8 / WV);
+      qmvs_walk_xlds<1, MT, NTT, NMAT, WV>(xs0, xs1, stage[wave], xres, xo, wave, len, w, sc, bi,
+                                           nb, a.N, a.K, acc);
     } else {
-      uint32_t xo[2 * MT];
-      x_offsets(xo, 2 * MT);
-      qmvs_walk_xlds<MT, MT, NTT, NMAT>(xs0, xs1, stage[wave], xres, xo, wave, w, sc, bi, nb, a.N,
-                                        a.K, acc);
+      uint32_t xo[8 * MT / WV];
+      x_offsets(xo, 8 * MT / WV);
+      qmvs_walk_xlds<MT, MT, NTT, NMAT, WV>(xs0, xs1, stage[wave], xres, xo, wave, len, w, sc, bi,
+                                            nb, a.N, a.K, acc);
     }
   }
   store_segment<MT, NTT, NMAT>(a, start, len, bad_e, nb, acc);
@@ -262,7 +263,9 @@ template <int MT, int NTT, int NMAT>
 static hipError_t launch_wc(const MoeArgs& a, int wc, int64_t max_seg, hipStream_t stream) {
   const int64_t cols = 16 * NTT * wc;
   dim3 grid((unsigned)((a.N + cols - 1) / cols), (unsigned)max_seg);
-  if (wc == 4 && moe_xlds_supported(a)) moe_qmvw_kernel<MT, NTT, NMAT><<<grid, 256, 0, stream>>>(a);
+  // Four waves per block: an 8-wave block (128 columns per x fetch, one block
+  // per CU) measured slower (configuration 4 at M=256: 1871 -> 1971 us).
+  if (wc == 4 && moe_xlds_supported(a)) moe_qmvw_kernel<MT, NTT, NMAT, 4><<<grid, 256, 0, stream>>>(a);
   else if (wc == 1) moe_qmvs_kernel<MT, NTT, 1, NMAT><<<grid, 256, 0, stream>>>(a);
   else if (wc == 2) moe_qmvs_kernel<MT, NTT, 2, NMAT><<<grid, 256, 0, stream>>>(a);
   else moe_qmvs_kernel<MT, NTT, 4, NMAT><<<grid, 256, 0, stream>>>(a);

@@ -220,28 +220,32 @@ __device__ __forceinline__ void qmvs_wait_vm_lgkm0() {
 // Bytes of one row of the block-shared x stage: one 4-unit step, 256 bf16 values.
 constexpr int kXStageRow = 512;
 
-// The walk of qmvs_slice for a block of 4 waves that all walk the same K range
-// (each wave its own 16 NTT columns from nb), with the segment's x rows shared
-// through LDS instead of loaded by every wave.
+// The walk of qmvs_slice for a block of WV (4 or 8) waves that all walk the same
+// K range (each wave its own 16 NTT columns from nb), with the segment's x rows
+// shared through LDS instead of loaded by every wave.
 //
 // x stage (xs0 / xs1, one step each, alternating): 16 MTW rows of kXStageRow
 // bytes; 16-byte chunk c of row r sits at position c ^ (r & 15), so the 16 rows
 // an A-fragment read touches at one chunk fall on distinct banks.  The block
-// fills a stage with buffer_load ... lds (no VGPR staging): instruction j of wave
-// wave covers rows 2 (2 MTW wave + j) and the next, lane L landing at row + L / 32,
+// fills a stage with buffer_load ... lds (no VGPR staging): with AX = 8 MTW / WV
+// instructions per wave, instruction j of wave `wave` covers rows 2 (AX wave + j)
+// and the next, lane L landing at row + L / 32,
 // position L % 32; xo[j] is that lane's byte offset (its x row and swizzled
-// chunk) in xres, and a step adds kXStageRow bytes.
+// chunk) in xres, and a step adds kXStageRow bytes.  An instruction whose two
+// rows are both at or past the segment's length `len` is not issued (its stage
+// rows keep stale bytes, which reach only accumulator rows that are never stored).
 //
 // Step st waits for its x stage (vmcnt then s_barrier: each wave's DMA has
 // landed and every wave has left step st - 1, whose stage the next DMA
 // overwrites), DMAs the x of step st + 1, stages its weights (loaded two steps
-// ahead, as in qmvs_slice) and runs the MFMAs.  Rows of the stage past the
-// segment hold its first slot's x; their accumulators are not stored.
-// Only acc[.][0, MTW) is touched.
-template <int MTW, int MT, int NTT, int NMAT>
+// ahead, as in qmvs_slice) and runs the MFMAs.  Skipped DMA instructions change
+// no wait: the explicit wait counts only the weight loads issued after a step's
+// x.  Only acc[.][0, MTW) is touched.
+template <int MTW, int MT, int NTT, int NMAT, int WV>
 __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8_t* stage,
                                                __amdgpu_buffer_rsrc_t xres,
-                                               const uint32_t (&xo)[2 * MTW], int wave,
+                                               const uint32_t (&xo)[8 * MTW / WV], int wave,
+                                               int64_t len,
                                                const uint32_t* const (&w)[NMAT],
                                                const uint16_t* const (&sc)[NMAT],
                                                const uint16_t* const (&bi)[NMAT], int64_t nb,
@@ -250,8 +254,9 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
   constexpr int SU = 4;
   using G = QmvsGeom<NTT, SU>;
   constexpr int NI = G::NI, LPR = G::LPR, RB = G::RB, ROWS = G::ROWS, SPL = G::SPL;
-  constexpr int AX = 2 * MTW;
+  constexpr int AX = 8 * MTW / WV;
   static_assert(MTW <= MT, "walked tiles");
+  static_assert(AX >= 1 && AX * WV == 8 * MTW, "x DMA split over the block's waves");
   typedef uint32_t sbv_t __attribute__((ext_vector_type(SPL / 2)));
   const int lane = threadIdx.x & 63;
   const int c16 = lane & 15, q = lane >> 4;
@@ -305,8 +310,9 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
   auto issue_x = [&](int64_t st, uint8_t* xs) {
 #pragma unroll
     for (int j = 0; j < AX; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (qmvs_lds_t*)(xs + (wave * AX + j) * 1024),
-                                               16, (int)xo[j], (int)(st * kXStageRow), 0, 0);
+      if (2 * (wave * AX + j) < len)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (qmvs_lds_t*)(xs + (wave * AX + j) * 1024),
+                                                 16, (int)xo[j], (int)(st * kXStageRow), 0, 0);
   };
   const bf16x8 ones = as_bf16x8(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
 
