@@ -468,16 +468,15 @@ hipError_t launch_moe_qmvs(const MoeArgs& a, int nmat, int window, int64_t max_s
     }
   }
   // K slices per block; the remaining waves of the block take further column
-  // groups.  From 2 slots per expert on average, one slice: the four waves walk
-  // the same K range, so the x rows each of them loads are L1 hits for the others
-  // (measured: configuration 4 at M=256, 2537 -> 2243 us; configuration 3 at
-  // M=512, 494 -> 437 us).  Below that the segments are few and short, and about
-  // four 4-unit steps per wave (at most 4 slices) balance the grid better.  With
-  // few segments (decode) the column tiles narrow (one 16-column tile per wave,
-  // then more K slices while every slice keeps a step) until the grid has about
-  // two blocks per CU.
+  // groups.  One slice: the four waves walk the same K range and share the
+  // segment's x rows through LDS (moe_qmvw_kernel; measured against about four
+  // 4-unit steps per wave in up to 4 slices: configuration 4 at M=256 2537 -> 1874
+  // us, at M=32 715 -> 661 us; configuration 3 at M=512 494 -> 374 us).  With few
+  // segments (decode, a shared expert) the column tiles narrow (one 16-column tile
+  // per wave, then more K slices while every slice keeps a step) until the grid has
+  // about two blocks per CU.
   const int64_t nst = a.K / 256;
-  int ks = a.S >= 2 * a.E ? 1 : (nst >= 16 ? 4 : (nst >= 8 ? 2 : 1));
+  int ks = 1;
   int ntt = nmat == 2 ? 1 : 2;
   auto blocks = [&](int ks_, int ntt_) {
     const int64_t cols = 16 * ntt_ * (4 / ks_);
