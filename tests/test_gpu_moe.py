@@ -375,6 +375,47 @@ def test_gather_qmm_segments_short_and_long(gpu, oracle):
     assert rel_err(oracle.bf16_to_f32(got[~bad]), oracle.bf16_to_f32(ref)) <= TOL
 
 
+@pytest.mark.parametrize("E,lens", [
+    # 600 slots over 8 experts (32-slot windows): runs of 1, odd lengths, runs that end
+    # just inside or just past a window; grid 32 column tiles x 28 segments
+    (8, [1, 3, 17, 31, 33, 64, 151, 300]),
+    # 232 slots over 64 experts (16-slot windows), runs of 1 to 6; grid 16 x 80
+    (64, None),
+])
+def test_gather_qmm_shared_x_walk(gpu, oracle, E, lens):
+    """gather_qmm on grids of more than 512 blocks, where the MFMA walk shares each
+    segment's x rows through LDS and DMAs only the rows inside the segment; K below
+    2048, so every segment, one-slot ones included, takes the walk.  Explicit lhs
+    with a bad x row and one bad expert id."""
+    from fastmlx_amd import FmxqError, ops
+
+    rng = np.random.default_rng(59 + E)
+    N, K, xb = 2048, 1024, 50
+    w, s, b = make_quant(rng, (E, N), K, 4, 64)
+    x = make_x(rng, xb, 1, K)
+    if lens is None:
+        lens = [int(v) for v in rng.integers(1, 7, size=E)]
+    rhs = np.concatenate([np.full(n, e, dtype=np.uint32) for e, n in enumerate(lens)])
+    rng.shuffle(rhs)
+    S = rhs.size
+    lhs = rng.integers(0, xb, size=S).astype(np.uint32)
+    rhs[5] = E
+    lhs[S // 2] = xb + 3
+    announce(f"gather_qmm shared-x walk E={E} slots={S}")
+    y = ops.gather_qmm(to_dev(x, gpu), to_dev(w, gpu), to_dev(s, gpu), to_dev(b, gpu),
+                       to_dev(rhs, gpu), to_dev(lhs, gpu), 1, True, 64, 4, False)
+    torch.cuda.synchronize()
+    got = to_np(y).reshape(S, N)
+    bad = np.zeros(S, dtype=bool)
+    bad[[5, S // 2]] = True
+    assert np.all(got[bad] == 0)
+    with pytest.raises(FmxqError):
+        ops.device_error()
+    ref = oracle.gather_qmm(x.reshape(xb, K), w, s, b, lhs[~bad].astype(np.int32),
+                            rhs[~bad].astype(np.int32))
+    assert rel_err(oracle.bf16_to_f32(got[~bad]), oracle.bf16_to_f32(ref)) <= TOL
+
+
 def test_switch_glu_many_slots_per_expert_long_rows(gpu, oracle):
     """More than 8 slots per expert on average with K >= 2048: the MFMA walk alone."""
     rng = np.random.default_rng(47)
