@@ -280,13 +280,22 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
       const int r = 16 * t + c16;
       wr[t][j] = r * RB + (qmvs_pos<SU>(2 * j + (q >> 1), r) << 4) + (q & 1) * 8;
     }
+  // Scale/bias loads.  16-row tiles (NTT = 1): one 8-byte load per lane covers two
+  // steps (lane -> row l % 16, kind (l / 16) & 1 (scales, biases), step l / 32 of
+  // the pair: that step's 4 groups), issued in even steps for the next pair; a
+  // lane's step is clamped to the last, so an odd step count reads no further.
+  // 32-row tiles: one load per lane and step as in qmvs_slice.
+  constexpr bool PAIR = ROWS == 16;
+  typedef uint32_t spv_t __attribute__((ext_vector_type(2)));
   const int sh = lane / ROWS;
   int64_t nrow = nb + lane % ROWS;
   nrow = nrow < N ? nrow : N - 1;
-  const int64_t soff = nrow * gpr + ((64 / ROWS == 2) ? 0 : (sh >> 1) * SPL);
+  const int64_t soff =
+      nrow * gpr + ((PAIR || 64 / ROWS == 2) ? 0 : (sh >> 1) * SPL);
   const uint16_t* sbrow[NMAT];
 #pragma unroll
   for (int p = 0; p < NMAT; ++p) sbrow[p] = ((sh & 1) ? bi[p] : sc[p]) + soff;
+  const int ph = lane >> 5;  // step of the pair (PAIR)
   // A-fragment byte offsets in a stage: row 16 mt + c16, chunk 8 j + 2 q (+1).
   int xa[SU][2];
 #pragma unroll
@@ -296,7 +305,10 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
 
   u32x4 wbuf[2][NMAT][NI];
   sbv_t sbuf[2][NMAT];
-  auto load_w = [&](int d, int64_t st) {
+  spv_t sp[NMAT], held[NMAT];
+  // Weights (and, without PAIR, the step's scales) of step st into set d; with PAIR
+  // and pair set, the scales of steps st and st + 1 after the weights.
+  auto load_w = [&](int d, int64_t st, bool pair) {
     st = st < nst ? st : nst - 1;
 #pragma unroll
     for (int p = 0; p < NMAT; ++p) {
@@ -304,7 +316,15 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
       for (int i = 0; i < NI; ++i)
         wbuf[d][p][i] = __builtin_nontemporal_load(
             reinterpret_cast<const u32x4*>(w[p] + wq[i] + st * SU * 8));
-      sbuf[d][p] = *reinterpret_cast<const sbv_t*>(sbrow[p] + st * SU);
+      if constexpr (!PAIR) sbuf[d][p] = *reinterpret_cast<const sbv_t*>(sbrow[p] + st * SU);
+    }
+    if constexpr (PAIR) {
+      if (pair) {
+        int64_t sl = st + ph;
+        sl = sl < nst ? sl : nst - 1;
+#pragma unroll
+        for (int p = 0; p < NMAT; ++p) sp[p] = *reinterpret_cast<const spv_t*>(sbrow[p] + sl * SU);
+      }
     }
   };
   auto issue_x = [&](int64_t st, uint8_t* xs) {
@@ -319,8 +339,8 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
   if (nst <= 0) return;
   issue_x(0, xs0);
   __builtin_amdgcn_sched_barrier(0);
-  load_w(0, 0);
-  load_w(1, 1);
+  load_w(0, 0, true);
+  load_w(1, 1, false);
   __builtin_amdgcn_sched_barrier(0);
   // One step; e (0 or 1) picks the stage and register set.  Pairs of steps run
   // unconditionally inside the loop and an odd last step after it, so every path
@@ -330,8 +350,10 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
     constexpr int e = decltype(ec)::value;
     uint8_t* xc = e ? xs1 : xs0;
     uint8_t* xn = e ? xs0 : xs1;
-    // Issued after this step's x: the loads of step stp + 1's weights.
-    qmvs_wait_vm_lgkm0<NMAT * (NI + 1)>();
+    // Issued after this step's x: the loads of step stp + 1's weights, and with
+    // PAIR the scales of the pair that follows (loaded in even steps only).
+    if constexpr (PAIR && e == 0) qmvs_wait_vm_lgkm0<NMAT * NI>();
+    else qmvs_wait_vm_lgkm0<NMAT * (NI + 1)>();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     // The weight stage is written and read back (B words of all SU units), and
@@ -351,26 +373,40 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
 #pragma unroll
         for (int t = 0; t < NTT; ++t)
           wv[j][p][t] = *reinterpret_cast<const u32x2*>(stage + p * G::STAGE + wr[t][j]);
-    sbv_t mine[NMAT];
-#pragma unroll
-    for (int p = 0; p < NMAT; ++p) mine[p] = sbuf[e][p];
     uint32_t sv[NMAT][NTT][SU / 2], bv[NMAT][NTT][SU / 2];
+    if constexpr (PAIR) {
+      if constexpr (e == 0) {
 #pragma unroll
-    for (int p = 0; p < NMAT; ++p)
+        for (int p = 0; p < NMAT; ++p) held[p] = sp[p];
+      }
 #pragma unroll
-      for (int t = 0; t < NTT; ++t)
+      for (int p = 0; p < NMAT; ++p)
 #pragma unroll
         for (int k = 0; k < SU / 2; ++k) {
-          const int row = 16 * t + c16;
-          const int hi = (64 / ROWS == 2) ? 0 : k / (SPL / 2);
-          const int idx = (64 / ROWS == 2) ? k : k % (SPL / 2);
-          sv[p][t][k] = (uint32_t)__shfl((int)mine[p][idx], (2 * hi) * ROWS + row, 64);
-          bv[p][t][k] = (uint32_t)__shfl((int)mine[p][idx], (2 * hi + 1) * ROWS + row, 64);
+          sv[p][0][k] = (uint32_t)__shfl((int)held[p][k], 32 * e + c16, 64);
+          bv[p][0][k] = (uint32_t)__shfl((int)held[p][k], 32 * e + 16 + c16, 64);
         }
+    } else {
+      sbv_t mine[NMAT];
+#pragma unroll
+      for (int p = 0; p < NMAT; ++p) mine[p] = sbuf[e][p];
+#pragma unroll
+      for (int p = 0; p < NMAT; ++p)
+#pragma unroll
+        for (int t = 0; t < NTT; ++t)
+#pragma unroll
+          for (int k = 0; k < SU / 2; ++k) {
+            const int row = 16 * t + c16;
+            const int hi = (64 / ROWS == 2) ? 0 : k / (SPL / 2);
+            const int idx = (64 / ROWS == 2) ? k : k % (SPL / 2);
+            sv[p][t][k] = (uint32_t)__shfl((int)mine[p][idx], (2 * hi) * ROWS + row, 64);
+            bv[p][t][k] = (uint32_t)__shfl((int)mine[p][idx], (2 * hi + 1) * ROWS + row, 64);
+          }
+    }
     __builtin_amdgcn_sched_barrier(0);
     if (stp + 1 < nst) issue_x(stp + 1, xn);
     __builtin_amdgcn_sched_barrier(0);
-    load_w(e, stp + 2);
+    load_w(e, stp + 2, e == 0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < SU; ++j) {
