@@ -183,7 +183,7 @@ __global__ __launch_bounds__(256) void moe_qmvs_kernel(MoeArgs a) {
 // step's texture-unit traffic is the weights plus a quarter of x instead of the
 // weights plus all of x per wave.
 template <int MT, int NTT, int NMAT, int WV>
-__global__ __launch_bounds__(WV * 64) __attribute__((amdgpu_waves_per_eu(2))) void moe_qmvw_kernel(
+__global__ __launch_bounds__(WV * 64) __attribute__((amdgpu_waves_per_eu(MT == 1 ? 3 : 2))) void moe_qmvw_kernel(
     MoeArgs a) {
   using G = QmvsGeom<NTT, 4>;
   __shared__ __attribute__((aligned(1024))) uint8_t xs0[16 * MT * kXStageRow];
