@@ -183,7 +183,7 @@ __global__ __launch_bounds__(256) void moe_qmvs_kernel(MoeArgs a) {
 // step's texture-unit traffic is the weights plus a quarter of x instead of the
 // weights plus all of x per wave.
 template <int MT, int NTT, int NMAT, int WV>
-__global__ __launch_bounds__(WV * 64) __attribute__((amdgpu_waves_per_eu(MT == 1 ? 3 : 2))) void moe_qmvw_kernel(
+__global__ __launch_bounds__(WV * 64) __attribute__((amdgpu_waves_per_eu(MT == 1 && NTT == 1 ? 3 : 2))) void moe_qmvw_kernel(
     MoeArgs a) {
   using G = QmvsGeom<NTT, 4>;
   __shared__ __attribute__((aligned(1024))) uint8_t xs0[16 * MT * kXStageRow];
@@ -426,8 +426,10 @@ static hipError_t launch_qmv1_nmat(const MoeArgs& a, int64_t segs, hipStream_t s
 
 }  // namespace
 
+// One expert's weights go through a buffer resource: below 2^31 bytes.
 bool moe_qmvs_supported(int64_t N, int64_t K, int bits, int group_size) {
-  return bits == 4 && group_size == 64 && K % 256 == 0 && N >= 1;
+  return bits == 4 && group_size == 64 && K % 256 == 0 && N >= 1 &&
+         N * (K / 2) < (int64_t(1) << 31);
 }
 
 // 32-slot windows (two 16-row tiles per block) once slots average 4 per expert:

@@ -70,16 +70,24 @@ __device__ __forceinline__ void qmvs_slice(uint8_t* stage, const uint32_t* const
   const int c16 = lane & 15, q = lane >> 4;
   const int64_t wpr = K / 8, gpr = K / 64;
 
-  int64_t wq[NI];
+  // Weights through buffer resources (byte offsets below 2^31, checked by the
+  // callers): a step past the slice loads from an offset past the matrix, which
+  // returns zeros without a memory access, so the pipeline's last loads fetch
+  // nothing yet still issue (the instruction stream stays the same).
+  uint32_t wq[NI];
   int wo[NI];
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     const int r = i * (64 / LPR) + lane / LPR;
     int64_t n = nb + r;
     n = n < N ? n : N - 1;
-    wq[i] = n * wpr + (lane % LPR) * 4;
+    wq[i] = (uint32_t)((n * wpr + (lane % LPR) * 4) * 4);
     wo[i] = r * RB + (qmvs_pos<SU>(lane % LPR, r) << 4);
   }
+  __amdgpu_buffer_rsrc_t wres[NMAT];
+#pragma unroll
+  for (int p = 0; p < NMAT; ++p)
+    wres[p] = __builtin_amdgcn_make_buffer_rsrc((void*)w[p], (short)0, (int)(N * wpr * 4), 0x00020000);
   int wr[NTT][SU];
 #pragma unroll
   for (int t = 0; t < NTT; ++t)
@@ -102,13 +110,16 @@ __device__ __forceinline__ void qmvs_slice(uint8_t* stage, const uint32_t* const
   sbv_t sbuf[2][NMAT];
   u32x4 xv[XD][MT][2];
   auto load_w = [&](int d, int64_t st) {
-    st = st < s1 ? st : s1 - 1;
+    const bool past = st >= s1;
+    st = past ? s1 - 1 : st;
 #pragma unroll
     for (int p = 0; p < NMAT; ++p) {
 #pragma unroll
       for (int i = 0; i < NI; ++i)
-        wbuf[d][p][i] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(w[p] + wq[i] + st * SU * 8));
+        wbuf[d][p][i] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       wres[p], past ? (int)0x80000000u : (int)(wq[i] + (uint32_t)st * SU * 32), 0,
+                       2 /* nt */));
       sbuf[d][p] = *reinterpret_cast<const sbv_t*>(sbrow[p] + st * SU);
     }
   };
@@ -262,16 +273,22 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
   const int c16 = lane & 15, q = lane >> 4;
   const int64_t wpr = K / 8, gpr = K / 64, nst = K / (SU * 64);
 
-  int64_t wq[NI];
+  // Weights through buffer resources as in qmvs_slice: steps past the end load
+  // zeros without a memory access.
+  uint32_t wq[NI];
   int wo[NI];
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     const int r = i * (64 / LPR) + lane / LPR;
     int64_t n = nb + r;
     n = n < N ? n : N - 1;
-    wq[i] = n * wpr + (lane % LPR) * 4;
+    wq[i] = (uint32_t)((n * wpr + (lane % LPR) * 4) * 4);
     wo[i] = r * RB + (qmvs_pos<SU>(lane % LPR, r) << 4);
   }
+  __amdgpu_buffer_rsrc_t wres[NMAT];
+#pragma unroll
+  for (int p = 0; p < NMAT; ++p)
+    wres[p] = __builtin_amdgcn_make_buffer_rsrc((void*)w[p], (short)0, (int)(N * wpr * 4), 0x00020000);
   int wr[NTT][SU];
 #pragma unroll
   for (int t = 0; t < NTT; ++t)
@@ -309,13 +326,16 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
   // Weights (and, without PAIR, the step's scales) of step st into set d; with PAIR
   // and pair set, the scales of steps st and st + 1 after the weights.
   auto load_w = [&](int d, int64_t st, bool pair) {
-    st = st < nst ? st : nst - 1;
+    const bool past = st >= nst;
+    st = past ? nst - 1 : st;
 #pragma unroll
     for (int p = 0; p < NMAT; ++p) {
 #pragma unroll
       for (int i = 0; i < NI; ++i)
-        wbuf[d][p][i] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(w[p] + wq[i] + st * SU * 8));
+        wbuf[d][p][i] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       wres[p], past ? (int)0x80000000u : (int)(wq[i] + (uint32_t)st * SU * 32), 0,
+                       2 /* nt */));
       if constexpr (!PAIR) sbuf[d][p] = *reinterpret_cast<const sbv_t*>(sbrow[p] + st * SU);
     }
     if constexpr (PAIR) {

@@ -317,7 +317,9 @@ static hipError_t launch_qmvs_mt(const QmmArgs& a, hipStream_t stream) {
 bool qmvs_supported(const QmmArgs& a) {
   auto al = [](const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0; };
   // 8-byte scale loads: K a multiple of 256 keeps every scale row 8-byte aligned.
+  // Weights go through a buffer resource: their byte size must stay below 2^31.
   return a.bits == 4 && a.group_size == 64 && a.M >= 1 && a.M <= 32 && a.K % 256 == 0 &&
+         a.N * (a.K / 2) < (int64_t(1) << 31) &&
          a.ldx % 8 == 0 && al(a.x, 16) && al(a.w, 16) && al(a.scales, 8) && al(a.biases, 8);
 }
 
