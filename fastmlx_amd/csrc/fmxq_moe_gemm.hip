@@ -12,7 +12,12 @@
 // slices computes its segment's rows against 16 NTT WC columns of that expert's
 // weights with the skinny-product walk of fmxq_qmvs.hpp (whole-segment weight
 // loads through LDS, v_mfma_f32_16x16x32_bf16), so each expert's weights are read
-// once per segment whatever the number of slots.
+// once per segment whatever the number of slots.  With one K slice (every grid of
+// about two blocks per CU or more) the block runs moe_qmvw_kernel: the 4 waves
+// share the segment's x rows through an LDS stage that the block fills by DMA
+// (qmvs_walk_xlds); smaller grids run moe_qmvs_kernel, each wave loading its own
+// x rows.  Segments of one slot with 2048 <= K <= 16384 take the GEMV form
+// (moe_qmv1_kernel) instead.
 //
 // NMAT = 2 fuses the gate and up projections: both walk the same x rows and the
 // block writes h = silu(gate) * up with the op chain's bf16 roundings
