@@ -375,14 +375,18 @@ def test_gather_qmm_segments_short_and_long(gpu, oracle):
     assert rel_err(oracle.bf16_to_f32(got[~bad]), oracle.bf16_to_f32(ref)) <= TOL
 
 
-@pytest.mark.parametrize("E,lens", [
+@pytest.mark.parametrize("E,lens,K", [
     # 600 slots over 8 experts (32-slot windows): runs of 1, odd lengths, runs that end
     # just inside or just past a window; grid 32 column tiles x 28 segments
-    (8, [1, 3, 17, 31, 33, 64, 151, 300]),
+    (8, [1, 3, 17, 31, 33, 64, 151, 300], 1024),
     # 232 slots over 64 experts (16-slot windows), runs of 1 to 6; grid 16 x 80
-    (64, None),
+    (64, None, 1024),
+    # one and three 256-value steps: the odd last step after the loop, and pipeline
+    # loads past the end from the first step on
+    (8, [1, 3, 17, 31, 33, 64, 151, 300], 256),
+    (64, None, 768),
 ])
-def test_gather_qmm_shared_x_walk(gpu, oracle, E, lens):
+def test_gather_qmm_shared_x_walk(gpu, oracle, E, lens, K):
     """gather_qmm on grids of more than 512 blocks, where the MFMA walk shares each
     segment's x rows through LDS and DMAs only the rows inside the segment; K below
     2048, so every segment, one-slot ones included, takes the walk.  Explicit lhs
@@ -390,7 +394,7 @@ def test_gather_qmm_shared_x_walk(gpu, oracle, E, lens):
     from fastmlx_amd import FmxqError, ops
 
     rng = np.random.default_rng(59 + E)
-    N, K, xb = 2048, 1024, 50
+    N, xb = 2048, 50
     w, s, b = make_quant(rng, (E, N), K, 4, 64)
     x = make_x(rng, xb, 1, K)
     if lens is None:
@@ -401,7 +405,7 @@ def test_gather_qmm_shared_x_walk(gpu, oracle, E, lens):
     lhs = rng.integers(0, xb, size=S).astype(np.uint32)
     rhs[5] = E
     lhs[S // 2] = xb + 3
-    announce(f"gather_qmm shared-x walk E={E} slots={S}")
+    announce(f"gather_qmm shared-x walk E={E} slots={S} K={K}")
     y = ops.gather_qmm(to_dev(x, gpu), to_dev(w, gpu), to_dev(s, gpu), to_dev(b, gpu),
                        to_dev(rhs, gpu), to_dev(lhs, gpu), 1, True, 64, 4, False)
     torch.cuda.synchronize()
