@@ -187,13 +187,7 @@ struct MoeArgs {
   int64_t S, N, K, E, x_rows;
   uint32_t* err_flag;
   int64_t lhs_div = 1;      // x row of slot s is lhs[s], or s / lhs_div without lhs
-  int64_t min_len = 0;      // the MFMA walk skips segments shorter than this
 };
-// Longest segment the grouped products run in their GEMV form.  The GEMV form
-// builds the x pairs of every slot for each 4-row weight block, so beyond one slot
-// the MFMA walk is quicker (measured: 2-4 slot segments in the GEMV form made
-// configuration 4 at M=32 30% slower).
-constexpr int kMoeGemvMaxLen = 1;
 // Slot counts up to which the MoE products skip the sort: every slot is its own
 // segment (a sort saves weight reads only when slots share an expert).
 constexpr int64_t kMoeUnsortedMaxSlots = 16;

@@ -16,8 +16,8 @@
 // about two blocks per CU or more) the block runs moe_qmvw_kernel: the 4 waves
 // share the segment's x rows through an LDS stage that the block fills by DMA
 // (qmvs_walk_xlds); smaller grids run moe_qmvs_kernel, each wave loading its own
-// x rows.  Segments of one slot with 2048 <= K <= 16384 take the GEMV form
-// (moe_qmv1_kernel) instead.
+// x rows.  Without a segment table (few slots), rows of 2048 <= K <= 16384 take
+// the GEMV form (moe_qmv1_kernel) instead.
 //
 // NMAT = 2 fuses the gate and up projections: both walk the same x rows and the
 // block writes h = silu(gate) * up with the op chain's bf16 roundings
@@ -98,7 +98,6 @@ __global__ __launch_bounds__(256) void moe_qmvs_kernel(MoeArgs a) {
   const int c16 = lane & 15, q = lane >> 4;
   const int64_t start = a.seg ? (int64_t)a.seg[2 * sg] : sg;
   const int64_t len = a.seg ? (int64_t)a.seg[2 * sg + 1] : 1;
-  if (len < a.min_len) return;  // taken by the GEMV form
   const uint32_t e = a.rhs[start];
   const int64_t nb = (int64_t)blockIdx.x * (16 * NTT * WC) + wc * (16 * NTT);
   const bool bad_e = (int64_t)e >= a.E;
@@ -201,7 +200,6 @@ __global__ __launch_bounds__(WV * 64) __attribute__((amdgpu_waves_per_eu(MT == 1
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t start = a.seg ? (int64_t)a.seg[2 * sg] : sg;
   const int64_t len = a.seg ? (int64_t)a.seg[2 * sg + 1] : 1;
-  if (len < a.min_len) return;  // taken by the GEMV form
   const uint32_t e = a.rhs[start];
   const int64_t nb = (int64_t)blockIdx.x * (16 * NTT * WV) + wave * (16 * NTT);
   const bool bad_e = (int64_t)e >= a.E;
@@ -278,8 +276,9 @@ static hipError_t launch_wc(const MoeArgs& a, int wc, int64_t max_seg, hipStream
 }
 
 
-// Short segments (up to MM slots; every slot is its own segment on the unsorted
-// few-slot path) with K >= 2048: the decode GEMV form of the same product.  Grid
+// The few-slot path (no sort: every slot its own segment, in slot order) with
+// 2048 <= K <= 16384: the decode GEMV form of the same product.  With a segment
+// table it takes segments of up to MM slots and leaves longer ones.  Grid
 // (row blocks of RW, segments); a block is KS waves splitting K, lane l owning
 // 16-byte chunk c0 + l of its slice for all RW rows of each of the NMAT matrices.
 // Each packed word is unpacked once and dotted with the segment's x rows (v_dot2
@@ -456,24 +455,17 @@ hipError_t launch_moe_qmvs(const MoeArgs& a, int nmat, int window, int64_t max_s
   if (!moe_qmvs_supported(a.N, a.K, 4, 64) || (window != 16 && window != 32) ||
       (nmat != 1 && nmat != 2))
     return hipErrorInvalidValue;
-  // Rows of 2048..16384 values (all lanes busy with 64-chunk slices; shorter rows
-  // stay on the MFMA walk): without a segment table every slot takes the GEMV form;
-  // with one, segments of up to kMoeGemvMaxLen slots take it (a launch of its own)
-  // and the MFMA walk below skips them.
+  // Without a segment table (the few-slot path: every slot its own segment), rows
+  // of 2048..16384 values take the GEMV form (all lanes busy with 64-chunk
+  // slices).  Sorted batches run every segment, one-slot ones included, on the
+  // MFMA walk: with x shared through LDS a one-slot segment DMAs a single x row
+  // pair, and the walk measured as fast as a separate GEMV launch for those
+  // segments or faster (configuration 3 at M=16 86 -> 81 us, at M=128 248 -> 239
+  // us), without the GEMV grid's blocks for every other segment.
   MoeArgs b = a;
-  if (a.K >= 2048 && a.K <= 16384) {
-    if (!a.seg)
-      return nmat == 2 ? launch_qmv1_nmat<2, 1>(a, a.S, stream)
-                       : launch_qmv1_nmat<1, 1>(a, a.S, stream);
-    // One-slot segments are common while slots are at most 8 per expert on
-    // average (uniform routings beyond that leave few).
-    if (a.S <= 8 * a.E) {
-      const hipError_t e = nmat == 2 ? launch_qmv1_nmat<2, kMoeGemvMaxLen>(a, max_seg, stream)
-                                     : launch_qmv1_nmat<1, kMoeGemvMaxLen>(a, max_seg, stream);
-      if (e != hipSuccess) return e;
-      b.min_len = kMoeGemvMaxLen + 1;
-    }
-  }
+  if (a.K >= 2048 && a.K <= 16384 && !a.seg)
+    return nmat == 2 ? launch_qmv1_nmat<2, 1>(a, a.S, stream)
+                     : launch_qmv1_nmat<1, 1>(a, a.S, stream);
   // K slices per block; the remaining waves of the block take further column
   // groups.  One slice: the four waves walk the same K range and share the
   // segment's x rows through LDS (moe_qmvw_kernel; measured against about four
