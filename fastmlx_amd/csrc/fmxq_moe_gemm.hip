@@ -438,9 +438,10 @@ bool moe_qmvs_supported(int64_t N, int64_t K, int bits, int group_size) {
 
 // 32-slot windows (two 16-row tiles per block) once slots average 4 per expert:
 // fewer re-reads of long runs.  Below that the 16-slot form wins: its kernels hold
-// fewer registers, so two blocks share a CU (measured: configuration 3 at M=128,
-// 2.5 slots per expert, 312 -> 289 us; configuration 4 at M=256, 8 per expert,
-// 2547 -> 2948 us with 16-slot windows).
+// fewer registers, so more blocks share a CU.  Measured with the shared-x walk:
+// 16-slot windows everywhere, configuration 4 at M=256 1699 -> 1825 us and
+// configuration 3 at M=512 346 -> 365 us; 32-slot windows everywhere,
+// configuration 3 at M=16 79 -> 83 us.
 int moe_window(int64_t S, int64_t E) { return S >= 4 * E ? 32 : 16; }
 
 int64_t moe_max_segments(int64_t S, int64_t E, int window) {
