@@ -21,6 +21,7 @@ _lib = None
 
 DEQ_MLX = 0
 DEQ_FUSED = 1
+DEQ_EXACT = 2
 
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -46,7 +47,7 @@ def lib():
         L.oracle_qmm_f64.argtypes = [_p, _p, _p, _p, _p, _i64, _i64, _i64, _int, _int, _int]
         L.oracle_gather_qmm.argtypes = [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64,
                                         _i64, _int, _int, _int]
-        L.oracle_switch_glu.argtypes = [_p] * 12 + [_i64] * 5 + [_int, _int, _p, _i64]
+        L.oracle_switch_glu.argtypes = [_p] * 12 + [_i64] * 5 + [_int, _int, _p, _i64, _int, _p]
         L.oracle_qmm_cpu_fast.argtypes = [_p, _p, _p, _p, _p, _i64, _i64, _i64, _int, _int]
         L.oracle_f32_to_bf16.argtypes = [ctypes.c_float]
         L.oracle_f32_to_bf16.restype = ctypes.c_uint16
@@ -134,10 +135,12 @@ def gather_qmm(x, w, scales, biases, xrow, expert, group_size=64, bits=4, mode=D
     return y
 
 
-def switch_glu(x, inds, gate, up, down, group_size=64, bits=4, token_sel=None):
+def switch_glu(x, inds, gate, up, down, group_size=64, bits=4, token_sel=None, mode=DEQ_MLX,
+               want_hscale=False):
     """SwitchGLU over stacked quantized experts; gate/up/down are (w, s, b) triples.
 
-    x [T, D] bf16 bits, inds [T, k] int32 -> out [T or n_sel, k, D] bf16 bits."""
+    x [T, D] bf16 bits, inds [T, k] int32 -> out [T or n_sel, k, D] bf16 bits, and
+    with want_hscale also sqrt(sum_i (h_i wd_i)^2) per output (float64)."""
     T, D = x.shape
     topk = inds.shape[1]
     E, I = gate[0].shape[0], gate[0].shape[1]
@@ -145,12 +148,13 @@ def switch_glu(x, inds, gate, up, down, group_size=64, bits=4, token_sel=None):
     sel = None if token_sel is None else np.ascontiguousarray(token_sel, dtype=np.int32)
     nt = T if sel is None else sel.shape[0]
     out = np.empty((nt, topk, D), dtype=np.uint16)
+    hs = np.empty((nt, topk, D), dtype=np.float64) if want_hscale else None
     _check(lib().oracle_switch_glu(_ptr(x), _ptr(inds), _ptr(gate[0]), _ptr(gate[1]),
                                    _ptr(gate[2]), _ptr(up[0]), _ptr(up[1]), _ptr(up[2]),
                                    _ptr(down[0]), _ptr(down[1]), _ptr(down[2]), _ptr(out),
                                    T, topk, E, D, I, group_size, bits, _ptr(sel),
-                                   0 if sel is None else nt), "switch_glu")
-    return out
+                                   0 if sel is None else nt, mode, _ptr(hs)), "switch_glu")
+    return (out, hs) if want_hscale else out
 
 
 def qmm_cpu_fast(x, w, scales, biases, group_size=64, bits=4):

@@ -68,6 +68,7 @@ static inline float deq_elem(uint32_t q, uint16_t s16, uint16_t b16, int mode) {
     /* multiply(q, scales) -> bf16, then add(., biases) -> bf16 */
     return r16(r16((float)q * s) + b);
   }
+  if (mode == ORACLE_DEQ_EXACT) return (float)q * s + b; /* q*s exact in fp32 */
   return r16((float)q * s + b);
 }
 
@@ -177,16 +178,23 @@ int oracle_gather_qmm(const uint16_t *x, const uint32_t *w,
   return 0;
 }
 
-/* One quantized GEMV row against expert e of a stacked projection. */
+/* One quantized GEMV row against expert e of a stacked projection.  sq
+ * (optional) receives sqrt(sum_k (x_k w_k)^2), the scale of what one-ulp
+ * changes of the x_k move the result by. */
 static float gemv_row(const float *xv, const uint32_t *w, const uint16_t *s,
                       const uint16_t *b, int64_t e, int64_t N, int64_t n,
-                      int64_t K, int group_size, int bits, float *wf) {
+                      int64_t K, int group_size, int bits, int mode, float *wf,
+                      double *sq) {
   const int64_t wpr = K * bits / 32, gpr = K / group_size;
   const int64_t row = e * N + n;
-  deq_row(w + row * wpr, s + row * gpr, b + row * gpr, wf, K, group_size, bits,
-          ORACLE_DEQ_MLX);
+  deq_row(w + row * wpr, s + row * gpr, b + row * gpr, wf, K, group_size, bits, mode);
   float acc = 0.0f;
-  for (int64_t k = 0; k < K; ++k) acc += xv[k] * wf[k];
+  double ss = 0.0;
+  for (int64_t k = 0; k < K; ++k) {
+    acc += xv[k] * wf[k];
+    if (sq) ss += ((double)xv[k] * wf[k]) * ((double)xv[k] * wf[k]);
+  }
+  if (sq) *sq = sqrt(ss);
   return acc;
 }
 
@@ -196,7 +204,8 @@ int oracle_switch_glu(const uint16_t *x, const int32_t *inds,
                       const uint32_t *wd, const uint16_t *sd, const uint16_t *bd,
                       uint16_t *out, int64_t T, int64_t topk, int64_t E,
                       int64_t D, int64_t I, int group_size, int bits,
-                      const int32_t *token_sel, int64_t n_sel) {
+                      const int32_t *token_sel, int64_t n_sel, int mode,
+                      double *hscale) {
   if (!supported(group_size, bits, D) || !supported(group_size, bits, I)) return -1;
   const int64_t nt = token_sel ? n_sel : T;
   for (int64_t j = 0; j < nt; ++j) {
@@ -218,16 +227,19 @@ int oracle_switch_glu(const uint16_t *x, const int32_t *inds,
         float *wf = (float *)malloc(sizeof(float) * (size_t)maxk);
 #pragma omp for schedule(static)
         for (int64_t n = 0; n < I; ++n) {
-          const float g = r16(gemv_row(xv, wg, sg, bg, e, I, n, D, group_size, bits, wf));
-          const float u = r16(gemv_row(xv, wu, su, bu, e, I, n, D, group_size, bits, wf));
+          const float g = r16(gemv_row(xv, wg, sg, bg, e, I, n, D, group_size, bits, mode, wf, NULL));
+          const float u = r16(gemv_row(xv, wu, su, bu, e, I, n, D, group_size, bits, mode, wf, NULL));
           const float sig = r16(1.0f / (1.0f + expf(-g)));
           const float silu = r16(g * sig);
           hv[n] = r16(silu * u);
         }
 #pragma omp for schedule(static)
         for (int64_t n = 0; n < D; ++n) {
-          const float d = gemv_row(hv, wd, sd, bd, e, D, n, I, group_size, bits, wf);
+          double sq = 0.0;
+          const float d = gemv_row(hv, wd, sd, bd, e, D, n, I, group_size, bits, mode, wf,
+                                   hscale ? &sq : NULL);
           out[(j * topk + q) * D + n] = oracle_f32_to_bf16(d);
+          if (hscale) hscale[(j * topk + q) * D + n] = sq;
         }
         free(wf);
       }

@@ -30,8 +30,13 @@ extern "C" {
 
 /* Rounding sequences for dequantize.  DEQ_MLX is the definition the build
  * adopts: MLX's CPU composition multiply(q, scales) then add(., biases), each a
- * bf16 op that rounds its result to nearest-even.  DEQ_FUSED rounds once. */
-enum { ORACLE_DEQ_MLX = 0, ORACLE_DEQ_FUSED = 1 };
+ * bf16 op that rounds its result to nearest-even.  DEQ_FUSED rounds once.
+ * DEQ_EXACT keeps the affine value s*q + b unrounded (s*q is exact in fp32;
+ * the add rounds to fp32 only): the products an integer-domain kernel forms as
+ * s*sum(x q) + b*sum(x).  The per-element parity bounds of the tests compare
+ * each kernel against the definition it computes (EXACT or FUSED); the
+ * published 2e-2 metric is checked against DEQ_MLX. */
+enum { ORACLE_DEQ_MLX = 0, ORACLE_DEQ_FUSED = 1, ORACLE_DEQ_EXACT = 2 };
 
 float oracle_bf16_to_f32(uint16_t h);
 uint16_t oracle_f32_to_bf16(float f);
@@ -75,14 +80,18 @@ int oracle_gather_qmm(const uint16_t *x, const uint32_t *w,
  *   x [T, D], inds [T, k] -> out [T, k, D]
  *   gate/up stacked [E, I, D*bits/32], down stacked [E, D, I*bits/32].
  * token_sel (optional, length n_sel) evaluates only those tokens, writing
- * out[j, k, D] for the j-th selected token. */
+ * out[j, k, D] for the j-th selected token.  mode is the dequant definition of
+ * all three products (ORACLE_DEQ_*).  hscale (optional, [n_sel, k, D]) receives
+ * sqrt(sum_i (h_i wd_i)^2) for each output: the scale by which a one-ulp change
+ * of the bf16 intermediates h_i can move that output. */
 int oracle_switch_glu(const uint16_t *x, const int32_t *inds,
                       const uint32_t *wg, const uint16_t *sg, const uint16_t *bg,
                       const uint32_t *wu, const uint16_t *su, const uint16_t *bu,
                       const uint32_t *wd, const uint16_t *sd, const uint16_t *bd,
                       uint16_t *out, int64_t T, int64_t topk, int64_t E,
                       int64_t D, int64_t I, int group_size, int bits,
-                      const int32_t *token_sel, int64_t n_sel);
+                      const int32_t *token_sel, int64_t n_sel, int mode,
+                      double *hscale);
 
 /* The CPU baseline: the same fp32-accumulated product as oracle_qmm_f32 with
  * the dequantization factored per group (s * sum(x q) + b * sum(x)), the form a

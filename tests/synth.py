@@ -38,7 +38,7 @@ def make_quant(rng: np.random.Generator, lead: tuple, K: int, bits: int = 4, gro
     """Quantized weight triple with leading shape `lead` (e.g. (N,) or (E, N))."""
     G = K // group
     # uniform random words are uniform, independent q values in every nibble/byte
-    w = rng.integers(0, 1 << 32, size=lead + (K * bits // 32,), dtype=np.uint64).astype(np.uint32)
+    w = rng.integers(0, 1 << 32, size=lead + (K * bits // 32,), dtype=np.uint32)
     if bits == 4:
         s = rng.uniform(0.002, 0.02, size=lead + (G,)).astype(np.float32)
         s16 = f32_to_bf16(s)

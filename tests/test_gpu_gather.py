@@ -4,7 +4,8 @@ import pytest
 import torch
 
 from gpu_util import announce, to_dev, to_np
-from synth import TOL, make_quant, make_x, rel_err, topk_uniform
+import parity
+from synth import make_quant, make_x, topk_uniform
 
 pytestmark = pytest.mark.gpu
 
@@ -30,10 +31,10 @@ def test_switchglu_broadcast_form(gpu, oracle, bits):
     inds = topk_uniform(rng, T, E, k)
     announce(f"gather broadcast bits={bits}")
     got = _run(gpu, x, w, s, b, inds.reshape(-1), lhs_div=k, bits=bits)
-    ref = oracle.gather_qmm(x.reshape(T, K), w, s, b, np.repeat(np.arange(T), k),
+    ref = parity.gather_refs(x.reshape(T, K), w, s, b, np.repeat(np.arange(T), k),
                             inds.reshape(-1), 64, bits)
     assert got.shape == (T * k, 1, N)
-    assert rel_err(oracle.bf16_to_f32(got.reshape(T * k, N)), oracle.bf16_to_f32(ref)) <= TOL
+    parity.check_dense(got.reshape(T * k, N), ref, what="gather_qmm")
 
 
 def _close_ulps(a, b, ulps=2):
@@ -55,9 +56,9 @@ def test_sorted_hint_does_not_change_result(gpu, oracle):
     a = _run(gpu, x, w, s, b, rhs, sorted_indices=True)
     c = _run(gpu, x, w, s, b, rhs, sorted_indices=False)
     assert _close_ulps(a, c) <= 2.0
-    ref = oracle.gather_qmm(x.reshape(S, K), w, s, b, np.arange(S), rhs.astype(np.int32))
+    ref = parity.gather_refs(x.reshape(S, K), w, s, b, np.arange(S), rhs.astype(np.int32))
     for got in (a, c):
-        assert rel_err(oracle.bf16_to_f32(got.reshape(S, N)), oracle.bf16_to_f32(ref)) <= TOL
+        parity.check_dense(got.reshape(S, N), ref, what="gather_qmm")
 
 
 @pytest.mark.parametrize("bits,group", [(4, 64), (4, 128), (8, 32), (8, 64)])
@@ -74,9 +75,9 @@ def test_grouped_kernel_runs(gpu, oracle, bits, group, runs):
     x = make_x(rng, S, 1, K)
     announce(f"grouped gather bits={bits} group={group} runs={runs[:6]}")
     got = _run(gpu, x, w, s, b, rhs, group=group, bits=bits, sorted_indices=True)
-    ref = oracle.gather_qmm(x.reshape(S, K), w, s, b, np.arange(S), rhs.astype(np.int32), group,
+    ref = parity.gather_refs(x.reshape(S, K), w, s, b, np.arange(S), rhs.astype(np.int32), group,
                             bits)
-    assert rel_err(oracle.bf16_to_f32(got.reshape(S, N)), oracle.bf16_to_f32(ref)) <= TOL
+    parity.check_dense(got.reshape(S, N), ref, what="gather_qmm")
 
 
 def test_grouped_kernel_lhs_multirow_and_bad_ids(gpu, oracle):
@@ -95,9 +96,9 @@ def test_grouped_kernel_lhs_multirow_and_bad_ids(gpu, oracle):
     good = rhs < E
     assert np.all(got[~good] == 0)
     xrow = (lhs[:, None].astype(np.int64) * Mx + np.arange(Mx)[None, :])[good].reshape(-1)
-    ref = oracle.gather_qmm(x.reshape(xb * Mx, K), w, s, b, xrow,
+    ref = parity.gather_refs(x.reshape(xb * Mx, K), w, s, b, xrow,
                             np.repeat(rhs[good], Mx).astype(np.int32))
-    assert rel_err(oracle.bf16_to_f32(got[good].reshape(-1, N)), oracle.bf16_to_f32(ref)) <= TOL
+    parity.check_dense(got[good].reshape(-1, N), ref, what="gather_qmm")
     with pytest.raises(FmxqError):
         ops.device_error()
 
@@ -112,9 +113,9 @@ def test_explicit_lhs_and_multi_row_items(gpu, oracle):
     announce("gather explicit lhs, Mx=3")
     got = _run(gpu, x, w, s, b, rhs, lhs=lhs, group=32, bits=8)
     xrow = (lhs[:, None].astype(np.int64) * Mx + np.arange(Mx)[None, :]).reshape(-1)
-    ref = oracle.gather_qmm(x.reshape(xb * Mx, K), w, s, b, xrow,
+    ref = parity.gather_refs(x.reshape(xb * Mx, K), w, s, b, xrow,
                             np.repeat(rhs, Mx).astype(np.int32), 32, 8)
-    assert rel_err(oracle.bf16_to_f32(got.reshape(-1, N)), oracle.bf16_to_f32(ref)) <= TOL
+    parity.check_dense(got.reshape(-1, N), ref, what="gather_qmm")
 
 
 def test_out_of_range_expert_zeroes_and_flags(gpu):
@@ -146,9 +147,9 @@ def test_config3_expert_projection(gpu, oracle, M):
     inds = topk_uniform(rng, M, E, k)
     announce(f"config3 gather M={M}")
     got = _run(gpu, x, w, s, b, inds.reshape(-1), lhs_div=k)
-    ref = oracle.gather_qmm(x.reshape(M, K), w, s, b, np.repeat(np.arange(M), k),
+    ref = parity.gather_refs(x.reshape(M, K), w, s, b, np.repeat(np.arange(M), k),
                             inds.reshape(-1))
-    assert rel_err(oracle.bf16_to_f32(got.reshape(-1, N)), oracle.bf16_to_f32(ref)) <= TOL
+    parity.check_dense(got.reshape(-1, N), ref, what="gather_qmm")
 
 
 @pytest.mark.parametrize("cfg,M", [("c3", 128), ("c3", 512), ("c4", 32), ("c4", 256)])
@@ -175,6 +176,6 @@ def test_sorted_switch_projection_full_size(gpu, oracle, cfg, M):
     got = _run(gpu, x, w, s, b, rhs, lhs=lhs, sorted_indices=True).reshape(-1, N)
     sel = np.unique(np.concatenate([[0, len(rhs) - 1],
                                     rng.choice(len(rhs), size=24, replace=False)]))
-    ref = oracle.gather_qmm(x.reshape(M, K), w, s, b, lhs[sel].astype(np.int32),
+    ref = parity.gather_refs(x.reshape(M, K), w, s, b, lhs[sel].astype(np.int32),
                             rhs[sel].astype(np.int32))
-    assert rel_err(oracle.bf16_to_f32(got[sel]), oracle.bf16_to_f32(ref)) <= TOL
+    parity.check_dense(got[sel], ref, what="gather_qmm")

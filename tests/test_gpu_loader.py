@@ -13,7 +13,8 @@ import numpy as np
 import pytest
 
 from gpu_util import announce
-from synth import TOL, make_x, rel_err, topk_uniform
+import parity
+from synth import make_x, topk_uniform
 
 pytestmark = pytest.mark.gpu
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -156,6 +157,6 @@ def test_int4_checkpoint_to_switch_glu(gpu, oracle):
                          trip["gate_proj"], trip["up_proj"], trip["down_proj"], 64, 4)
     got = y.to_numpy().reshape(T, k, D)
     np_trip = {p: tuple(a.to_numpy() for a in trip[p]) for p in trip}
-    want = oracle.switch_glu(x, inds, np_trip["gate_proj"], np_trip["up_proj"],
-                             np_trip["down_proj"], 64, 4)
-    assert rel_err(oracle.bf16_to_f32(got), oracle.bf16_to_f32(want)) <= TOL
+    sref = parity.SwitchRef(x, inds, np_trip["gate_proj"], np_trip["up_proj"],
+                            np_trip["down_proj"], 64, 4)
+    parity.check_switch(got, sref)

@@ -198,6 +198,142 @@ def test_cpu_fast_baseline_within_tolerance(oracle):
         assert rel_err(fast, ref) < 2e-2
 
 
+def test_exact_mode_closed_forms(oracle):
+    """DEQ_EXACT keeps s*q + b unrounded.  With s = 2^-4 and b = -0.5 every value
+    (q - 8)/16 is a bf16, so all three definitions agree and one-hot x returns it;
+    with s = 1 + 2^-7 the exact value 3.0390625 is not a bf16, and one-hot x
+    returns it exactly, where the rounding modes return 3.03125 / 3.046875."""
+    K = 64
+    q = (np.arange(K, dtype=np.uint32) % 16).reshape(1, K)
+    w = pack(q, 4)
+    s = np.array([[0x3D80]], dtype=np.uint16)   # 2^-4
+    b = np.array([[0xBF00]], dtype=np.uint16)   # -0.5
+    want = (q[0].astype(np.float64) - 8.0) / 16.0
+    for k in (0, 7, 8, 63):
+        x = np.zeros((1, K), dtype=np.uint16)
+        x[0, k] = 0x3F80
+        for mode in (oracle.DEQ_MLX, oracle.DEQ_FUSED, oracle.DEQ_EXACT):
+            assert oracle.qmm_f64(x, w, s, b, 64, 4, mode=mode)[0, 0] == want[k]
+    w3 = pack(np.array([[3] + [0] * 63], dtype=np.uint32), 4)
+    s3 = np.array([[0x3F81]], dtype=np.uint16)
+    b3 = np.array([[0x3C80]], dtype=np.uint16)
+    x = np.zeros((1, K), dtype=np.uint16)
+    x[0, 0] = 0x3F80
+    got = {m: oracle.qmm_f64(x, w3, s3, b3, 64, 4, mode=m)[0, 0]
+           for m in (oracle.DEQ_MLX, oracle.DEQ_FUSED, oracle.DEQ_EXACT)}
+    assert got[oracle.DEQ_EXACT] == 3.0390625
+    assert got[oracle.DEQ_FUSED] == 3.03125 and got[oracle.DEQ_MLX] == 3.046875
+
+
+def test_exact_mode_is_the_factored_sum(oracle):
+    """EXACT equals s * sum(x q) + b * sum(x) per group in fp64 (the form the
+    integer-domain kernels compute), far tighter than the bf16-weight modes do."""
+    rng = np.random.default_rng(44)
+    N, K = 24, 1024
+    w, s, b = make_quant(rng, (N,), K, 4, 64)
+    x = make_x(rng, 2, K)
+    xf = oracle.bf16_to_f32(x).astype(np.float64).reshape(2, K // 64, 64)
+    qf = unpack(w, 4).astype(np.float64).reshape(N, K // 64, 64)
+    sf = oracle.bf16_to_f32(s).astype(np.float64)
+    bf = oracle.bf16_to_f32(b).astype(np.float64)
+    ref = (np.einsum("mgk,ngk->mng", xf, qf) * sf[None] + xf.sum(-1)[:, None, :] * bf[None]).sum(-1)
+    ex = oracle.qmm_f64(x, w, s, b, 64, 4, mode=oracle.DEQ_EXACT)
+    assert np.max(np.abs(ex - ref)) <= 1e-5 * np.max(np.abs(ref))
+    mlx = oracle.qmm_f64(x, w, s, b, 64, 4, mode=oracle.DEQ_MLX)
+    assert np.max(np.abs(mlx - ref)) > 100 * np.max(np.abs(ex - ref))
+
+
+def _slip_cases(rng, N, K, G):
+    """Planted kernel mistakes, each confined to one 64-value group of one row."""
+    n, g = int(rng.integers(N)), int(rng.integers(1, G - 1))
+    yield "dropped group", lambda s, b: (s.__setitem__((n, g), 0), b.__setitem__((n, g), 0))
+    yield "neighbour's scale", lambda s, b: s.__setitem__((n, g), s[n, g + 1])
+    yield "bias left out", lambda s, b: b.__setitem__((n, g), 0)
+
+
+@pytest.mark.parametrize("K", [4096, 14336])
+def test_parity_bound_accepts_kernels_and_catches_group_slips(oracle, K):
+    """The per-element bound of the GPU tests (tests/parity.py) passes a result
+    computed with either kernel definition, and fails every planted one-group slip."""
+    import parity
+
+    rng = np.random.default_rng(K)
+    N, M = 48, 2
+    w, s, b = make_quant(rng, (N,), K, 4, 64)
+    x = make_x(rng, M, K)
+    ref = parity.DenseRef(x, w, s, b, 64, 4)
+    for mode in (oracle.DEQ_EXACT, oracle.DEQ_FUSED):
+        good = oracle.qmm(x, w, s, b, 64, 4, mode=mode)
+        parity.check_dense(good, ref, what=f"mode {mode}")
+    for name, plant in _slip_cases(rng, N, K, K // 64):
+        s2, b2 = s.copy(), b.copy()
+        plant(s2, b2)
+        bad = oracle.qmm(x, w, s2, b2, 64, 4, mode=oracle.DEQ_EXACT)
+        with pytest.raises(AssertionError, match="per-element"):
+            parity.check_dense(bad, ref, what=name)
+
+
+def test_max_abs_rel_metric_misses_a_typical_group_drop(oracle):
+    """Why the per-element bound exists: on 14336-deep rows, dropping the group of
+    median contribution in one row stays inside max-abs-rel 2e-2 but fails the
+    bound by a wide margin."""
+    import parity
+
+    rng = np.random.default_rng(3)
+    N, M, K = 512, 2, 14336
+    w, s, b = make_quant(rng, (N,), K, 4, 64)
+    x = make_x(rng, M, K)
+    ref = parity.DenseRef(x, w, s, b, 64, 4)
+    n = 7
+    contrib = []
+    for g in range(K // 64):  # row n's per-group contribution to y[0, n]
+        s1, b1 = s.copy(), b.copy()
+        s1[n, g] = b1[n, g] = 0
+        contrib.append(ref.exact[0, n] - oracle.qmm_f64(x[:1], w[n:n + 1], s1[n:n + 1],
+                                                         b1[n:n + 1], 64, 4,
+                                                         mode=oracle.DEQ_EXACT)[0, 0])
+    g = int(np.argsort(np.abs(contrib))[len(contrib) // 2])
+    s2, b2 = s.copy(), b.copy()
+    s2[n, g] = b2[n, g] = 0
+    bad = oracle.qmm(x, w, s2, b2, 64, 4, mode=oracle.DEQ_EXACT)
+    assert rel_err(oracle.bf16_to_f32(bad), ref.mlx) <= 2e-2
+    with pytest.raises(AssertionError, match="per-element"):
+        parity.check_dense(bad, ref)
+
+
+def test_switch_bound_catches_a_down_group_slip(oracle):
+    """SwitchGLU outputs at configuration 3's expert shape (2048 -> 512 -> 2048):
+    both kernel definitions pass the per-slot bound, and so does the MLX-definition
+    output, whose intermediates flip far more often than a kernel's.  Dropping the
+    down group of median contribution from one row fails the bound."""
+    import parity
+
+    rng = np.random.default_rng(46)
+    T, k, E, D, I = 3, 2, 8, 2048, 512
+    gate = make_quant(rng, (E, I), D, 4, 64)
+    up = make_quant(rng, (E, I), D, 4, 64)
+    down = make_quant(rng, (E, D), I, 4, 64)
+    x = make_x(rng, T, D)
+    inds = np.array([[5, 1], [6, 2], [4, 7]], dtype=np.int32)
+    sref = parity.SwitchRef(x, inds, gate, up, down)
+    for mode in (oracle.DEQ_EXACT, oracle.DEQ_FUSED, oracle.DEQ_MLX):
+        got = oracle.switch_glu(x, inds, gate, up, down, mode=mode)
+        parity.check_switch(got, sref, what=f"mode {mode}")
+    e, n = 5, 11  # token 0's first expert, output row 11
+    base = parity.f64(oracle.switch_glu(x, inds, gate, up, down, mode=oracle.DEQ_EXACT,
+                                        token_sel=np.array([0])))[0, 0, n]
+
+    def dropped(g):
+        sd, bd = down[1].copy(), down[2].copy()
+        sd[e, n, g] = bd[e, n, g] = 0
+        return oracle.switch_glu(x, inds, gate, up, (down[0], sd, bd), mode=oracle.DEQ_EXACT)
+
+    contrib = [abs(parity.f64(dropped(g))[0, 0, n] - base) for g in range(I // 64)]
+    g = int(np.argsort(contrib)[len(contrib) // 2])
+    with pytest.raises(AssertionError, match="per-element"):
+        parity.check_switch(dropped(g), sref)
+
+
 # ---------------------------------------------------------------- gather / SwitchGLU
 
 def test_gather_single_expert_reduces_to_qmm(oracle):
