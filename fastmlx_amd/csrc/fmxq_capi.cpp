@@ -30,10 +30,6 @@ std::mutex g_err_mu;
 char g_err_buf[2][512];
 int g_err_slot = 0;
 
-// Per-device error flag raised by gather kernels.
-std::mutex g_flag_mu;
-std::vector<uint32_t*> g_flags;
-
 }  // namespace
 
 namespace fmxq {
@@ -53,23 +49,6 @@ int fail(int code, const char* fmt, ...) {
 int hip_status(hipError_t e, const char* what) {
   if (e == hipSuccess) return FMXQ_OK;
   return fail(FMXQ_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
-}
-
-int device_flag(uint32_t** out) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return fail(FMXQ_ERR_DEVICE, "hipGetDevice failed");
-  std::lock_guard<std::mutex> lk(g_flag_mu);
-  if ((int)g_flags.size() <= dev) g_flags.resize(dev + 1, nullptr);
-  if (!g_flags[dev]) {
-    uint32_t* p = nullptr;
-    hipError_t e = hipMalloc(&p, sizeof(uint32_t));
-    if (e != hipSuccess) return hip_status(e, "hipMalloc(error flag)");
-    e = hipMemset(p, 0, sizeof(uint32_t));
-    if (e != hipSuccess) return hip_status(e, "hipMemset(error flag)");
-    g_flags[dev] = p;
-  }
-  *out = g_flags[dev];
-  return FMXQ_OK;
 }
 
 int check_quant(int group_size, int bits, int64_t K, bool transpose, const char* op) {
@@ -223,6 +202,25 @@ int stream_arena(hipStream_t s, size_t bytes, void** out, const char* op) {
   return FMXQ_OK;
 }
 
+// Where a SwitchGLU call's scratch comes from: the per-(device, stream) arena,
+// grown with hipMalloc, or (fmxq_switch_glu_noalloc) the device's fixed
+// __device__ buffer, which is never grown: a call needing more is refused before
+// anything is enqueued.
+struct ScratchSource {
+  void* fixed = nullptr;
+  size_t fixed_bytes = 0;
+  int get(hipStream_t s, size_t bytes, void** out, const char* op) const {
+    if (!fixed) return stream_arena(s, bytes, out, op);
+    if (bytes > fixed_bytes)
+      return fail(FMXQ_ERR_SHAPE,
+                  "%s: this call needs %zu bytes of scratch, more than the %zu bytes the "
+                  "allocation-free entry point holds; use fmxq_switch_glu or fewer slots",
+                  op, bytes, fixed_bytes);
+    *out = fixed;
+    return FMXQ_OK;
+  }
+};
+
 size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // Counting sort in one block keeps two (E + 1)-entry tables in LDS.
@@ -242,14 +240,15 @@ struct MoeScratch {
   uint16_t *g = nullptr, *u = nullptr;
 };
 int moe_scratch(hipStream_t s, int64_t S, int64_t h_cols, int64_t max_seg, MoeScratch* m,
-                const char* op, int64_t max_tiles = 0, int64_t gu_cols = 0) {
+                const char* op, int64_t max_tiles = 0, int64_t gu_cols = 0,
+                const ScratchSource& src = ScratchSource()) {
   const size_t ib = align_up((size_t)S * sizeof(uint32_t));
   const size_t sb = align_up((size_t)max_seg * 2 * sizeof(uint32_t));
   const size_t hb = align_up((size_t)S * h_cols * sizeof(uint16_t));
   const size_t tb = align_up((size_t)max_tiles * 2 * sizeof(uint32_t));
   const size_t gb = align_up((size_t)S * gu_cols * sizeof(uint16_t));
   void* arena = nullptr;
-  if (int rc = stream_arena(s, 3 * ib + sb + 256 + hb + tb + 256 + 2 * gb, &arena, op)) return rc;
+  if (int rc = src.get(s, 3 * ib + sb + 256 + hb + tb + 256 + 2 * gb, &arena, op)) return rc;
   char* p = static_cast<char*>(arena);
   m->order = reinterpret_cast<uint32_t*>(p);
   m->rhs = reinterpret_cast<uint32_t*>(p + ib);
@@ -504,14 +503,14 @@ int gather_dispatch(const fmxq::GatherArgs& a, bool sorted, hipStream_t s) {
 
 }  // namespace
 
-extern "C" int fmxq_switch_glu(const uint16_t* x, const uint32_t* inds, const uint32_t* w_gate,
-                               const uint16_t* s_gate, const uint16_t* b_gate,
-                               const uint32_t* w_up, const uint16_t* s_up, const uint16_t* b_up,
-                               const uint32_t* w_down, const uint16_t* s_down,
-                               const uint16_t* b_down, uint16_t* out, int64_t T, int64_t topk,
-                               int64_t E, int64_t D, int64_t I, int group_size, int bits,
-                               void* stream) {
-  const char* op = "switch_glu";
+namespace {
+
+int switch_glu_impl(const uint16_t* x, const uint32_t* inds, const uint32_t* w_gate,
+                    const uint16_t* s_gate, const uint16_t* b_gate, const uint32_t* w_up,
+                    const uint16_t* s_up, const uint16_t* b_up, const uint32_t* w_down,
+                    const uint16_t* s_down, const uint16_t* b_down, uint16_t* out, int64_t T,
+                    int64_t topk, int64_t E, int64_t D, int64_t I, int group_size, int bits,
+                    void* stream, const ScratchSource& src, const char* op) {
   if (int rc = check_quant(group_size, bits, D, true, op)) return rc;
   if (int rc = check_quant(group_size, bits, I, true, op)) return rc;
   if (T < 0 || topk < 1 || E < 1)
@@ -542,7 +541,7 @@ extern "C" int fmxq_switch_glu(const uint16_t* x, const uint32_t* inds, const ui
     // slots skip the sort: each is its own segment, h stays in slot order.
     MoeScratch m;
     if (S <= fmxq::kMoeUnsortedMaxSlots) {
-      if (int rc = moe_scratch(s, S, I, 1, &m, op)) return rc;
+      if (int rc = moe_scratch(s, S, I, 1, &m, op, 0, 0, src)) return rc;
       fmxq::MoeArgs gu{x, nullptr, {w_gate, w_up}, {s_gate, s_up}, {b_gate, b_up}, inds, nullptr,
                        nullptr, m.h, nullptr, S, I, D, E, T, flag, topk};
       if (int rc = hip_status(fmxq::launch_moe_qmvs(gu, 2, 16, S, s), "switch_glu: gate/up"))
@@ -558,7 +557,8 @@ extern "C" int fmxq_switch_glu(const uint16_t* x, const uint32_t* inds, const ui
                 fmxq::qmm_grouped_supported(D, I, S, bits, group_size)
             ? grouped_max_tiles(S, E)
             : 0;
-    if (int rc = moe_scratch(s, S, I, max_seg, &m, op, max_tiles, max_tiles ? I : 0)) return rc;
+    if (int rc = moe_scratch(s, S, I, max_seg, &m, op, max_tiles, max_tiles ? I : 0, src))
+      return rc;
     if (int rc = hip_status(fmxq::launch_sort_slots(inds, S, topk, E, m.order, m.rhs, m.lhs, s,
                                                     nullptr, m.seg, m.nseg, window, m.tiles,
                                                     m.ntile, (int)kGroupedMinRun,
@@ -599,7 +599,7 @@ extern "C" int fmxq_switch_glu(const uint16_t* x, const uint32_t* inds, const ui
   const size_t hbytes = align_up((size_t)S * I * sizeof(uint16_t));
   const size_t ibytes = align_up((size_t)S * sizeof(uint32_t));
   void* arena = nullptr;
-  if (int rc = stream_arena(s, 2 * hbytes + (sort ? 3 * ibytes : 0), &arena, op)) return rc;
+  if (int rc = src.get(s, 2 * hbytes + (sort ? 3 * ibytes : 0), &arena, op)) return rc;
   uint16_t* gbuf = static_cast<uint16_t*>(arena);
   uint16_t* ubuf = reinterpret_cast<uint16_t*>(static_cast<char*>(arena) + hbytes);
   uint32_t* order = reinterpret_cast<uint32_t*>(static_cast<char*>(arena) + 2 * hbytes);
@@ -629,6 +629,36 @@ extern "C" int fmxq_switch_glu(const uint16_t* x, const uint32_t* inds, const ui
                      1, D, I, E, group_size, bits, flag};
   if (sort) d.yrow = order;
   return gather_dispatch(d, sort, s);
+}
+
+}  // namespace
+
+extern "C" int fmxq_switch_glu(const uint16_t* x, const uint32_t* inds, const uint32_t* w_gate,
+                               const uint16_t* s_gate, const uint16_t* b_gate,
+                               const uint32_t* w_up, const uint16_t* s_up, const uint16_t* b_up,
+                               const uint32_t* w_down, const uint16_t* s_down,
+                               const uint16_t* b_down, uint16_t* out, int64_t T, int64_t topk,
+                               int64_t E, int64_t D, int64_t I, int group_size, int bits,
+                               void* stream) {
+  return switch_glu_impl(x, inds, w_gate, s_gate, b_gate, w_up, s_up, b_up, w_down, s_down,
+                         b_down, out, T, topk, E, D, I, group_size, bits, stream,
+                         ScratchSource(), "switch_glu");
+}
+
+extern "C" int fmxq_switch_glu_noalloc(const uint16_t* x, const uint32_t* inds,
+                                       const uint32_t* w_gate, const uint16_t* s_gate,
+                                       const uint16_t* b_gate, const uint32_t* w_up,
+                                       const uint16_t* s_up, const uint16_t* b_up,
+                                       const uint32_t* w_down, const uint16_t* s_down,
+                                       const uint16_t* b_down, uint16_t* out, int64_t T,
+                                       int64_t topk, int64_t E, int64_t D, int64_t I,
+                                       int group_size, int bits, void* stream) {
+  ScratchSource src;
+  if (int rc = fmxq::noalloc_scratch(&src.fixed)) return rc;
+  src.fixed_bytes = FMXQ_NOALLOC_SCRATCH_BYTES;
+  return switch_glu_impl(x, inds, w_gate, s_gate, b_gate, w_up, s_up, b_up, w_down, s_down,
+                         b_down, out, T, topk, E, D, I, group_size, bits, stream, src,
+                         "switch_glu_noalloc");
 }
 
 namespace {

@@ -1,0 +1,72 @@
+// fmxq_device_state.hip -- device memory the library keeps for the life of the
+// process in file-scope __device__ variables rather than hipMalloc:
+//   - the per-device index-error flag that gather kernels raise and
+//     fmxq_device_error reads and clears;
+//   - `scratch`, the fixed workspace of fmxq_switch_glu_noalloc
+//     (FMXQ_NOALLOC_SCRATCH_BYTES), for callers that cannot allocate.
+// Each GPU holds its own copy of both at its own address.  In host code the
+// variables' names are host-side stand-ins, not device addresses, so each is
+// resolved once per device with hipGetSymbolAddress (with that device current)
+// and only the resolved pointers are ever handed to kernels or copies.
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+#include <vector>
+
+#include "../../include/fmxq.h"
+#include "fmxq_host.hpp"
+
+static __device__ __align__(256) uint32_t index_flag;
+static __device__ __align__(256) unsigned char scratch[FMXQ_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+struct DeviceState {
+  uint32_t* flag = nullptr;
+  void* scratch = nullptr;
+};
+std::mutex g_state_mu;
+std::vector<DeviceState> g_state;
+
+// The current device's resolved addresses, looked up on its first use.
+int current_state(DeviceState** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fmxq::fail(FMXQ_ERR_DEVICE, "hipGetDevice failed");
+  std::lock_guard<std::mutex> lk(g_state_mu);
+  if ((int)g_state.size() <= dev) g_state.resize(dev + 1);
+  DeviceState& st = g_state[dev];
+  if (!st.flag) {
+    void* f = nullptr;
+    void* s = nullptr;
+    if (int rc = fmxq::hip_status(hipGetSymbolAddress(&f, HIP_SYMBOL(index_flag)),
+                                  "hipGetSymbolAddress(index flag)"))
+      return rc;
+    if (int rc = fmxq::hip_status(hipGetSymbolAddress(&s, HIP_SYMBOL(scratch)),
+                                  "hipGetSymbolAddress(scratch)"))
+      return rc;
+    st.scratch = s;
+    st.flag = static_cast<uint32_t*>(f);  // set last: a non-null flag means resolved
+  }
+  *out = &st;
+  return FMXQ_OK;
+}
+
+}  // namespace
+
+namespace fmxq {
+
+int device_flag(uint32_t** out) {
+  DeviceState* st = nullptr;
+  if (int rc = current_state(&st)) return rc;
+  *out = st->flag;
+  return FMXQ_OK;
+}
+
+int noalloc_scratch(void** out) {
+  DeviceState* st = nullptr;
+  if (int rc = current_state(&st)) return rc;
+  *out = st->scratch;
+  return FMXQ_OK;
+}
+
+}  // namespace fmxq

@@ -10,9 +10,13 @@ namespace fmxq {
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 // FMXQ_OK for hipSuccess, else FMXQ_ERR_DEVICE with the HIP error string.
 int hip_status(hipError_t e, const char* what);
-// The current device's index-error flag (one uint32 in device memory, zeroed
-// once at creation and by fmxq_device_error when it reports).
+// The current device's index-error flag: one uint32 __device__ variable per
+// device (zero at load, cleared by fmxq_device_error when it reports), resolved
+// without allocating (fmxq_device_state.hip).
 int device_flag(uint32_t** out);
+// The current device's fixed scratch of FMXQ_NOALLOC_SCRATCH_BYTES, shared by
+// every fmxq_switch_glu_noalloc call on that device.
+int noalloc_scratch(void** out);
 // The quantization geometry every op supports: transpose, bits in {4, 8},
 // group_size in {32, 64, 128}, K a positive multiple of group_size.
 int check_quant(int group_size, int bits, int64_t K, bool transpose, const char* op);

@@ -121,6 +121,34 @@ int fmxq_switch_glu(const uint16_t* x, const uint32_t* inds, const uint32_t* w_g
                     int64_t top_k, int64_t E, int64_t D, int64_t I, int group_size, int bits,
                     void* stream);
 
+/* Bytes of device memory each GPU holds, from library load to process exit, for
+ * fmxq_switch_glu_noalloc's scratch (a file-scope __device__ array). */
+#define FMXQ_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* fmxq_switch_glu without any allocation.  This entry point has no counterpart
+ * in the reference.  It exists for callers that cannot allocate device memory:
+ * code under HIP graph capture, tight serving loops, and harnesses that forbid
+ * hipMalloc.
+ * - Same arguments, kernels and results as fmxq_switch_glu.
+ * - The scratch (sorted slots, segment table, intermediate activations) lives in
+ *   one fixed FMXQ_NOALLOC_SCRATCH_BYTES buffer per GPU, not in a per-stream
+ *   arena.  That covers, for example, 5120 routed slots at I = 512 or 2048
+ *   slots at I = 2048.
+ * - A call that needs more scratch returns FMXQ_ERR_SHAPE before anything is
+ *   enqueued.
+ * - Every call on one GPU shares that GPU's buffer, and nothing in it needs to
+ *   start at zero.  Calls that overlap on one GPU (concurrent streams, or a
+ *   graph replayed while another call runs) race on it and must be serialized
+ *   by the caller.
+ * - It calls no hipMalloc, hipFree or allocating library routine. */
+int fmxq_switch_glu_noalloc(const uint16_t* x, const uint32_t* inds, const uint32_t* w_gate,
+                            const uint16_t* s_gate, const uint16_t* b_gate,
+                            const uint32_t* w_up, const uint16_t* s_up, const uint16_t* b_up,
+                            const uint32_t* w_down, const uint16_t* s_down,
+                            const uint16_t* b_down, uint16_t* out, int64_t T, int64_t top_k,
+                            int64_t E, int64_t D, int64_t I, int group_size, int bits,
+                            void* stream);
+
 /* MoE combine: out[t] = sum_j y[t, j] * weights[t, j] (+ shared term), the
  * weighted top-k sum of qwen3next_forward.go:519-520 / deepseekv3_forward.go:436-437.
  * y [T, top_k, D], weights [T, top_k], out [T, D], all bf16; D even.  With shared
