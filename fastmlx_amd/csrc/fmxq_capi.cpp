@@ -316,8 +316,12 @@ int qmm_common(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
   const bool skinny = M > fmxq::kQmvMaxM && M <= fmxq::kSkinnyMaxM && fmxq::qmvs_supported(a) &&
                       !(M <= 8 && N < 2048 && fmxq::qmv_supported(a));
   if (skinny) return hip_status(fmxq::launch_qmvs(a, s), op);
-  if (fmxq::qmv_supported(a)) return hip_status(fmxq::launch_qmv(a, s), op);
-  if (M <= fmxq::kSkinnyMaxM && fmxq::qmv_mfma_supported(a))
+  // 5 <= M <= 32 shapes qmvs does not take (int8, other group sizes) run on the
+  // prefill GEMM's 64-row tile; M <= 4 stays on the dot2 GEMV.
+  const bool small_gemm = M > fmxq::kQmvMaxM && M <= fmxq::kSkinnyMaxM &&
+                          !fmxq::qmvs_supported(a) && fmxq::qmm_prefill_supported(a);
+  if (!small_gemm && fmxq::qmv_supported(a)) return hip_status(fmxq::launch_qmv(a, s), op);
+  if (!small_gemm && M <= fmxq::kSkinnyMaxM && fmxq::qmv_mfma_supported(a))
     return hip_status(fmxq::launch_qmv_mfma(a, s), op);
   if (fmxq::qmm_prefill_supported(a)) {
     int cus = 0;

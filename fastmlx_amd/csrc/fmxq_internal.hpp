@@ -108,9 +108,12 @@ struct QmmPlan {
 QmmPlan qmm_plan(int64_t M, int64_t N, int64_t K);
 hipError_t launch_qmm(const QmmArgs& a, hipStream_t stream);
 
-// Prefill GEMM for M > kPrefillMinM (fmxq_qmm_prefill.hip): K a multiple of 64,
-// x rows 16-byte aligned, 4- or 8-bit with group_size >= 32, no split-K.
+// Prefill GEMM (fmxq_qmm_prefill.hip): K a multiple of 64, x rows 16-byte
+// aligned, 4- or 8-bit with group_size >= 32.  It takes every M > 32, and the
+// 5 <= M <= 32 shapes the int4 skinny kernel (qmvs) does not.
 constexpr int64_t kPrefillMinM = 32;
+// Most K parts a split tile is cut into (each writes fp32 partials).
+constexpr int kPrefillMaxSplits = 16;
 bool qmm_prefill_supported(const QmmArgs& a);
 // K split of the tiles of a part-full last wave on `cus` compute units (one block
 // per CU): splits 1 means none; otherwise ws_floats of workspace for split_tail.

@@ -1,4 +1,5 @@
-// fmxq_qmm_prefill.hip -- MFMA GEMM for quantized_matmul at verify and prefill sizes (M > 32).
+// fmxq_qmm_prefill.hip -- MFMA GEMM for quantized_matmul at verify and prefill sizes (M > 32,
+// and the 5 <= M <= 32 shapes no GEMV kernel takes).
 //
 // Replaces the GEMM side of mlx_quantized_matmul (mlxgo/binding_cgo.go:636-643)
 // for x [M, K] with M = batch * seq rows (prefill at batch_generator.go:258).
@@ -488,6 +489,10 @@ struct TileShape {
   int bm, bn;
 };
 TileShape prefill_tile(const QmmArgs& a) {
+  // Up to 64 rows of x (verify batches, and the skinny shapes no GEMV kernel
+  // takes): 64 x 128 tiles.  Fewer rows of a tile are wasted on rows past M, and
+  // split tiles write a quarter of the fp32 partials of a 128 x 256 tile.
+  if (a.M <= 64) return {64, 128};
   if (a.bits == 8 || a.M > 128) return {256, 128};
   return {128, 256};
 }
@@ -504,13 +509,14 @@ PrefillPlan qmm_prefill_plan(const QmmArgs& a, int cus) {
   const int64_t tail = tiles < cus ? tiles : tiles % cus;
   int splits = 1;
   if (tail > 0 && tail * 2 <= cus)
-    while (splits < 8 && tail * splits * 2 <= cus && nk / (splits * 2) >= 8) splits *= 2;
+    while (splits < kPrefillMaxSplits && tail * splits * 2 <= cus && nk / (splits * 2) >= 8)
+      splits *= 2;
   if (splits == 1) return {1, 0, 0};
   return {splits, tail, tail * splits * ts.bm * ts.bn};
 }
 
 bool qmm_prefill_supported(const QmmArgs& a) {
-  return a.M > kPrefillMinM && a.K % kStepK == 0 && a.K > 0 && a.ldx % 8 == 0 &&
+  return a.M >= 1 && a.K % kStepK == 0 && a.K > 0 && a.ldx % 8 == 0 &&
          (a.bits == 4 || a.bits == 8) && a.group_size >= 32 &&
          (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
          (reinterpret_cast<uintptr_t>(a.w) & 15) == 0 &&
@@ -542,9 +548,13 @@ hipError_t launch_qmm_grouped(const QmmArgs& a, int64_t max_tiles, hipStream_t s
 
 hipError_t launch_qmm_prefill(const QmmArgs& a, hipStream_t stream) {
   if (!qmm_prefill_supported(a)) return hipErrorInvalidValue;
-  if (a.splits > 1 && (!a.ws || a.split_tail < 1 || a.splits > 8)) return hipErrorInvalidValue;
-  // 128 x 256 tiles for M <= 128 (4-bit; the 8-bit form of that tile spills).
+  if (a.splits > 1 && (!a.ws || a.split_tail < 1 || a.splits > kPrefillMaxSplits))
+    return hipErrorInvalidValue;
+  // 128 x 256 tiles for 64 < M <= 128 (4-bit; the 8-bit form of that tile spills).
   const TileShape ts = prefill_tile(a);
+  if (ts.bm == 64)
+    return a.bits == 8 ? launch_tile<8, 64, 128, 2, 4>(a, stream)
+                       : launch_tile<4, 64, 128, 2, 4>(a, stream);
   if (a.bits == 8) return launch_tile<8, 256, 128, 4, 2>(a, stream);
   if (ts.bm == 256) return launch_tile<4, 256, 128, 4, 2>(a, stream);
   return launch_tile<4, 128, 256, 2, 4>(a, stream);

@@ -53,10 +53,10 @@ struct SkStage {
 };
 
 // NT: 32-row tiles per wave.  RL: accumulator registers carrying rows < M
-// (4 per 8 rows).  KS: waves of a block splitting K.
-template <int BITS, int NT, int RL, int KS>
-__global__ __launch_bounds__(256) void qmv_mfma_kernel(QmmArgs a) {
-  constexpr int RG = 4 / KS;
+// (4 per 8 rows).  KS: waves of a block splitting K; WAVES: waves per block.
+template <int BITS, int NT, int RL, int KS, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void qmv_mfma_kernel(QmmArgs a) {
+  constexpr int RG = WAVES / KS;
   constexpr int U = BITS == 4 ? 64 : 32;            // values per unit (two 16-byte halves)
   constexpr float OFF = BITS == 4 ? 128.f : 2176.f;  // exponent-trick offset per value
   constexpr float XSCALE = BITS == 4 ? 1.f : 0.5f;   // int8 A duplicates each x value
@@ -186,20 +186,30 @@ bool qmv_mfma_supported(const QmmArgs& a) {
   return a.group_size >= 32 && a.K % 32 == 0;
 }
 
-template <int BITS, int NT, int RL, int KS>
+template <int BITS, int NT, int RL, int KS, int WAVES>
 static hipError_t launch_sk(const QmmArgs& a, hipStream_t stream) {
-  constexpr int rows_per_block = (4 / KS) * 32 * NT;
+  constexpr int rows_per_block = (WAVES / KS) * 32 * NT;
   const unsigned blocks = (unsigned)((a.N + rows_per_block - 1) / rows_per_block);
-  qmv_mfma_kernel<BITS, NT, RL, KS><<<blocks, 256, 0, stream>>>(a);
+  qmv_mfma_kernel<BITS, NT, RL, KS, WAVES><<<blocks, WAVES * 64, 0, stream>>>(a);
   return hipGetLastError();
 }
 
 template <int BITS, int RL>
 static hipError_t launch_sk_rl(const QmmArgs& a, hipStream_t stream) {
-  // Split K over the 4 waves of a block unless there are rows enough to give each
-  // wave its own 32-row tile across at least ~1024 waves.
-  if (a.N >= 32 * 4 * 1024 / 4) return launch_sk<BITS, 1, RL, 1>(a, stream);
-  return launch_sk<BITS, 1, RL, 4>(a, stream);
+  // Split K over the waves of a block until the launch has about 2048 waves
+  // (eight per CU), keeping at least eight units per wave: a 32-row tile per
+  // wave is too few waves for narrow outputs (4096 rows: 128 tiles).
+  const int64_t tiles = (a.N + 31) / 32;
+  const int64_t units = a.K / (BITS == 4 ? 64 : 32);
+  int ks = 1;
+  while (ks < 16 && tiles * ks < 2048 && units / (2 * ks) >= 8) ks *= 2;
+  switch (ks) {
+    case 1: return launch_sk<BITS, 1, RL, 1, 4>(a, stream);
+    case 2: return launch_sk<BITS, 1, RL, 2, 4>(a, stream);
+    case 4: return launch_sk<BITS, 1, RL, 4, 4>(a, stream);
+    case 8: return launch_sk<BITS, 1, RL, 8, 8>(a, stream);
+    default: return launch_sk<BITS, 1, RL, 16, 16>(a, stream);
+  }
 }
 
 hipError_t launch_qmv_mfma(const QmmArgs& a, hipStream_t stream) {
