@@ -290,8 +290,9 @@ def dense_point(torch, ops, mats, M, N, K, bits, gen, dev):
 
 def moe_points(torch, ops, gen, dev, cpu):
     """Configs 3 and 4: one MoE layer per step.
-    - The step is SwitchGLU over the routed experts, then the weighted top-k
-      combine; configuration 4 adds its shared expert.
+    - The step is switch_glu_combine: SwitchGLU over the routed experts and the
+      weighted top-k combine in one call (up to 16 slots, the down projection and
+      the combine are one kernel).  Configuration 4 adds its shared expert.
     - Each step of a replayed graph has its own routing, and for configuration 4
       its own shared expert, so consecutive steps do not find their experts in
       the 256 MB last-level cache."""
@@ -311,13 +312,11 @@ def moe_points(torch, ops, gen, dev, cpu):
             inds = torch.argsort(torch.rand(M, E, device=dev, generator=gen), dim=1)[:, :k]
             w = torch.softmax(torch.randn(M, k, device=dev, generator=gen), dim=1)
             routes.append((inds.to(torch.int32).contiguous(), w.to(torch.bfloat16)))
-        ys = torch.empty(M, k, D, device=dev, dtype=torch.bfloat16)
         yo = torch.empty(M, D, device=dev, dtype=torch.bfloat16)
 
         def fn():
             for inds, w in routes:
-                ops.switch_glu(x, inds, gate, up, down, GROUP, 4, out=ys)
-                ops.moe_combine(ys, w, out=yo)
+                ops.switch_glu_combine(x, inds, gate, up, down, w, out=yo)
         g = capture(torch, fn)
         per = time_graph(torch, g, 10, 2) / R
         hit = sum(int(torch.unique(r[0]).numel()) for r in routes) / R
@@ -359,15 +358,13 @@ def moe_points(torch, ops, gen, dev, cpu):
             w = w / w.sum(dim=1, keepdim=True)
             routes.append((inds.to(torch.int32).contiguous(), w.to(torch.bfloat16)))
         zero = torch.zeros(M, 1, device=dev, dtype=torch.int32)
-        ys = torch.empty(M, k, D, device=dev, dtype=torch.bfloat16)
         ysh = torch.empty(M, 1, D, device=dev, dtype=torch.bfloat16)
         yo = torch.empty(M, D, device=dev, dtype=torch.bfloat16)
 
         def fn():
             for (inds, w), (sg, su, sd) in zip(routes, shared):
-                ops.switch_glu(x, inds, gate, up, down, GROUP, 4, out=ys)
                 ops.switch_glu(x, zero, sg, su, sd, GROUP, 4, out=ysh)
-                ops.moe_combine(ys, w, shared=ysh.view(M, D), out=yo)
+                ops.switch_glu_combine(x, inds, gate, up, down, w, shared=ysh.view(M, D), out=yo)
         g = capture(torch, fn)
         per = time_graph(torch, g, 6, 1) / R
         hit = sum(int(torch.unique(r[0]).numel()) for r in routes) / R

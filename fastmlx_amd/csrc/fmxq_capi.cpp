@@ -16,6 +16,7 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "../../include/fmxq.h"
@@ -179,14 +180,16 @@ int device_cus(int* out) {
 // Per-(device, stream) scratch for the SwitchGLU intermediates, grown on demand
 // (never while the stream is being captured) and, like the split-K workspace,
 // never freed while a captured graph may still point at it.
+// Slot 1 holds the expert rows between a SwitchGLU and its combine
+// (fmxq_switch_glu_combine), while slot 0 serves the SwitchGLU itself.
 std::mutex g_arena_mu;
-std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> g_arena;
+std::map<std::tuple<int, hipStream_t, int>, std::pair<void*, size_t>> g_arena;
 
-int stream_arena(hipStream_t s, size_t bytes, void** out, const char* op) {
+int stream_arena(hipStream_t s, size_t bytes, void** out, const char* op, int slot = 0) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return fail(FMXQ_ERR_DEVICE, "hipGetDevice failed");
   std::lock_guard<std::mutex> lk(g_arena_mu);
-  auto& a = g_arena[{dev, s}];
+  auto& a = g_arena[{dev, s, slot}];
   if (a.second < bytes) {
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(s, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
@@ -663,6 +666,61 @@ extern "C" int fmxq_switch_glu_noalloc(const uint16_t* x, const uint32_t* inds,
   return switch_glu_impl(x, inds, w_gate, s_gate, b_gate, w_up, s_up, b_up, w_down, s_down,
                          b_down, out, T, topk, E, D, I, group_size, bits, stream, src,
                          "switch_glu_noalloc");
+}
+
+extern "C" int fmxq_switch_glu_combine(
+    const uint16_t* x, const uint32_t* inds, const uint32_t* w_gate, const uint16_t* s_gate,
+    const uint16_t* b_gate, const uint32_t* w_up, const uint16_t* s_up, const uint16_t* b_up,
+    const uint32_t* w_down, const uint16_t* s_down, const uint16_t* b_down,
+    const uint16_t* weights, const uint16_t* shared, const uint16_t* shared_gate, uint16_t* out,
+    int64_t T, int64_t topk, int64_t E, int64_t D, int64_t I, int group_size, int bits,
+    void* stream) {
+  const char* op = "switch_glu_combine";
+  if (int rc = check_quant(group_size, bits, D, true, op)) return rc;
+  if (int rc = check_quant(group_size, bits, I, true, op)) return rc;
+  if (T < 0 || topk < 1 || E < 1 || D % 2 != 0)
+    return fail(FMXQ_ERR_SHAPE, "%s: need T >= 0, top_k >= 1, E >= 1 and an even D", op);
+  const int64_t S = T * topk;
+  if (S == 0) return FMXQ_OK;
+  if (!x || !inds || !w_gate || !s_gate || !b_gate || !w_up || !s_up || !b_up || !w_down ||
+      !s_down || !b_down || !weights || !out)
+    return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: null operand", op);
+  if (shared_gate && !shared)
+    return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: shared_gate without shared", op);
+  if (!aligned16(x) || !aligned16(w_gate) || !aligned16(w_up) || !aligned16(w_down))
+    return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: x and weights must be 16-byte aligned", op);
+  if (S > 0x7fffffffLL) return fail(FMXQ_ERR_SHAPE, "%s: too many slots", op);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // Decode-sized batches: gate and up into h (no sort), then one kernel for the
+  // down projection and the combine.
+  if (S <= fmxq::kMoeUnsortedMaxSlots &&
+      fmxq::moe_down_combine_supported(T, topk, D, I, bits, group_size) &&
+      fmxq::moe_qmvs_supported(I, D, bits, group_size) && aligned16(s_gate) &&
+      aligned16(b_gate) && aligned16(s_up) && aligned16(b_up)) {
+    uint32_t* flag = nullptr;
+    if (int rc = device_flag(&flag)) return rc;
+    MoeScratch m;
+    if (int rc = moe_scratch(s, S, I, 1, &m, op)) return rc;
+    fmxq::MoeArgs gu{x, nullptr, {w_gate, w_up}, {s_gate, s_up}, {b_gate, b_up}, inds, nullptr,
+                     nullptr, m.h, nullptr, S, I, D, E, T, flag, topk};
+    if (int rc = hip_status(fmxq::launch_moe_qmvs(gu, 2, 16, S, s), "switch_glu_combine: gate/up"))
+      return rc;
+    return hip_status(fmxq::launch_moe_down_combine(m.h, inds, w_down, s_down, b_down, weights,
+                                                    shared, shared_gate, out, T, topk, E, D, I,
+                                                    flag, s),
+                      "switch_glu_combine: down/combine");
+  }
+  // Otherwise the two calls in sequence, the expert rows in the arena's slot 1.
+  void* rows = nullptr;
+  if (int rc = stream_arena(s, align_up((size_t)S * D * sizeof(uint16_t)), &rows, op, 1))
+    return rc;
+  if (int rc = switch_glu_impl(x, inds, w_gate, s_gate, b_gate, w_up, s_up, b_up, w_down, s_down,
+                               b_down, static_cast<uint16_t*>(rows), T, topk, E, D, I, group_size,
+                               bits, stream, ScratchSource(), op))
+    return rc;
+  return hip_status(fmxq::launch_moe_combine(static_cast<const uint16_t*>(rows), weights, shared,
+                                             shared_gate, out, T, topk, D, s),
+                    "switch_glu_combine: combine");
 }
 
 namespace {

@@ -200,6 +200,16 @@ int64_t moe_max_segments(int64_t S, int64_t E, int window);
 hipError_t launch_moe_qmvs(const MoeArgs& a, int nmat, int window, int64_t max_seg,
                            hipStream_t stream);
 
+// Few-slot down projection fused with the top-k combine (one block per row
+// tile and token, one wave per slot): out [T, D] from the h rows [T k, I].
+bool moe_down_combine_supported(int64_t T, int64_t k, int64_t D, int64_t I, int bits,
+                                int group_size);
+hipError_t launch_moe_down_combine(const uint16_t* h, const uint32_t* inds, const uint32_t* w,
+                                   const uint16_t* s, const uint16_t* b, const uint16_t* weights,
+                                   const uint16_t* shared, const uint16_t* sgate, uint16_t* out,
+                                   int64_t T, int64_t k, int64_t E, int64_t D, int64_t I,
+                                   uint32_t* err_flag, hipStream_t stream);
+
 // Grouped MFMA gather for expert-sorted batches (int4 group_size >= 64, int8 >= 32).
 constexpr int64_t kGroupedMinSlots = 32;
 bool gather_mfma_supported(const GatherArgs& a);

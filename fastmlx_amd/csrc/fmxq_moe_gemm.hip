@@ -428,7 +428,135 @@ static hipError_t launch_qmv1_nmat(const MoeArgs& a, int64_t segs, hipStream_t s
   return launch_qmv1_ks<NMAT, 8, MM>(a, segs, stream);
 }
 
+// moe_down_combine_kernel: the few-slot down projection fused with the top-k
+// combine (qwen3next_forward.go:519-524, deepseekv3_forward.go:436-440).  Block
+// (row tile of RW output columns, token t), one wave per slot j of the token:
+//   - wave j computes e_j = bf16(h[t k + j] . deq(Wd[e_j])^T) for the tile's rows
+//     in the GEMV form of moe_qmv1_kernel (lane -> 16-byte chunk of 32 values,
+//     LPR lanes per row, RW / (64 / LPR) passes of 64 / LPR rows), then
+//     p_j = bf16(e_j * w[t, j]) into LDS;
+//   - the first RW threads sum p_j in slot order in fp32 and finish as
+//     moe_combine_kernel: bf16, then the shared term (sigmoid-gated or plain).
+// A bad expert id gives p_j = 0 and raises the flag, as the unfused path's zero
+// row does.
+struct DownCombineArgs {
+  const uint16_t* h;         // [T k, I] silu(gate) * up rows in slot order
+  const uint32_t* inds;      // [T k] expert of each slot
+  const uint32_t* w;         // [E, D, I/8]
+  const uint16_t* s;         // [E, D, I/64]
+  const uint16_t* b;
+  const uint16_t* weights;   // [T, k] bf16 router weights
+  const uint16_t* shared;    // [T, D] or null
+  const uint16_t* sgate;     // [T] or null
+  uint16_t* out;             // [T, D]
+  int64_t T, k, E, D, I;
+  uint32_t* err_flag;
+};
+
+template <int RW, int LPR, int CPL>
+__global__ __launch_bounds__(1024) void moe_down_combine_kernel(DownCombineArgs a) {
+  constexpr int RPP = 64 / LPR, PASSES = RW / RPP;
+  static_assert(RW % RPP == 0, "rows per pass");
+  __shared__ float part[16][RW];
+  const int lane = threadIdx.x & 63;
+  const int j = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t t = blockIdx.y, n0 = (int64_t)blockIdx.x * RW;
+  const int64_t slot = t * a.k + j;
+  const uint32_t e = a.inds[slot];
+  const bool bad = (int64_t)e >= a.E;
+  const int rsub = lane / LPR, cl = lane % LPR;
+  const int64_t wpr = a.I / 8, gpr = a.I / 64;
+  float res[PASSES];
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) res[p] = 0.f;
+  if (!bad) {
+    u32x4 wv[PASSES][CPL];
+    uint32_t sv[PASSES][CPL], bv[PASSES][CPL];
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      int64_t n = n0 + p * RPP + rsub;
+      n = n < a.D ? n : a.D - 1;  // rows past D re-read row D-1; not stored
+      const int64_t row = (int64_t)e * a.D + n;
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const int c = cl + LPR * i;
+        wv[p][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.w + row * wpr) + c);
+        sv[p][i] = a.s[row * gpr + (c >> 1)];
+        bv[p][i] = a.b[row * gpr + (c >> 1)];
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    XChunk<4> xc[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) xc[i].load(a.h + slot * a.I, (int64_t)(cl + LPR * i) * 32);
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p)
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const float sc = bf16_bits_to_f32(sv[p][i]);
+        const float bo = __builtin_fmaf(-magic_offset<4>(), sc, bf16_bits_to_f32(bv[p][i]));
+        res[p] += __builtin_fmaf(sc, chunk_dot<4>(wv[p][i], xc[i]), bo * xc[i].sum);
+      }
+  }
+  // Row totals: butterfly within each group of LPR lanes.
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p)
+#pragma unroll
+    for (int off = LPR / 2; off >= 1; off >>= 1) res[p] += __shfl_xor(res[p], off, 64);
+  if (cl == 0) {
+    const float wj = bf16_bits_to_f32(a.weights[slot]);
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) part[j][p * RPP + rsub] = bad ? 0.f : r16(r16(res[p]) * wj);
+  }
+  if (bad && lane == 0) atomicOr(a.err_flag, 1u);
+  __syncthreads();
+  if (threadIdx.x < RW) {
+    const int r = threadIdx.x;
+    const int64_t n = n0 + r;
+    if (n < a.D) {
+      float acc = 0.f;
+      for (int jj = 0; jj < a.k; ++jj) acc += part[jj][r];
+      acc = r16(acc);
+      if (a.shared) {
+        float sh = bf16_bits_to_f32(a.shared[t * a.D + n]);
+        if (a.sgate) sh = r16(r16(1.f / (1.f + __expf(-bf16_bits_to_f32(a.sgate[t])))) * sh);
+        acc = r16(acc + sh);
+      }
+      a.out[t * a.D + n] = (uint16_t)f32_to_bf16_rne(acc);
+    }
+  }
+}
+
+template <int RW, int LPR, int CPL>
+static hipError_t launch_down_combine_cfg(const DownCombineArgs& a, hipStream_t stream) {
+  dim3 grid((unsigned)((a.D + RW - 1) / RW), (unsigned)a.T);
+  moe_down_combine_kernel<RW, LPR, CPL><<<grid, (unsigned)(a.k * 64), 0, stream>>>(a);
+  return hipGetLastError();
+}
+
 }  // namespace
+
+bool moe_down_combine_supported(int64_t T, int64_t k, int64_t D, int64_t I, int bits,
+                                int group_size) {
+  return bits == 4 && group_size == 64 && k >= 1 && k <= 16 && T >= 1 && T <= 65535 &&
+         D >= 1 && (I == 512 || I == 1024 || I == 2048 || I == 4096 || I == 8192);
+}
+
+hipError_t launch_moe_down_combine(const uint16_t* h, const uint32_t* inds, const uint32_t* w,
+                                   const uint16_t* s, const uint16_t* b, const uint16_t* weights,
+                                   const uint16_t* shared, const uint16_t* sgate, uint16_t* out,
+                                   int64_t T, int64_t k, int64_t E, int64_t D, int64_t I,
+                                   uint32_t* err_flag, hipStream_t stream) {
+  if (!moe_down_combine_supported(T, k, D, I, 4, 64)) return hipErrorInvalidValue;
+  const DownCombineArgs a{h, inds, w, s, b, weights, shared, sgate, out, T, k, E, D, I, err_flag};
+  switch (I) {
+    case 512: return launch_down_combine_cfg<16, 16, 1>(a, stream);
+    case 1024: return launch_down_combine_cfg<16, 32, 1>(a, stream);
+    case 2048: return launch_down_combine_cfg<8, 64, 1>(a, stream);
+    case 4096: return launch_down_combine_cfg<8, 64, 2>(a, stream);
+    default: return launch_down_combine_cfg<8, 64, 4>(a, stream);
+  }
+}
 
 // One expert's weights go through a buffer resource: below 2^31 bytes.
 bool moe_qmvs_supported(int64_t N, int64_t K, int bits, int group_size) {

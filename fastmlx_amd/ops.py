@@ -111,6 +111,29 @@ def switch_glu(x, inds, gate, up, down, group_size: int = 64, bits: int = 4, out
     return out
 
 
+def switch_glu_combine(x, inds, gate, up, down, weights, shared=None, shared_gate=None,
+                       group_size: int = 64, bits: int = 4, out=None):
+    """One MoE layer's routed part: switch_glu then moe_combine in one call.
+
+    weights [T, top_k] bf16; shared [T, D] (optional) is added, sigmoid-gated by
+    shared_gate [T] when given.  Returns [T, D] bf16."""
+    T, D = x.shape
+    topk = inds.shape[-1]
+    E, I = gate[0].shape[0], gate[0].shape[1]
+    if out is None:
+        out = torch.empty(T, D, dtype=torch.bfloat16, device=x.device)
+    p = [_dev(x, "x", _BF16_LIKE), _dev(inds, "inds", _U32_LIKE)]
+    for name, (w, s, b) in (("gate", gate), ("up", up), ("down", down)):
+        p += [_dev(w, f"{name}.w", _U32_LIKE), _dev(s, f"{name}.scales", _BF16_LIKE),
+              _dev(b, f"{name}.biases", _BF16_LIKE)]
+    sp = None if shared is None else _dev(shared, "shared", _BF16_LIKE)
+    gp = None if shared_gate is None else _dev(shared_gate, "shared_gate", _BF16_LIKE)
+    check(load().fmxq_switch_glu_combine(*p, _dev(weights, "weights", _BF16_LIKE), sp, gp,
+                                         _dev(out, "out", _BF16_LIKE), T, topk, E, D, I,
+                                         group_size, bits, _stream(x)))
+    return out
+
+
 def moe_combine(y, weights, shared=None, shared_gate=None, out=None):
     """sum_j y[:, j] * weights[:, j] (+ shared, optionally sigmoid-gated); y [T, k, D]."""
     T, topk, D = y.shape

@@ -121,6 +121,22 @@ int fmxq_switch_glu(const uint16_t* x, const uint32_t* inds, const uint32_t* w_g
                     int64_t top_k, int64_t E, int64_t D, int64_t I, int group_size, int bits,
                     void* stream);
 
+/* One MoE layer's routed part: fmxq_switch_glu followed by fmxq_moe_combine,
+ * out [T, D] = sum_j bf16(y[t, j] * weights[t, j]) (+ the shared term), the
+ * expert outputs y never leaving the chip for decode-sized batches
+ * (qwen3next_forward.go:510-525, deepseekv3_forward.go:427-442).  Arguments are
+ * those of the two calls; the op chain and its bf16 roundings are theirs.  Up to
+ * 16 routing slots (int4, group 64) the down projection and the weighted sum run
+ * as one kernel; otherwise the expert rows go through a per-stream buffer. */
+int fmxq_switch_glu_combine(const uint16_t* x, const uint32_t* inds, const uint32_t* w_gate,
+                            const uint16_t* s_gate, const uint16_t* b_gate,
+                            const uint32_t* w_up, const uint16_t* s_up, const uint16_t* b_up,
+                            const uint32_t* w_down, const uint16_t* s_down,
+                            const uint16_t* b_down, const uint16_t* weights,
+                            const uint16_t* shared, const uint16_t* shared_gate, uint16_t* out,
+                            int64_t T, int64_t top_k, int64_t E, int64_t D, int64_t I,
+                            int group_size, int bits, void* stream);
+
 /* Bytes of device memory each GPU holds, from library load to process exit, for
  * fmxq_switch_glu_noalloc's scratch (a file-scope __device__ array). */
 #define FMXQ_NOALLOC_SCRATCH_BYTES (32u << 20)

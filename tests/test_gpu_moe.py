@@ -513,3 +513,91 @@ def test_gather_qmm_long_runs_bad_row_and_id(gpu, oracle):
     ref = parity.gather_refs(x.reshape(xb, K), w, s, b, lhs[~bad].astype(np.int32),
                              rhs[~bad].astype(np.int32))
     parity.check_dense(got[~bad], ref, what="gather_qmm")
+
+
+# --- switch_glu_combine: one MoE layer's routed part in one call ---
+
+@pytest.mark.parametrize("cfg,M", [("c3", 1), ("c3", 16), ("c4", 1), ("c4", 2), ("c4", 32)])
+def test_switch_glu_combine_configs(gpu, oracle, cfg, M):
+    """The fused layer at configurations 3 and 4.
+    - Up to 16 slots run the down projection and the weighted sum as one kernel.
+    - More slots run SwitchGLU, then the combine.
+    - Configuration 4 adds its shared expert (computed by a one-expert SwitchGLU).
+    Checked element by element against the oracle's op chain."""
+    from fastmlx_amd import ops
+
+    (gate, up, down), dstack, shared, dshared = _layer_weights(gpu, cfg)
+    rng = np.random.default_rng(900 + M)
+    E, D = gate[0].shape[0], down[0].shape[1]
+    if cfg == "c3":
+        k = 10
+        inds = topk_uniform(rng, M, E, k)
+        wts = rng.dirichlet(np.ones(k), size=M).astype(np.float32)
+    else:
+        k = 8
+        inds = topk_zipf(rng, M, E, k)
+        g = 1 / (1 + np.exp(-rng.standard_normal((M, k))))
+        wts = (g / g.sum(1, keepdims=True)).astype(np.float32)
+    x = make_x(rng, M, D)
+    w16 = oracle.f32_to_bf16(wts)
+    dx = to_dev(x, gpu)
+    announce(f"switch_glu_combine {cfg} M={M} slots={M * k}")
+    ysh = None
+    if dshared is not None:
+        ysh = ops.switch_glu(dx, torch.zeros(M, 1, dtype=torch.int32, device=gpu), *dshared, 64, 4)
+    out = ops.switch_glu_combine(dx, to_dev(inds.astype(np.uint32), gpu), *dstack, to_dev(w16, gpu),
+                                 None if ysh is None else ysh.view(M, D))
+    torch.cuda.synchronize()
+    got = to_np(out)
+    sel = np.unique(np.concatenate([[0, M - 1], rng.choice(M, size=min(M, 3), replace=False)]))
+    sref = parity.SwitchRef(x, inds, gate, up, down, token_sel=sel, fused=False)
+    near = sref.refs[0]
+    sh = None
+    if shared is not None:
+        zi = np.zeros((M, 1), dtype=np.int32)
+        ssref = parity.SwitchRef(x, zi, *shared, token_sel=sel, fused=False)
+        parity.check_switch(to_np(ysh)[sel], ssref, what="shared expert")
+        snear = parity.nearest(to_np(ysh)[sel], ssref)
+        sh = (snear[:, 0], parity.switch_bound(snear, snear, ssref.hscale)[:, 0])
+    parity.combine_check(got[sel], near, parity.switch_bound(near, near, sref.hscale), w16[sel],
+                         shared=sh, what=f"switch_glu_combine {cfg} M={M}")
+
+
+@pytest.mark.parametrize("I,gated", [(512, True), (1024, False), (4096, True)])
+def test_switch_glu_combine_few_slots_shapes(gpu, oracle, I, gated):
+    """The fused down/combine kernel's other row forms (32 lanes per 1024-value row,
+    two chunks per lane at 4096), a sigmoid-gated shared term, and a bad expert id
+    (its slot contributes zero and the flag is raised)."""
+    from fastmlx_amd import FmxqError, ops
+
+    rng = np.random.default_rng(I + gated)
+    E, D, T, k = 9, 512, 2, 6
+    gate, up, down = _stack(rng, E, D, I)
+    x = make_x(rng, T, D)
+    inds = topk_uniform(rng, T, E, k)
+    inds[1, 4] = E + 3
+    wts = oracle.f32_to_bf16(rng.dirichlet(np.ones(k), size=T).astype(np.float32))
+    sh = make_x(rng, T, D)
+    sg = make_x(rng, T) if gated else None
+    dev = lambda t: to_dev(t, gpu)
+    announce(f"switch_glu_combine I={I} gated={gated}")
+    out = ops.switch_glu_combine(dev(x), dev(inds.astype(np.uint32)), tuple(map(dev, gate)),
+                                 tuple(map(dev, up)), tuple(map(dev, down)), dev(wts), dev(sh),
+                                 None if sg is None else dev(sg))
+    torch.cuda.synchronize()
+    got = to_np(out)
+    with pytest.raises(FmxqError):
+        ops.device_error()
+    safe = np.where(inds >= E, 0, inds)
+    sref = parity.SwitchRef(x, safe, gate, up, down, fused=False)
+    near = sref.refs[0].copy()
+    near[1, 4] = 0.0  # the bad slot's row is zero
+    allow = parity.switch_bound(near, near, sref.hscale)
+    allow[1, 4] = 0.0
+    shv = oracle.bf16_to_f32(sh).astype(np.float64)
+    if gated:
+        r16 = lambda v: oracle.bf16_to_f32(oracle.f32_to_bf16(np.asarray(v, np.float32))).astype(np.float64)
+        gt = r16(1 / (1 + np.exp(-oracle.bf16_to_f32(sg).astype(np.float64))))
+        shv = r16(gt[:, None] * shv)
+    parity.combine_check(got, near, allow, wts, shared=(shv, 2.0 ** -8 * np.abs(shv)),
+                         what=f"switch_glu_combine I={I}")
