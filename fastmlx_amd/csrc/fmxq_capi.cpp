@@ -23,29 +23,7 @@
 #include "fmxq_host.hpp"
 #include "fmxq_internal.hpp"
 
-namespace {
-
-std::mutex g_err_mu;
-// The returned pointer must survive until the next failure; keep two buffers
-// and alternate so a reader of the previous message is not overwritten mid-read.
-char g_err_buf[2][512];
-int g_err_slot = 0;
-
-}  // namespace
-
 namespace fmxq {
-
-int fail(int code, const char* fmt, ...) {
-  char tmp[512];
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(tmp, sizeof(tmp), fmt, ap);
-  va_end(ap);
-  std::lock_guard<std::mutex> lk(g_err_mu);
-  g_err_slot ^= 1;
-  std::snprintf(g_err_buf[g_err_slot], sizeof(g_err_buf[0]), "%s", tmp);
-  return code;
-}
 
 int hip_status(hipError_t e, const char* what) {
   if (e == hipSuccess) return FMXQ_OK;
@@ -350,11 +328,6 @@ int qmm_common(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
 extern "C" {
 
 int fmxq_version(void) { return 100; }
-
-const char* fmxq_last_error(void) {
-  std::lock_guard<std::mutex> lk(g_err_mu);
-  return g_err_buf[g_err_slot];
-}
 
 int fmxq_dequantize(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                     uint16_t* out, int64_t rows, int64_t K, int group_size, int bits,

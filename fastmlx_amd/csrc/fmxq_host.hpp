@@ -4,10 +4,10 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "fmxq_status.hpp"
+
 namespace fmxq {
 
-// Records a message for fmxq_last_error() and returns code.
-int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 // FMXQ_OK for hipSuccess, else FMXQ_ERR_DEVICE with the HIP error string.
 int hip_status(hipError_t e, const char* what);
 // The current device's index-error flag: one uint32 __device__ variable per

@@ -87,6 +87,14 @@ def test_parse_json_forms():
                    '["w"]', '{"w":3}', '{"w":{"dtype":"F32","shape":[-1],"data_offsets":[0,4]}}']:
         with pytest.raises(MLXError):
             loader.parse_safetensors_header(_blob(hj_bad, 4))
+    # A name or metadata string that decodes a NUL is refused: the C-ABI hands
+    # names out as C strings, so such a tensor could not be looked up again (Go
+    # strings can hold it; this is the one form the reference accepts and this
+    # parser does not).
+    for hj_nul in ['{"a\\u0000b":{"dtype":"F32","shape":[1],"data_offsets":[0,4]}}',
+                   '{"__metadata__":{"k\\u0000":"v"}}', '{"__metadata__":{"k":"\\u0000"}}']:
+        with pytest.raises(MLXError, match="NUL"):
+            loader.parse_safetensors_header(_blob(hj_nul, 4))
     # a null entry decodes to the zero record, whose empty dtype is unknown
     with pytest.raises(MLXError):
         loader.parse_safetensors_header(_blob('{"w":null}', 0))
