@@ -292,7 +292,20 @@ int qmm_common(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
     return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: x and w must be 16-byte aligned", op);
   fmxq::QmmArgs a{x, w, scales, biases, bias, y, M, N, K, K, N, group_size, bits};
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // M <= 4: dot2 GEMV.  5 <= M <= 32: qmvs, except that narrow outputs (N < 2048)
+  // 9 <= M <= 64 (int4 group 64): qmvw, x shared through LDS and K split over
+  // blocks; at M <= 16 only for wide outputs or long rows, where it beats qmvs.
+  if (M > 8 && M <= fmxq::kQmvwMaxM && (M > 16 || N >= 8192 || K >= 8192) &&
+      fmxq::qmvw_supported(a)) {
+    int cus = 0;
+    if (int rc = device_cus(&cus)) return rc;
+    const fmxq::QmvwPlan qp = fmxq::qmvw_plan(a, cus);
+    if (qp.parts > 1) {
+      if (int rc = prefill_workspace(s, qp.ws_floats, &a.ws)) return rc;
+      a.splits = qp.parts;
+    }
+    return hip_status(fmxq::launch_qmvw(a, qp, s), op);
+  }
+  // M <= 4: dot2 GEMV.  Other M <= 32: qmvs, except that narrow outputs (N < 2048)
   // at M <= 8 stay on the dot2 GEMV, which is quicker there.
   const bool skinny = M > fmxq::kQmvMaxM && M <= fmxq::kSkinnyMaxM && fmxq::qmvs_supported(a) &&
                       !(M <= 8 && N < 2048 && fmxq::qmv_supported(a));

@@ -97,6 +97,16 @@ bool qmvs_supported(const QmmArgs& a);
 hipError_t launch_qmvs(const QmmArgs& a, hipStream_t stream);
 bool qmv_mfma_supported(const QmmArgs& a);
 hipError_t launch_qmv_mfma(const QmmArgs& a, hipStream_t stream);
+// int4 group-64 product for M <= kQmvwMaxM with x shared through LDS by the waves
+// of a block and K split over blocks (fmxq_skinny.hip, qmvw_kernel).
+constexpr int kQmvwMaxM = 64;
+struct QmvwPlan {
+  int mt, ntt, wv, parts, d;
+  int64_t ws_floats;  // fp32 partials when parts > 1
+};
+bool qmvw_supported(const QmmArgs& a);
+QmvwPlan qmvw_plan(const QmmArgs& a, int cus);
+hipError_t launch_qmvw(const QmmArgs& a, const QmvwPlan& p, hipStream_t stream);
 
 // MFMA GEMM for larger M.  qmm_plan() reports the split-K factor and the
 // workspace launch_qmm() will need for these sizes.

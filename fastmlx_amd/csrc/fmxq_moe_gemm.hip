@@ -244,12 +244,12 @@ __global__ __launch_bounds__(WV * 64) __attribute__((amdgpu_waves_per_eu(MT == 1
       uint32_t xo[8 / WV];
       x_offsets(xo, 8 / WV);
       qmvs_walk_xlds<1, MT, NTT, NMAT, WV>(xs0, xs1, stage[wave], xres, xo, wave, len, w, sc, bi,
-                                           nb, a.N, a.K, acc);
+                                           nb, a.N, a.K, 0, a.K / 256, acc);
     } else {
       uint32_t xo[8 * MT / WV];
       x_offsets(xo, 8 * MT / WV);
       qmvs_walk_xlds<MT, MT, NTT, NMAT, WV>(xs0, xs1, stage[wave], xres, xo, wave, len, w, sc, bi,
-                                            nb, a.N, a.K, acc);
+                                            nb, a.N, a.K, 0, a.K / 256, acc);
     }
   }
   store_segment<MT, NTT, NMAT>(a, start, len, bad_e, nb, acc);

@@ -232,8 +232,8 @@ __device__ __forceinline__ void qmvs_wait_vm_lgkm0() {
 constexpr int kXStageRow = 512;
 
 // The walk of qmvs_slice for a block of WV (4 or 8) waves that all walk the same
-// K range (each wave its own 16 NTT columns from nb), with the segment's x rows
-// shared through LDS instead of loaded by every wave.
+// steps [s0, s1) of 256 K values (each wave its own 16 NTT columns from nb), with
+// the segment's x rows shared through LDS instead of loaded by every wave.
 //
 // x stage (xs0 / xs1, one step each, alternating): 16 MTW rows of kXStageRow
 // bytes; 16-byte chunk c of row r sits at position c ^ (r & 15), so the 16 rows
@@ -260,7 +260,7 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
                                                const uint32_t* const (&w)[NMAT],
                                                const uint16_t* const (&sc)[NMAT],
                                                const uint16_t* const (&bi)[NMAT], int64_t nb,
-                                               int64_t N, int64_t K,
+                                               int64_t N, int64_t K, int64_t s0, int64_t s1,
                                                f32x4 (&acc)[NMAT][MT][NTT]) {
   constexpr int SU = 4;
   using G = QmvsGeom<NTT, SU>;
@@ -271,10 +271,10 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
   typedef uint32_t sbv_t __attribute__((ext_vector_type(SPL / 2)));
   const int lane = threadIdx.x & 63;
   const int c16 = lane & 15, q = lane >> 4;
-  const int64_t wpr = K / 8, gpr = K / 64, nst = K / (SU * 64);
+  const int64_t wpr = K / 8, gpr = K / 64;
 
-  // Weights through buffer resources as in qmvs_slice: steps past the end load
-  // zeros without a memory access.
+  // Weights through buffer resources as in qmvs_slice: steps past s1 load zeros
+  // without a memory access.
   uint32_t wq[NI];
   int wo[NI];
 #pragma unroll
@@ -299,8 +299,9 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
     }
   // Scale/bias loads.  16-row tiles (NTT = 1): one 8-byte load per lane covers two
   // steps (lane -> row l % 16, kind (l / 16) & 1 (scales, biases), step l / 32 of
-  // the pair: that step's 4 groups), issued in even steps for the next pair; a
-  // lane's step is clamped to the last, so an odd step count reads no further.
+  // the pair: that step's 4 groups), issued in even steps (counted from s0) for
+  // the next pair; a lane's step is clamped to s1 - 1, so an odd step count reads
+  // no further.
   // 32-row tiles: one load per lane and step as in qmvs_slice.
   constexpr bool PAIR = ROWS == 16;
   typedef uint32_t spv_t __attribute__((ext_vector_type(2)));
@@ -326,8 +327,8 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
   // Weights (and, without PAIR, the step's scales) of step st into set d; with PAIR
   // and pair set, the scales of steps st and st + 1 after the weights.
   auto load_w = [&](int d, int64_t st, bool pair) {
-    const bool past = st >= nst;
-    st = past ? nst - 1 : st;
+    const bool past = st >= s1;
+    st = past ? s1 - 1 : st;
 #pragma unroll
     for (int p = 0; p < NMAT; ++p) {
 #pragma unroll
@@ -341,7 +342,7 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
     if constexpr (PAIR) {
       if (pair) {
         int64_t sl = st + ph;
-        sl = sl < nst ? sl : nst - 1;
+        sl = sl < s1 ? sl : s1 - 1;
 #pragma unroll
         for (int p = 0; p < NMAT; ++p) sp[p] = *reinterpret_cast<const spv_t*>(sbrow[p] + sl * SU);
       }
@@ -356,11 +357,11 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
   };
   const bf16x8 ones = as_bf16x8(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
 
-  if (nst <= 0) return;
-  issue_x(0, xs0);
+  if (s1 <= s0) return;
+  issue_x(s0, xs0);
   __builtin_amdgcn_sched_barrier(0);
-  load_w(0, 0, true);
-  load_w(1, 1, false);
+  load_w(0, s0, true);
+  load_w(1, s0 + 1, false);
   __builtin_amdgcn_sched_barrier(0);
   // One step; e (0 or 1) picks the stage and register set.  Pairs of steps run
   // unconditionally inside the loop and an odd last step after it, so every path
@@ -424,7 +425,7 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
           }
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (stp + 1 < nst) issue_x(stp + 1, xn);
+    if (stp + 1 < s1) issue_x(stp + 1, xn);
     __builtin_amdgcn_sched_barrier(0);
     load_w(e, stp + 2, e == 0);
     __builtin_amdgcn_sched_barrier(0);
@@ -469,14 +470,177 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
       }
     }
   };
-  int64_t st = 0;
+  int64_t st = s0;
 #pragma clang loop unroll(disable)
-  for (; st + 1 < nst; st += 2) {
+  for (; st + 1 < s1; st += 2) {
     step(std::integral_constant<int, 0>{}, st);
     step(std::integral_constant<int, 1>{}, st + 1);
   }
-  if (st < nst) step(std::integral_constant<int, 0>{}, st);
+  if (st < s1) step(std::integral_constant<int, 0>{}, st);
   qmvs_wait_vm_lgkm0<0>();
+}
+
+// The dense form of qmvs_walk_xlds for walks of at most D steps, with every load
+// of the walk issued before the first step: each wave loads the scale/bias words
+// of its D steps, the block DMAs the x rows of all D steps into D stage slots
+// (xs + d * 16 MT kXStageRow; slot layout as above, every DMA instruction issued,
+// rows past the x rows re-reading a valid one), then each wave loads the weights
+// of its D steps into registers.  One wait (vmcnt: the weight loads issued after the last x DMA) and
+// one s_barrier make all x slots visible to all waves; step d then waits only for
+// its own weights.  So the walk pays one memory round trip rather than one per
+// step.  Steps d with s0 + d >= s1 load from clamped
+// addresses (weights from an offset past the buffer, which reads zeros without
+// a memory access) and are not computed.
+template <int MT, int NTT, int WV, int D>
+__device__ __forceinline__ void qmvs_walk_xall(uint8_t* xs, uint8_t* stage, __amdgpu_buffer_rsrc_t xres,
+                                               const uint32_t (&xo)[8 * MT / WV], int wave,
+                                               const uint32_t* w, const uint16_t* sc,
+                                               const uint16_t* bi, int64_t nb, int64_t N, int64_t K,
+                                               int64_t s0, int64_t s1, f32x4 (&acc)[MT][NTT]) {
+  constexpr int SU = 4;
+  using G = QmvsGeom<NTT, SU>;
+  constexpr int NI = G::NI, LPR = G::LPR, RB = G::RB, ROWS = G::ROWS, SPL = G::SPL;
+  constexpr int AX = 8 * MT / WV;
+  constexpr int XSLOT = 16 * MT * kXStageRow;
+  static_assert(AX >= 1 && AX * WV == 8 * MT, "x DMA split over the block's waves");
+  static_assert(D >= 1 && D * NI < 64, "vmcnt range");
+  typedef uint32_t sbv_t __attribute__((ext_vector_type(SPL / 2)));
+  const int lane = threadIdx.x & 63;
+  const int c16 = lane & 15, q = lane >> 4;
+  const int64_t wpr = K / 8, gpr = K / 64;
+  if (s1 <= s0) return;
+
+  uint32_t wq[NI];
+  int wo[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int r = i * (64 / LPR) + lane / LPR;
+    int64_t n = nb + r;
+    n = n < N ? n : N - 1;
+    wq[i] = (uint32_t)((n * wpr + (lane % LPR) * 4) * 4);
+    wo[i] = r * RB + (qmvs_pos<SU>(lane % LPR, r) << 4);
+  }
+  const __amdgpu_buffer_rsrc_t wres =
+      __builtin_amdgcn_make_buffer_rsrc((void*)w, (short)0, (int)(N * wpr * 4), 0x00020000);
+  int wr[NTT][SU];
+#pragma unroll
+  for (int t = 0; t < NTT; ++t)
+#pragma unroll
+    for (int j = 0; j < SU; ++j) {
+      const int r = 16 * t + c16;
+      wr[t][j] = r * RB + (qmvs_pos<SU>(2 * j + (q >> 1), r) << 4) + (q & 1) * 8;
+    }
+  // Scale/bias words as in qmvs_slice: lane -> row l % ROWS, kind (l / ROWS) & 1,
+  // and for 16-row tiles which half of the step's groups (l / ROWS / 2).
+  const int sh = lane / ROWS;
+  int64_t nrow = nb + lane % ROWS;
+  nrow = nrow < N ? nrow : N - 1;
+  const uint16_t* sbrow = ((sh & 1) ? bi : sc) + nrow * gpr + ((64 / ROWS == 2) ? 0 : (sh >> 1) * SPL);
+  int xa[SU][2];
+#pragma unroll
+  for (int j = 0; j < SU; ++j)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) xa[j][h] = c16 * kXStageRow + (((8 * j + 2 * q + h) ^ c16) << 4);
+
+  // Issue order: scale/bias words, x DMAs, weights.  The wait for x then counts
+  // only the weight loads (16-byte loads, which the compiler cannot merge), however
+  // the scale loads were combined.
+  u32x4 wbuf[D][NI];
+  sbv_t sbuf[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    const int64_t st = s0 + d < s1 ? s0 + d : s1 - 1;
+    sbuf[d] = *reinterpret_cast<const sbv_t*>(sbrow + st * SU);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    const int64_t st = s0 + d < s1 ? s0 + d : s1 - 1;
+#pragma unroll
+    for (int j = 0; j < AX; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          xres, (qmvs_lds_t*)(xs + d * XSLOT + (wave * AX + j) * 1024), 16, (int)xo[j],
+          (int)(st * kXStageRow), 0, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    const bool past = s0 + d >= s1;
+    const int64_t st = past ? s1 - 1 : s0 + d;
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+      wbuf[d][i] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                     wres, past ? (int)0x80000000u : (int)(wq[i] + (uint32_t)st * SU * 32), 0,
+                     2 /* nt */));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  qmvs_wait_vm_lgkm0<D * NI>();
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  const bf16x8 ones = as_bf16x8(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    if (s0 + d >= s1) break;
+    const uint8_t* xc = xs + d * XSLOT;
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+      *reinterpret_cast<u32x4*>(stage + wo[i]) = wbuf[d][i];
+    u32x2 wv[SU][NTT];
+#pragma unroll
+    for (int j = 0; j < SU; ++j)
+#pragma unroll
+      for (int t = 0; t < NTT; ++t)
+        wv[j][t] = *reinterpret_cast<const u32x2*>(stage + wr[t][j]);
+    uint32_t sv[NTT][SU / 2], bv[NTT][SU / 2];
+#pragma unroll
+    for (int t = 0; t < NTT; ++t)
+#pragma unroll
+      for (int k = 0; k < SU / 2; ++k) {
+        const int row = 16 * t + c16;
+        const int hi = (64 / ROWS == 2) ? 0 : k / (SPL / 2);
+        const int idx = (64 / ROWS == 2) ? k : k % (SPL / 2);
+        sv[t][k] = (uint32_t)__shfl((int)sbuf[d][idx], (2 * hi) * ROWS + row, 64);
+        bv[t][k] = (uint32_t)__shfl((int)sbuf[d][idx], (2 * hi + 1) * ROWS + row, 64);
+      }
+#pragma unroll
+    for (int j = 0; j < SU; ++j) {
+      bf16x8 A[MT][2];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        A[mt][0] = xfrag4(*reinterpret_cast<const u32x4*>(xc + mt * 16 * kXStageRow + xa[j][0]));
+        A[mt][1] = xfrag4(*reinterpret_cast<const u32x4*>(xc + mt * 16 * kXStageRow + xa[j][1]));
+      }
+      f32x4 xsum[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        xsum[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mt][0], ones, f32x4{}, 0, 0, 0);
+        xsum[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mt][1], ones, xsum[mt], 0, 0, 0);
+      }
+      f32x4 P[MT][NTT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int t = 0; t < NTT; ++t) {
+          P[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mt][0], wfrag<4>(wv[j][t][0]),
+                                                             f32x4{}, 0, 0, 0);
+          P[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mt][1], wfrag<4>(wv[j][t][1]),
+                                                             P[mt][t], 0, 0, 0);
+        }
+#pragma unroll
+      for (int t = 0; t < NTT; ++t) {
+        const float sf = (j & 1) ? bf16_hi(sv[t][j >> 1]) : bf16_lo(sv[t][j >> 1]);
+        const float bf = (j & 1) ? bf16_hi(bv[t][j >> 1]) : bf16_lo(bv[t][j >> 1]);
+        const float bo = __builtin_fmaf(-128.f, sf, bf);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc[mt][t][r] = __builtin_fmaf(sf, P[mt][t][r], __builtin_fmaf(bo, xsum[mt][r], acc[mt][t][r]));
+      }
+    }
+  }
 }
 
 }  // namespace fmxq

@@ -38,6 +38,21 @@
 //   - A = x in the matching pair order, loaded per unit from global memory
 //     (rows >= M read a valid row; their outputs are discarded).
 // In both the K axis is split over the KS waves of a block, which meet in LDS.
+//
+// qmvw_kernel (int4, group 64, 9 <= M <= 64 where it wins: M > 16, or wide
+// outputs / long rows at M <= 16):
+//   - the same 16x16x32 tile walk, but the WV = 4 waves of a block own 4 W tiles
+//     side by side over one K part and share the block's x rows, which the block
+//     DMAs into LDS (buffer_load ... lds) once per step: qmvs reads x once per
+//     wave, and at M = 16 that is twice the weight bytes through the texture
+//     units (isolating the two streams on MI355X: x, not the weights, set the
+//     qmvs time);
+//   - the K parts of a row block are separate blocks (grid y) writing fp32
+//     partials; qmvw_fixup_kernel sums them in part order and rounds;
+//   - walks of at most 4 steps issue every load first (qmvs_walk_xall), longer
+//     ones double-buffer x one step ahead (qmvs_walk_xlds).
+#include <algorithm>
+
 #include "fmxq_common.hpp"
 #include "fmxq_internal.hpp"
 #include "fmxq_mfma_frag.hpp"
@@ -337,6 +352,207 @@ hipError_t launch_qmvs(const QmmArgs& a, hipStream_t stream) {
   if (a.M <= 0 || a.N <= 0) return hipSuccess;
   if (!qmvs_supported(a)) return hipErrorInvalidValue;
   return a.M <= 16 ? launch_qmvs_mt<1>(a, stream) : launch_qmvs_mt<2>(a, stream);
+}
+
+// ---------------------------------------------------------------------------
+// qmvw_kernel.  Block: WV waves side by side over WV * 16 NTT rows of W and one
+// K part (steps [s0, s1) of 256 values); the block's x rows (16 MT of them) go to
+// LDS once per step for all its waves (qmvs_walk_xlds), so x costs the texture
+// units a 1 / WV share of what it costs qmvs, where every wave loads its own.
+// Grid: (row blocks, K parts).  One part stores bf16 outputs; several write fp32
+// partials [part][M][N] to a.ws and qmvw_fixup_kernel sums them in part order.
+
+namespace {
+
+template <int MT, int NTT, int WV, int D>
+__global__ __launch_bounds__(WV * 64) __attribute__((amdgpu_waves_per_eu(MT == 1 && NTT == 1 ? 3 : 2)))
+void qmvw_kernel(QmmArgs a) {
+  using G = QmvsGeom<NTT, 4>;
+  constexpr int AX = 8 * MT / WV;
+  constexpr int XSLOTS = D > 0 ? D : 2;
+  __shared__ __attribute__((aligned(1024))) uint8_t xs[XSLOTS][16 * MT * kXStageRow];
+  __shared__ __attribute__((aligned(16))) uint8_t stage[WV][G::STAGE];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c16 = lane & 15, q = lane >> 4;
+  const int64_t nb = (int64_t)blockIdx.x * (16 * NTT * WV) + wave * (16 * NTT);
+  const int parts = a.splits > 1 ? a.splits : 1;
+  const int part = (int)blockIdx.y;
+  const int64_t nst = a.K / 256;
+  const int64_t s0 = part * nst / parts, s1 = (part + 1) * nst / parts;
+
+  // x through a buffer resource (qmvw_supported keeps its byte size below 2^31).
+  // DMA instruction j of this wave fills stage rows 2 (AX wave + j) and the next
+  // (qmvs_walk_xlds); a row past M reads row M - 1 and reaches no stored output.
+  const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)a.x, (short)0, (int)(((a.M - 1) * a.ldx + a.K) * 2), 0x00020000);
+  uint32_t xo[AX];
+#pragma unroll
+  for (int j = 0; j < AX; ++j) {
+    const int r = 2 * (wave * AX + j) + (lane >> 5);
+    const int c = (lane & 31) ^ (r & 15);
+    const int64_t xr = r < a.M ? r : a.M - 1;
+    xo[j] = (uint32_t)(xr * a.ldx * 2 + c * 16);
+  }
+  f32x4 acc[1][MT][NTT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int t = 0; t < NTT; ++t) acc[0][mt][t] = f32x4{};
+  if constexpr (D > 0) {
+    qmvs_walk_xall<MT, NTT, WV, D>(&xs[0][0], stage[wave], xres, xo, wave, a.w, a.scales, a.biases,
+                                   nb, a.N, a.K, s0, s1, acc[0]);
+  } else {
+    const uint32_t* const w[1] = {a.w};
+    const uint16_t* const sc[1] = {a.scales};
+    const uint16_t* const bi[1] = {a.biases};
+    qmvs_walk_xlds<MT, MT, NTT, 1, WV>(xs[0], xs[1], stage[wave], xres, xo, wave, a.M, w, sc, bi,
+                                       nb, a.N, a.K, s0, s1, acc);
+  }
+
+  // C layout of a 16x16 tile: register r of lane l is row 4 (l / 16) + r, column
+  // l % 16.
+#pragma unroll
+  for (int t = 0; t < NTT; ++t) {
+    const int64_t n = nb + 16 * t + c16;
+    if (n >= a.N) continue;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t m = 16 * mt + 4 * q + r;
+        if (m >= a.M) continue;
+        if (parts == 1) a.y[m * a.ldy + n] = finish_out(acc[0][mt][t][r], a.bias, n);
+        else a.ws[((int64_t)part * a.M + m) * a.N + n] = acc[0][mt][t][r];
+      }
+  }
+}
+
+// Grid (ceil(N / 1024), M): thread t of block x sums the parts of outputs
+// 4 (256 x + t) .. +4 of row blockIdx.y (N % 4 == 0, so 16-byte pieces), or of
+// output 256 x + t alone when N % 4 != 0 (grid x then ceil(N / 256)).
+__global__ __launch_bounds__(256) void qmvw_fixup_kernel(QmmArgs a) {
+  const int64_t m = blockIdx.y;
+  const int64_t mn = a.M * a.N;
+  const float* src = a.ws + m * a.N;
+  uint16_t* dst = a.y + m * a.ldy;
+  if ((a.N & 3) == 0) {
+    const int64_t n = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
+    if (n >= a.N) return;
+    f32x4 v = *reinterpret_cast<const f32x4*>(src + n);
+    for (int p = 1; p < a.splits; ++p) v += *reinterpret_cast<const f32x4*>(src + p * mn + n);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[n + i] = finish_out(v[i], a.bias, n + i);
+  } else {
+    const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (n >= a.N) return;
+    float v = src[n];
+    for (int p = 1; p < a.splits; ++p) v += src[p * mn + n];
+    dst[n] = finish_out(v, a.bias, n);
+  }
+}
+
+template <int MT, int NTT, int WV, int D>
+hipError_t launch_qmvw_cfg(const QmmArgs& a, hipStream_t stream) {
+  const int parts = a.splits > 1 ? a.splits : 1;
+  const dim3 grid((unsigned)((a.N + 16 * NTT * WV - 1) / (16 * NTT * WV)), (unsigned)parts);
+  qmvw_kernel<MT, NTT, WV, D><<<grid, WV * 64, 0, stream>>>(a);
+  if (parts > 1) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int64_t per = (a.N & 3) == 0 ? 1024 : 256;
+    qmvw_fixup_kernel<<<dim3((unsigned)((a.N + per - 1) / per), (unsigned)a.M), 256, 0, stream>>>(a);
+  }
+  return hipGetLastError();
+}
+
+template <int MT, int NTT, int WV>
+hipError_t launch_qmvw_d(const QmmArgs& a, int d, hipStream_t stream) {
+  if (d == 2) return launch_qmvw_cfg<MT, NTT, WV, 2>(a, stream);
+  if constexpr (MT <= 2) {
+    if (d == 4) return launch_qmvw_cfg<MT, NTT, WV, 4>(a, stream);
+  }
+  return launch_qmvw_cfg<MT, NTT, WV, 0>(a, stream);
+}
+
+template <int MT>
+hipError_t launch_qmvw_mt(const QmmArgs& a, int ntt, int d, hipStream_t stream) {
+  if constexpr (MT <= 2) {
+    if (ntt == 2) return launch_qmvw_d<MT, 2, 4>(a, d, stream);
+  }
+  return launch_qmvw_d<MT, 1, 4>(a, d, stream);
+}
+
+}  // namespace
+
+bool qmvw_supported(const QmmArgs& a) {
+  auto al = [](const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0; };
+  // K a multiple of 256 (whole steps; 8-byte scale loads stay aligned).  Weights
+  // and x go through buffer resources: their byte sizes must stay below 2^31.
+  return a.bits == 4 && a.group_size == 64 && a.M >= 1 && a.M <= kQmvwMaxM && a.K % 256 == 0 &&
+         a.N * (a.K / 2) < (int64_t(1) << 31) &&
+         ((a.M - 1) * a.ldx + a.K) * 2 < (int64_t(1) << 31) && a.ldx % 8 == 0 &&
+         al(a.x, 16) && al(a.w, 16) && al(a.scales, 8) && al(a.biases, 8);
+}
+
+// Shapes measured on MI355X (4-bit group 64, M = 16 / 32 / 64; the Llama-3-8B
+// projections): long rows (K >= 8192) split K into 8 pipelined parts; wide
+// outputs (N >= 8192) take 32-row W tiles and 4 up-front parts for x tiles of up
+// to 32 rows, 2 pipelined parts for 64; N >= 4096 takes 4 parts; narrower outputs
+// 8 up-front parts of two steps.  No more parts than give about two blocks per CU
+// (a 128256-row head needs none), and the up-front walk only where its parts
+// hold at most d steps.
+QmvwPlan qmvw_plan(const QmmArgs& a, int cus) {
+  QmvwPlan p;
+  p.mt = a.M <= 16 ? 1 : a.M <= 32 ? 2 : 4;
+  p.ntt = 1;
+  p.wv = 4;
+  const int64_t nst = a.K / 256;
+  int64_t parts;
+  if (a.K >= 8192) {
+    parts = 8;
+    p.d = 0;
+  } else if (a.N >= 8192) {
+    if (p.mt <= 2) {
+      p.ntt = 2;
+      parts = 4;
+      p.d = 4;
+    } else {
+      parts = 2;
+      p.d = 0;
+    }
+  } else if (a.N >= 4096) {
+    parts = 4;
+    p.d = p.mt <= 2 ? 4 : 0;
+  } else {
+    parts = 8;
+    p.d = 2;
+  }
+  const int64_t rows = 16 * p.ntt * p.wv;
+  const int64_t rblocks = (a.N + rows - 1) / rows;
+  const int64_t enough = (2 * (int64_t)cus + rblocks - 1) / rblocks;
+  parts = std::min(parts, std::max<int64_t>(enough, 1));
+  parts = std::max<int64_t>(1, std::min(parts, nst));
+  if (p.d > 0 && parts * p.d < nst) p.d = 0;
+  p.parts = (int)parts;
+  p.ws_floats = parts > 1 ? parts * a.M * a.N : 0;
+  return p;
+}
+
+hipError_t launch_qmvw(const QmmArgs& a, const QmvwPlan& p, hipStream_t stream) {
+  if (a.M <= 0 || a.N <= 0) return hipSuccess;
+  if (!qmvw_supported(a) || (p.parts > 1 && (!a.ws || a.splits != p.parts)))
+    return hipErrorInvalidValue;
+  // The upfront walk holds at most d steps: every part must fit.
+  if (p.wv != 4 || (p.mt == 4 && p.ntt != 1) ||
+      (p.d > 0 && ((a.K / 256 + p.parts - 1) / p.parts > p.d || (p.mt == 4 && p.d > 2))))
+    return hipErrorInvalidValue;
+  if (p.mt == 1) return launch_qmvw_mt<1>(a, p.ntt, p.d, stream);
+  if (p.mt == 2) return launch_qmvw_mt<2>(a, p.ntt, p.d, stream);
+  // 64-row x tiles use 16-row W tiles only (32-row ones would spill), and at most
+  // two up-front steps (LDS).
+  return launch_qmvw_mt<4>(a, 1, p.d, stream);
 }
 
 }  // namespace fmxq

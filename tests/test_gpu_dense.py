@@ -196,6 +196,37 @@ def test_qmv1_slice_shapes(gpu, oracle, N, K, bias):
     _qmm_case(gpu, oracle, 1, N, K, 4, 64, seed=9300 + N + K, bias=bias)
 
 
+@pytest.mark.parametrize("M", [9, 17, 33, 48, 64])
+@pytest.mark.parametrize("N,K,bias", [
+    (8200, 1024, False),  # wide: 32-row W tiles, 4 up-front parts of one step (64-row x: 2 pipelined)
+    (4100, 2048, True),   # 4 parts of two steps, ragged last row block, bias in the fixup
+    (1022, 4096, False),  # narrow: 8 up-front parts of two steps; N % 4 != 0 (scalar fixup)
+    (2050, 8192, False),  # long rows: 8 pipelined parts of four steps, N % 4 != 0
+    (4096, 7936, False),  # 31 steps: too many for the up-front walk, which falls back
+    (130, 256, True),     # one step: a single part stores bf16 directly
+])
+def test_qmvw_parts_and_walks(gpu, oracle, M, N, K, bias):
+    """The int4 group-64 product with x shared through LDS (qmvw, 9 <= M <= 64 on
+    wide or long shapes, every shape from M = 17): each plan branch (pipelined and
+    up-front walks, one or several K parts, 16- and 32-row W tiles, 16 to 64 x
+    rows), ragged rows, both fixup forms and the bias epilogue.  Two calls in a
+    row agree exactly (the parts are summed in a fixed order)."""
+    rows = np.unique(np.array([0, 1, M // 2, M - 2, M - 1]))
+    y1 = _qmm_case(gpu, oracle, M, N, K, 4, 64, seed=9400 + M * 5 + N + K, rows_checked=rows,
+                   bias=bias)
+    del y1
+    from fastmlx_amd import ops
+
+    rng = np.random.default_rng(1)
+    w, s, b = make_quant(rng, (N,), K, 4, 64)
+    x = make_x(rng, M, K)
+    dx, dw, ds, db = (to_dev(t, gpu) for t in (x, w, s, b))
+    r1 = to_np(ops.quantized_matmul(dx, dw, ds, db, True, 64, 4))
+    r2 = to_np(ops.quantized_matmul(dx, dw, ds, db, True, 64, 4))
+    torch.cuda.synchronize()
+    assert np.array_equal(r1, r2)
+
+
 def test_qmvs_bias(gpu, oracle):
     _qmm_case(gpu, oracle, 12, 8256, 512, 4, 64, seed=9201, bias=True)
     _qmm_case(gpu, oracle, 30, 2080, 1024, 4, 64, seed=9202, bias=True)
