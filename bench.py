@@ -395,8 +395,10 @@ def probe(args):
 
     Dense cases rotate --copies weight copies (16 copies of a 29 MB matrix exceed
     the 256 MB last-level cache); moe_c3 / moe_c4 run one SwitchGLU per launch at
-    --tokens; copy is a plain device copy of --mib MiB, which reads and writes
-    exactly that many bytes per dispatch (the byte counters' calibration)."""
+    --tokens (with --combine, switch_glu_combine with softmax routing weights, the
+    call the bench times); copy is a plain device copy of --mib MiB, which reads
+    and writes exactly that many bytes per dispatch (the byte counters'
+    calibration)."""
     import torch
 
     from fastmlx_amd import ops
@@ -431,13 +433,19 @@ def probe(args):
                 ranks = torch.multinomial(pz.expand(M, E), k, replacement=False, generator=gen)
                 r = torch.randperm(E, device=dev, generator=gen)[ranks]
             routes.append(r.to(torch.int32).contiguous())
+        ws = [torch.softmax(torch.randn(M, k, device=dev, generator=gen), dim=1).to(torch.bfloat16)
+              for _ in range(R)]
         ys = torch.empty(M, k, D, device=dev, dtype=torch.bfloat16)
+        yo = torch.empty(M, D, device=dev, dtype=torch.bfloat16)
         torch.cuda.synchronize()
         for i in range(args.launches):
-            ops.switch_glu(x, routes[i % R], gate, up, down, GROUP, 4, out=ys)
+            if args.combine:
+                ops.switch_glu_combine(x, routes[i % R], gate, up, down, ws[i % R], out=yo)
+            else:
+                ops.switch_glu(x, routes[i % R], gate, up, down, GROUP, 4, out=ys)
         hit = sum(int(torch.unique(r).numel()) for r in routes) / R
         info.update(algorithmic_bytes=moe_bytes(M, D, I, k, int(round(hit)), 4, GROUP),
-                    experts_hit=hit)
+                    experts_hit=hit, combine=bool(args.combine))
     else:
         M, N, K, bits = PROBES[args.probe]
         copies = args.copies if M <= 32 else 1
@@ -472,6 +480,8 @@ def main():
     ap.add_argument("--copies", type=int, default=16)
     ap.add_argument("--mib", type=int, default=512)
     ap.add_argument("--tokens", type=int, default=128)
+    ap.add_argument("--combine", action="store_true",
+                    help="moe probes: switch_glu_combine (the bench's call) instead of switch_glu")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path has no "

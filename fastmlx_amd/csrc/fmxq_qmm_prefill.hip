@@ -450,9 +450,17 @@ __global__ __launch_bounds__(256) void prefill_fixup_kernel(QmmArgs a) {
   const int64_t t = full + tt;
   const int64_t m = (t % nt_m) * BM + e / BN, n = (t / nt_m) * BN + e % BN;
   if (m >= a.M || n >= a.N) return;
+  // Every part is loaded before the first add (one round trip, not one per
+  // part); the sum runs in part order.
+  f32x4 part[kPrefillMaxSplits];
+#pragma unroll
+  for (int sp = 0; sp < kPrefillMaxSplits; ++sp)
+    if (sp < a.splits)
+      part[sp] = *reinterpret_cast<const f32x4*>(a.ws + (tt * a.splits + sp) * (int64_t)(BM * BN) + e);
   f32x4 v = {};
-  for (int sp = 0; sp < a.splits; ++sp)
-    v += *reinterpret_cast<const f32x4*>(a.ws + (tt * a.splits + sp) * (int64_t)(BM * BN) + e);
+#pragma unroll
+  for (int sp = 0; sp < kPrefillMaxSplits; ++sp)
+    if (sp < a.splits) v += part[sp];
   uint32_t p0 = pack_bf16x2(v[0], v[1]), p1 = pack_bf16x2(v[2], v[3]);
   if (a.bias) {
     float bv[4];

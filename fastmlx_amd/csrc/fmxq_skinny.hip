@@ -431,25 +431,42 @@ void qmvw_kernel(QmmArgs a) {
 
 // Grid (ceil(N / 1024), M): thread t of block x sums the parts of outputs
 // 4 (256 x + t) .. +4 of row blockIdx.y (N % 4 == 0, so 16-byte pieces), or of
-// output 256 x + t alone when N % 4 != 0 (grid x then ceil(N / 256)).
+// output 256 x + t alone when N % 4 != 0 (grid x then ceil(N / 256)).  All parts
+// are loaded before the first add (at most kQmvwMaxParts), so a thread waits for
+// one round trip instead of one per part; the sum runs in part order.
+constexpr int kQmvwMaxParts = 16;
+
 __global__ __launch_bounds__(256) void qmvw_fixup_kernel(QmmArgs a) {
   const int64_t m = blockIdx.y;
   const int64_t mn = a.M * a.N;
   const float* src = a.ws + m * a.N;
   uint16_t* dst = a.y + m * a.ldy;
+  const int parts = a.splits;
   if ((a.N & 3) == 0) {
     const int64_t n = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
     if (n >= a.N) return;
-    f32x4 v = *reinterpret_cast<const f32x4*>(src + n);
-    for (int p = 1; p < a.splits; ++p) v += *reinterpret_cast<const f32x4*>(src + p * mn + n);
+    f32x4 v[kQmvwMaxParts];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dst[n + i] = finish_out(v[i], a.bias, n + i);
+    for (int p = 0; p < kQmvwMaxParts; ++p)
+      if (p < parts) v[p] = *reinterpret_cast<const f32x4*>(src + p * mn + n);
+    f32x4 t = v[0];
+#pragma unroll
+    for (int p = 1; p < kQmvwMaxParts; ++p)
+      if (p < parts) t += v[p];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[n + i] = finish_out(t[i], a.bias, n + i);
   } else {
     const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (n >= a.N) return;
-    float v = src[n];
-    for (int p = 1; p < a.splits; ++p) v += src[p * mn + n];
-    dst[n] = finish_out(v, a.bias, n);
+    float v[kQmvwMaxParts];
+#pragma unroll
+    for (int p = 0; p < kQmvwMaxParts; ++p)
+      if (p < parts) v[p] = src[p * mn + n];
+    float t = v[0];
+#pragma unroll
+    for (int p = 1; p < kQmvwMaxParts; ++p)
+      if (p < parts) t += v[p];
+    dst[n] = finish_out(t, a.bias, n);
   }
 }
 
@@ -533,7 +550,7 @@ QmvwPlan qmvw_plan(const QmmArgs& a, int cus) {
   const int64_t rblocks = (a.N + rows - 1) / rows;
   const int64_t enough = (2 * (int64_t)cus + rblocks - 1) / rblocks;
   parts = std::min(parts, std::max<int64_t>(enough, 1));
-  parts = std::max<int64_t>(1, std::min(parts, nst));
+  parts = std::max<int64_t>(1, std::min({parts, nst, (int64_t)kQmvwMaxParts}));
   if (p.d > 0 && parts * p.d < nst) p.d = 0;
   p.parts = (int)parts;
   p.ws_floats = parts > 1 ? parts * a.M * a.N : 0;
@@ -542,7 +559,8 @@ QmvwPlan qmvw_plan(const QmmArgs& a, int cus) {
 
 hipError_t launch_qmvw(const QmmArgs& a, const QmvwPlan& p, hipStream_t stream) {
   if (a.M <= 0 || a.N <= 0) return hipSuccess;
-  if (!qmvw_supported(a) || (p.parts > 1 && (!a.ws || a.splits != p.parts)))
+  if (!qmvw_supported(a) || p.parts > kQmvwMaxParts ||
+      (p.parts > 1 && (!a.ws || a.splits != p.parts)))
     return hipErrorInvalidValue;
   // The upfront walk holds at most d steps: every part must fit.
   if (p.wv != 4 || (p.mt == 4 && p.ntt != 1) ||
