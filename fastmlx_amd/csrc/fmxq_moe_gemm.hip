@@ -190,8 +190,7 @@ template <int MT, int NTT, int NMAT, int WV>
 __global__ __launch_bounds__(WV * 64) __attribute__((amdgpu_waves_per_eu(MT == 1 && NTT == 1 ? 3 : 2))) void moe_qmvw_kernel(
     MoeArgs a) {
   using G = QmvsGeom<NTT, 4>;
-  __shared__ __attribute__((aligned(1024))) uint8_t xs0[16 * MT * kXStageRow];
-  __shared__ __attribute__((aligned(1024))) uint8_t xs1[16 * MT * kXStageRow];
+  __shared__ __attribute__((aligned(1024))) uint8_t xs[2][16 * MT * kXStageRow];
   __shared__ __attribute__((aligned(16))) uint8_t stage[WV][NMAT * G::STAGE];
 
   const int64_t sg = blockIdx.y;
@@ -239,17 +238,34 @@ __global__ __launch_bounds__(WV * 64) __attribute__((amdgpu_waves_per_eu(MT == 1
         xo[j] = (uint32_t)(xr * a.K * 2 + c * 16);
       }
     };
+    // One matrix with K <= 512 (the down projection of 512-wide experts): a walk
+    // of one or two steps, so every load is issued first (qmvs_walk_xall).
+    const bool upfront = NMAT == 1 && a.K <= 512;
     if (MT == 2 && len <= 16) {
       // Short segment of a 32-slot window: 16 stage rows, one tile walked.
       uint32_t xo[8 / WV];
       x_offsets(xo, 8 / WV);
-      qmvs_walk_xlds<1, MT, NTT, NMAT, WV>(xs0, xs1, stage[wave], xres, xo, wave, len, w, sc, bi,
-                                           nb, a.N, a.K, 0, a.K / 256, acc);
+      if (upfront) {
+        f32x4 acc1[1][NTT];
+#pragma unroll
+        for (int t = 0; t < NTT; ++t) acc1[0][t] = f32x4{};
+        qmvs_walk_xall<1, NTT, WV, 2>(&xs[0][0], stage[wave], xres, xo, wave, w[0], sc[0], bi[0],
+                                      nb, a.N, a.K, 0, a.K / 256, acc1);
+#pragma unroll
+        for (int t = 0; t < NTT; ++t) acc[0][0][t] = acc1[0][t];
+      } else {
+        qmvs_walk_xlds<1, MT, NTT, NMAT, WV>(xs[0], xs[1], stage[wave], xres, xo, wave, len, w, sc,
+                                             bi, nb, a.N, a.K, 0, a.K / 256, acc);
+      }
     } else {
       uint32_t xo[8 * MT / WV];
       x_offsets(xo, 8 * MT / WV);
-      qmvs_walk_xlds<MT, MT, NTT, NMAT, WV>(xs0, xs1, stage[wave], xres, xo, wave, len, w, sc, bi,
-                                            nb, a.N, a.K, 0, a.K / 256, acc);
+      if (upfront)
+        qmvs_walk_xall<MT, NTT, WV, 2>(&xs[0][0], stage[wave], xres, xo, wave, w[0], sc[0], bi[0],
+                                       nb, a.N, a.K, 0, a.K / 256, acc[0]);
+      else
+        qmvs_walk_xlds<MT, MT, NTT, NMAT, WV>(xs[0], xs[1], stage[wave], xres, xo, wave, len, w,
+                                              sc, bi, nb, a.N, a.K, 0, a.K / 256, acc);
     }
   }
   store_segment<MT, NTT, NMAT>(a, start, len, bad_e, nb, acc);
