@@ -134,6 +134,16 @@ struct PrefillPlan {
 };
 PrefillPlan qmm_prefill_plan(const QmmArgs& a, int cus);
 hipError_t launch_qmm_prefill(const QmmArgs& a, hipStream_t stream);
+// Dequantize-then-GEMM for large M (fmxq_capi.cpp): W dequantized once into a
+// per-stream bf16 workspace with the prefill kernel's single rounding
+// (launch_dequant_fused), then a library bf16 GEMM.  Taken for bias-free int4 /
+// int8 products with M >= kDeqGemmMinM and N K <= kDeqGemmMaxElems (the
+// workspace is 2 N K bytes).
+constexpr int64_t kDeqGemmMinM = 1024;
+constexpr int64_t kDeqGemmMaxElems = int64_t(1) << 26;
+hipError_t launch_dequant_fused(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                                uint16_t* out, int64_t N, int64_t K, int group_size, int bits,
+                                hipStream_t stream);
 // Grouped form (QmmArgs::g_*): grid = N tiles x max_tiles work-list entries.
 constexpr int kGroupedTileRows = 128;
 bool qmm_grouped_supported(int64_t N, int64_t K, int64_t x_rows, int bits, int group_size);

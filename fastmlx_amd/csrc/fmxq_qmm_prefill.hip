@@ -505,6 +505,46 @@ TileShape prefill_tile(const QmmArgs& a) {
   return {128, 256};
 }
 
+// dequant_fused_kernel: W [N, K] packed -> [N, K] bf16 with the prefill GEMM's own
+// dequantization (w = bf16(fma(s, q, b)), one rounding: dequant_word4 /
+// dequant_words8), for the dequantize-then-GEMM path at large M.  Thread t owns
+// packed-word quad t (4 words: 32 int4 or 16 int8 values, inside one group since
+// group_size >= 32) of the row-major word array: one 16-byte load, one scale and
+// one bias, 64 or 32 bytes of output in 16-byte stores.  Grid: ceil(quads / 256)
+// blocks; quads < 2^31 (checked by the launcher).
+template <int BITS>
+__global__ __launch_bounds__(256) void dequant_fused_kernel(const uint32_t* __restrict__ w,
+                                                            const uint16_t* __restrict__ scales,
+                                                            const uint16_t* __restrict__ biases,
+                                                            uint16_t* __restrict__ out,
+                                                            uint32_t quads, uint32_t qpr,
+                                                            int gshift, uint32_t gpr) {
+  constexpr int PER = 32 / BITS;  // values per word
+  const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+  if (t >= quads) return;
+  const uint32_t r = t / qpr, qd = t - r * qpr;
+  const uint32_t k0 = qd * 4 * PER;
+  const u32x4 words = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(w) + t);
+  const uint64_t g = (uint64_t)r * gpr + (k0 >> gshift);
+  const float sv = bf16_bits_to_f32(scales[g]), bv = bf16_bits_to_f32(biases[g]);
+  u32x4* dst = reinterpret_cast<u32x4*>(out + (uint64_t)r * (qpr * 4 * PER) + k0);
+  if constexpr (BITS == 4) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t o[4];
+      dequant_word4(words[j], sv, bv, o);
+      dst[j] = u32x4{o[0], o[1], o[2], o[3]};
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      uint32_t o[4];
+      dequant_words8(words[2 * j], words[2 * j + 1], sv, bv, o);
+      dst[j] = u32x4{o[0], o[1], o[2], o[3]};
+    }
+  }
+}
+
 }  // namespace
 
 PrefillPlan qmm_prefill_plan(const QmmArgs& a, int cus) {
@@ -566,6 +606,29 @@ hipError_t launch_qmm_prefill(const QmmArgs& a, hipStream_t stream) {
   if (a.bits == 8) return launch_tile<8, 256, 128, 4, 2>(a, stream);
   if (ts.bm == 256) return launch_tile<4, 256, 128, 4, 2>(a, stream);
   return launch_tile<4, 128, 256, 2, 4>(a, stream);
+}
+
+hipError_t launch_dequant_fused(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                                uint16_t* out, int64_t N, int64_t K, int group_size, int bits,
+                                hipStream_t stream) {
+  const int64_t per = 32 / bits;
+  const int64_t qpr = K / per / 4;
+  const int64_t quads = N * qpr;
+  if (quads == 0) return hipSuccess;
+  if ((bits != 4 && bits != 8) || group_size < 32 || (group_size & (group_size - 1)) ||
+      K % (4 * per) || K % group_size || quads >= (int64_t(1) << 31))
+    return hipErrorInvalidValue;
+  const int gshift = __builtin_ctz((unsigned)group_size);
+  const unsigned blocks = (unsigned)((quads + 255) / 256);
+  if (bits == 4)
+    dequant_fused_kernel<4><<<blocks, 256, 0, stream>>>(w, scales, biases, out, (uint32_t)quads,
+                                                        (uint32_t)qpr, gshift,
+                                                        (uint32_t)(K / group_size));
+  else
+    dequant_fused_kernel<8><<<blocks, 256, 0, stream>>>(w, scales, biases, out, (uint32_t)quads,
+                                                        (uint32_t)qpr, gshift,
+                                                        (uint32_t)(K / group_size));
+  return hipGetLastError();
 }
 
 }  // namespace fmxq

@@ -227,6 +227,22 @@ def test_qmvw_parts_and_walks(gpu, oracle, M, N, K, bias):
     assert np.array_equal(r1, r2)
 
 
+@pytest.mark.parametrize("M,N,K,bits,group", [
+    (1024, 1024, 1024, 4, 64),   # the threshold M
+    (1500, 4104, 2048, 4, 32),   # ragged M, N not a multiple of the GEMM tiles
+    (1024, 2048, 4096, 4, 128),
+    (1100, 1032, 3072, 8, 64),
+    (2048, 4096, 1024, 8, 32),
+])
+def test_deq_gemm_shapes(gpu, oracle, M, N, K, bits, group):
+    """Bias-free products at M >= 1024: W dequantized once with the prefill
+    kernel's single rounding, then the library bf16 GEMM (fp32 accumulation); the
+    per-element bound against the fp64 oracle holds as for the fused kernels."""
+    rows = np.unique(np.array([0, 1, M // 3, M // 2, M - 2, M - 1]))
+    _qmm_case(gpu, oracle, M, N, K, bits, group, seed=9700 + M + N + K + bits + group,
+              rows_checked=rows)
+
+
 def test_qmvs_bias(gpu, oracle):
     _qmm_case(gpu, oracle, 12, 8256, 512, 4, 64, seed=9201, bias=True)
     _qmm_case(gpu, oracle, 30, 2080, 1024, 4, 64, seed=9202, bias=True)
@@ -305,7 +321,10 @@ def test_graph_replay_matches_eager(gpu):
     from fastmlx_amd import ops
 
     rng = np.random.default_rng(77)
-    shapes = [(1, 4096, 4096), (4, 1024, 4096), (16, 2048, 2048), (96, 512, 1024)]
+    # M=1 / 4 GEMVs, qmvs (M=16, narrow), qmvw with K parts and its fixup (M=32),
+    # the prefill GEMM (M=96) and the dequantize-then-GEMM path (M=1024).
+    shapes = [(1, 4096, 4096), (4, 1024, 4096), (16, 2048, 2048), (32, 4096, 4096),
+              (96, 512, 1024), (1024, 1024, 1024)]
     tensors = []
     for M, N, K in shapes:
         w, s, b = make_quant(rng, (N,), K, 4, 64)
