@@ -55,7 +55,7 @@ LLAMA_PROJ = [  # name, N (out), K (in): llama.go:403-428
 GROUP = 64
 PROFILES = os.path.join(ROOT, "profiles")
 ROOF_PMC = os.path.join(PROFILES, "qmv1_down_4096x14336_M1_traffic.md")
-QMM_PMC = os.path.join(PROFILES, "qmm_prefill_14336x4096_M2048_counters.md")
+QMM_PMC = os.path.join(PROFILES, "qmm_deq_gemm_14336x4096_M2048_counters.md")
 
 
 def gen_quant(torch, N, K, bits, gen, dev):
