@@ -507,41 +507,46 @@ TileShape prefill_tile(const QmmArgs& a) {
 
 // dequant_fused_kernel: W [N, K] packed -> [N, K] bf16 with the prefill GEMM's own
 // dequantization (w = bf16(fma(s, q, b)), one rounding: dequant_word4 /
-// dequant_words8), for the dequantize-then-GEMM path at large M.  Thread t owns
-// packed-word quad t (4 words: 32 int4 or 16 int8 values, inside one group since
-// group_size >= 32) of the row-major word array: one 16-byte load, one scale and
-// one bias, 64 or 32 bytes of output in 16-byte stores.  Grid: ceil(quads / 256)
-// blocks; quads < 2^31 (checked by the launcher).
+// dequant_words8), for the dequantize-then-GEMM path at large M.  The work is cut
+// into units of 8 consecutive values (one int4 word, two int8 words), 16 output
+// bytes each; the rows are contiguous, so unit u's group is 8 u >> log2(group)
+// over the whole matrix.  Thread (wave w, lane l) of block b takes units
+// b 1024 + w 256 + 64 j + l, j = 0..3: every load and every 16-byte store
+// instruction of a wave covers one contiguous span (1 KiB of output), where one
+// 64-byte run per thread had each store touch 64 segments.
 template <int BITS>
 __global__ __launch_bounds__(256) void dequant_fused_kernel(const uint32_t* __restrict__ w,
                                                             const uint16_t* __restrict__ scales,
                                                             const uint16_t* __restrict__ biases,
                                                             uint16_t* __restrict__ out,
-                                                            uint32_t quads, uint32_t qpr,
-                                                            int gshift, uint32_t gpr) {
-  constexpr int PER = 32 / BITS;  // values per word
-  const uint32_t t = blockIdx.x * 256u + threadIdx.x;
-  if (t >= quads) return;
-  const uint32_t r = t / qpr, qd = t - r * qpr;
-  const uint32_t k0 = qd * 4 * PER;
-  const u32x4 words = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(w) + t);
-  const uint64_t g = (uint64_t)r * gpr + (k0 >> gshift);
-  const float sv = bf16_bits_to_f32(scales[g]), bv = bf16_bits_to_f32(biases[g]);
-  u32x4* dst = reinterpret_cast<u32x4*>(out + (uint64_t)r * (qpr * 4 * PER) + k0);
-  if constexpr (BITS == 4) {
+                                                            uint32_t units, int gshift) {
+  const uint32_t base = blockIdx.x * 1024u + (threadIdx.x >> 6) * 256u + (threadIdx.x & 63);
+  uint32_t wv[4][BITS / 4];
+  float sv[4], bv[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint32_t o[4];
-      dequant_word4(words[j], sv, bv, o);
-      dst[j] = u32x4{o[0], o[1], o[2], o[3]};
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t u = base + 64u * j;
+    if (u < units) {
+      if constexpr (BITS == 4) {
+        wv[j][0] = __builtin_nontemporal_load(w + u);
+      } else {
+        const u32x2 p = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(w) + u);
+        wv[j][0] = p[0];
+        wv[j][1] = p[1];
+      }
+      const uint32_t g = (u * 8u) >> gshift;
+      sv[j] = bf16_bits_to_f32(scales[g]);
+      bv[j] = bf16_bits_to_f32(biases[g]);
     }
-  } else {
+  }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      uint32_t o[4];
-      dequant_words8(words[2 * j], words[2 * j + 1], sv, bv, o);
-      dst[j] = u32x4{o[0], o[1], o[2], o[3]};
-    }
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t u = base + 64u * j;
+    if (u >= units) continue;
+    uint32_t o[4];
+    if constexpr (BITS == 4) dequant_word4(wv[j][0], sv[j], bv[j], o);
+    else dequant_words8(wv[j][0], wv[j][1], sv[j], bv[j], o);
+    reinterpret_cast<u32x4*>(out)[u] = u32x4{o[0], o[1], o[2], o[3]};
   }
 }
 
@@ -611,23 +616,21 @@ hipError_t launch_qmm_prefill(const QmmArgs& a, hipStream_t stream) {
 hipError_t launch_dequant_fused(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                                 uint16_t* out, int64_t N, int64_t K, int group_size, int bits,
                                 hipStream_t stream) {
-  const int64_t per = 32 / bits;
-  const int64_t qpr = K / per / 4;
-  const int64_t quads = N * qpr;
-  if (quads == 0) return hipSuccess;
-  if ((bits != 4 && bits != 8) || group_size < 32 || (group_size & (group_size - 1)) ||
-      K % (4 * per) || K % group_size || quads >= (int64_t(1) << 31))
+  const int64_t units = N * K / 8;
+  if (units == 0) return hipSuccess;
+  // Units of 8 values inside one group (group_size >= 8, a power of two), and
+  // unit * 8 below 2^32.
+  if ((bits != 4 && bits != 8) || group_size < 8 || (group_size & (group_size - 1)) ||
+      K % group_size || K % 8 || units * 8 >= (int64_t(1) << 32))
     return hipErrorInvalidValue;
   const int gshift = __builtin_ctz((unsigned)group_size);
-  const unsigned blocks = (unsigned)((quads + 255) / 256);
+  const unsigned blocks = (unsigned)((units + 1023) / 1024);
   if (bits == 4)
-    dequant_fused_kernel<4><<<blocks, 256, 0, stream>>>(w, scales, biases, out, (uint32_t)quads,
-                                                        (uint32_t)qpr, gshift,
-                                                        (uint32_t)(K / group_size));
+    dequant_fused_kernel<4><<<blocks, 256, 0, stream>>>(w, scales, biases, out, (uint32_t)units,
+                                                        gshift);
   else
-    dequant_fused_kernel<8><<<blocks, 256, 0, stream>>>(w, scales, biases, out, (uint32_t)quads,
-                                                        (uint32_t)qpr, gshift,
-                                                        (uint32_t)(K / group_size));
+    dequant_fused_kernel<8><<<blocks, 256, 0, stream>>>(w, scales, biases, out, (uint32_t)units,
+                                                        gshift);
   return hipGetLastError();
 }
 
