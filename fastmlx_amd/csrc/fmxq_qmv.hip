@@ -335,16 +335,19 @@ __global__ __launch_bounds__(KS * RG * 64) void qmv1_slice_kernel(QmmArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) xr[j] = xs[j];
   }
+  // Lanes past the wave's RW rows x 4 pieces load nothing.
   u32x4 ps[NP], pb[NP];
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
     const int L = lane + 64 * p;
     const int r = L >> 2, pc = L & 3;
-    int64_t n = nbase + (r < RW ? r : 0);
-    n = n < a.N ? n : a.N - 1;
-    const int64_t off = n * gpr + ks * 32 + pc * 8;
-    ps[p] = *reinterpret_cast<const u32x4*>(a.scales + off);
-    pb[p] = *reinterpret_cast<const u32x4*>(a.biases + off);
+    if (r < RW) {
+      int64_t n = nbase + r;
+      n = n < a.N ? n : a.N - 1;
+      const int64_t off = n * gpr + ks * 32 + pc * 8;
+      ps[p] = *reinterpret_cast<const u32x4*>(a.scales + off);
+      pb[p] = *reinterpret_cast<const u32x4*>(a.biases + off);
+    }
   }
   // Keep the weight loads behind x and the pieces: the wait for those then does
   // not hold on the weights.
