@@ -329,6 +329,12 @@ __global__ __launch_bounds__(KS * RG * 64) void qmv1_slice_kernel(QmmArgs a) {
   const int c = ks * 64 + lane;
   const int64_t wpr = a.K / 8, gpr = a.K / 64;
   const int64_t nbase = ((int64_t)blockIdx.x * RG + rg) * RW;
+  // Row indices in 32 bits (launch_qmv1_slice keeps N below 2^31), wave-uniform
+  // for the weight rows: the clamp and the row offsets then stay on the scalar
+  // unit (gfx9 has no 64-bit signed scalar compare, so an int64 clamp would move
+  // every row address to 64-bit vector arithmetic).
+  const int nb32 = __builtin_amdgcn_readfirstlane((int)nbase);
+  const int nlast = (int)a.N - 1;
   u32x4 xr[4];
   {
     const u32x4* xs = reinterpret_cast<const u32x4*>(a.x + (int64_t)c * 32);
@@ -342,9 +348,8 @@ __global__ __launch_bounds__(KS * RG * 64) void qmv1_slice_kernel(QmmArgs a) {
     const int L = lane + 64 * p;
     const int r = L >> 2, pc = L & 3;
     if (r < RW) {
-      int64_t n = nbase + r;
-      n = n < a.N ? n : a.N - 1;
-      const int64_t off = n * gpr + ks * 32 + pc * 8;
+      const int n = min(nb32 + r, nlast);
+      const int64_t off = (int64_t)n * gpr + ks * 32 + pc * 8;
       ps[p] = *reinterpret_cast<const u32x4*>(a.scales + off);
       pb[p] = *reinterpret_cast<const u32x4*>(a.biases + off);
     }
@@ -355,9 +360,9 @@ __global__ __launch_bounds__(KS * RG * 64) void qmv1_slice_kernel(QmmArgs a) {
   u32x4 wv[RW];
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
-    int64_t n = nbase + r;
-    n = n < a.N ? n : a.N - 1;  // rows past N load row N-1; their outputs are not stored
-    wv[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.w + n * wpr) + c);
+    // rows past N load row N-1; their outputs are not stored
+    const int n = __builtin_amdgcn_readfirstlane(min(nb32 + r, nlast));
+    wv[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.w + (int64_t)n * wpr) + c);
   }
   __builtin_amdgcn_sched_barrier(0);
   XChunk<4> xc;
@@ -432,7 +437,9 @@ static hipError_t launch_qmv1_slice_cfg(const QmmArgs& a, hipStream_t stream) {
 // K = 4096 with N <= 4096 (4.2 -> 3.9 us for 4096 x 4096).  The 14336-row,
 // 4096-deep projections stay on qmv1_kernel (equal times).
 static hipError_t launch_qmv1_slice(const QmmArgs& a, hipStream_t stream) {
-  if (a.M != 1 || a.bits != 4 || a.group_size != 64 || a.K % 2048 != 0) return hipErrorNotSupported;
+  if (a.M != 1 || a.bits != 4 || a.group_size != 64 || a.K % 2048 != 0 ||
+      a.N >= (int64_t(1) << 31))
+    return hipErrorNotSupported;
   if ((reinterpret_cast<uintptr_t>(a.scales) & 15u) || (reinterpret_cast<uintptr_t>(a.biases) & 15u) ||
       (reinterpret_cast<uintptr_t>(a.x) & 15u) || (reinterpret_cast<uintptr_t>(a.w) & 15u))
     return hipErrorNotSupported;
