@@ -414,7 +414,7 @@ int fmxq_dequantize_rows(const uint32_t* w, const uint16_t* scales, const uint16
   if (!aligned16(w) || !aligned16(out))
     return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: w and out must be 16-byte aligned", op);
   uint32_t* flag = nullptr;
-  if (int rc = device_flag(&flag)) return rc;
+  if (int rc = device_flag(static_cast<hipStream_t>(stream), &flag)) return rc;
   return hip_status(fmxq::launch_dequantize(w, scales, biases, out, n_idx, K, group_size, bits,
                                             static_cast<hipStream_t>(stream), idx, table_rows,
                                             flag),
@@ -464,7 +464,7 @@ int fmxq_gather_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* scales
   if (batch * Mx > 0x7fffffffLL)
     return fail(FMXQ_ERR_SHAPE, "%s: batch*Mx=%lld too large", op, (long long)(batch * Mx));
   uint32_t* flag = nullptr;
-  if (int rc = device_flag(&flag)) return rc;
+  if (int rc = device_flag(static_cast<hipStream_t>(stream), &flag)) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (Mx == 1 && E <= kSortMaxExperts && fmxq::moe_qmvs_supported(N, K, bits, group_size) &&
       aligned16(scales) && aligned16(biases)) {
@@ -511,7 +511,7 @@ int fmxq_gather_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* scales
 
 int fmxq_device_error(void* stream) {
   uint32_t* flag = nullptr;
-  if (int rc = device_flag(&flag)) return rc;
+  if (int rc = device_flag(static_cast<hipStream_t>(stream), &flag)) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (int rc = hip_status(hipStreamSynchronize(s), "device_error: synchronize")) return rc;
   uint32_t v = 0;
@@ -563,7 +563,7 @@ int switch_glu_impl(const uint16_t* x, const uint32_t* inds, const uint32_t* w_g
   if (S > 0x7fffffffLL) return fail(FMXQ_ERR_SHAPE, "%s: too many slots", op);
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint32_t* flag = nullptr;
-  if (int rc = device_flag(&flag)) return rc;
+  if (int rc = device_flag(static_cast<hipStream_t>(stream), &flag)) return rc;
   const int window = fmxq::moe_window(S, E);
   const int64_t max_seg = fmxq::moe_max_segments(S, E, window);
   if (E <= kSortMaxExperts && max_seg <= kMaxSegmentsGrid &&
@@ -727,7 +727,7 @@ extern "C" int fmxq_switch_glu_combine(
       fmxq::moe_qmvs_supported(I, D, bits, group_size) && aligned16(s_gate) &&
       aligned16(b_gate) && aligned16(s_up) && aligned16(b_up)) {
     uint32_t* flag = nullptr;
-    if (int rc = device_flag(&flag)) return rc;
+    if (int rc = device_flag(static_cast<hipStream_t>(stream), &flag)) return rc;
     MoeScratch m;
     if (int rc = moe_scratch(s, S, I, 1, &m, op)) return rc;
     fmxq::MoeArgs gu{x, nullptr, {w_gate, w_up}, {s_gate, s_up}, {b_gate, b_up}, inds, nullptr,

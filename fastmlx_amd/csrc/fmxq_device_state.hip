@@ -1,7 +1,9 @@
 // fmxq_device_state.hip -- device memory the library keeps for the life of the
 // process in file-scope __device__ variables rather than hipMalloc:
-//   - the per-device index-error flag that gather kernels raise and
-//     fmxq_device_error reads and clears;
+//   - the index-error flags that gather kernels raise and fmxq_device_error
+//     reads and clears: kFlagSlots words per device, one per stream (streams
+//     get slots in order of first use; past kFlagSlots streams on one device,
+//     slots are shared in turn);
 //   - `scratch`, the fixed workspace of fmxq_switch_glu_noalloc
 //     (FMXQ_NOALLOC_SCRATCH_BYTES), for callers that cannot allocate.
 // Each GPU holds its own copy of both at its own address.  In host code the
@@ -10,20 +12,24 @@
 // and only the resolved pointers are ever handed to kernels or copies.
 #include <hip/hip_runtime.h>
 
+#include <map>
 #include <mutex>
 #include <vector>
 
 #include "../../include/fmxq.h"
 #include "fmxq_host.hpp"
 
-static __device__ __align__(256) uint32_t index_flag;
+constexpr int kFlagSlots = 64;
+static __device__ __align__(256) uint32_t index_flag[kFlagSlots];
 static __device__ __align__(256) unsigned char scratch[FMXQ_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
 struct DeviceState {
-  uint32_t* flag = nullptr;
+  uint32_t* flag = nullptr;  // kFlagSlots words
   void* scratch = nullptr;
+  std::map<hipStream_t, int> slot;
+  int next_slot = 0;
 };
 std::mutex g_state_mu;
 std::vector<DeviceState> g_state;
@@ -55,10 +61,14 @@ int current_state(DeviceState** out) {
 
 namespace fmxq {
 
-int device_flag(uint32_t** out) {
+int device_flag(hipStream_t stream, uint32_t** out) {
   DeviceState* st = nullptr;
   if (int rc = current_state(&st)) return rc;
-  *out = st->flag;
+  std::lock_guard<std::mutex> lk(g_state_mu);
+  auto it = st->slot.find(stream);
+  if (it == st->slot.end())
+    it = st->slot.emplace(stream, st->next_slot++ % kFlagSlots).first;
+  *out = st->flag + it->second;
   return FMXQ_OK;
 }
 

@@ -10,10 +10,10 @@ namespace fmxq {
 
 // FMXQ_OK for hipSuccess, else FMXQ_ERR_DEVICE with the HIP error string.
 int hip_status(hipError_t e, const char* what);
-// The current device's index-error flag: one uint32 __device__ variable per
-// device (zero at load, cleared by fmxq_device_error when it reports), resolved
-// without allocating (fmxq_device_state.hip).
-int device_flag(uint32_t** out);
+// The index-error flag of `stream` on the current device: a uint32 __device__
+// word of that stream's own (zero at load, cleared by fmxq_device_error when it
+// reports), resolved without allocating (fmxq_device_state.hip).
+int device_flag(hipStream_t stream, uint32_t** out);
 // The current device's fixed scratch of FMXQ_NOALLOC_SCRATCH_BYTES, shared by
 // every fmxq_switch_glu_noalloc call on that device.
 int noalloc_scratch(void** out);

@@ -204,7 +204,10 @@ int fmxq_route_group_topk(const void* gates, int gates_bf16, const float* bias, 
 
 /* Synchronizes `stream`, then reports (and clears) the device-side error flag
  * that gather kernels raise on an out-of-range index: returns FMXQ_OK or
- * FMXQ_ERR_INDEX. */
+ * FMXQ_ERR_INDEX.  The flag is the stream's own (kernels enqueued on `stream`
+ * raise it; other streams' flags are neither read nor cleared).  Streams get
+ * flag slots in order of first use, 64 per device; beyond 64 streams on one
+ * device, slots are shared in turn. */
 int fmxq_device_error(void* stream);
 
 #ifdef __cplusplus

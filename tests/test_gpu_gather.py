@@ -137,6 +137,31 @@ def test_out_of_range_expert_zeroes_and_flags(gpu):
     ops.device_error()  # cleared
 
 
+def test_index_flag_is_per_stream(gpu):
+    """The out-of-range flag belongs to the stream whose kernel raised it: another
+    stream's check neither reports nor clears it."""
+    from fastmlx_amd import FmxqError, ops
+
+    rng = np.random.default_rng(6)
+    E, N, K = 4, 64, 128
+    w, s, b = make_quant(rng, (E, N), K, 4, 64)
+    x = make_x(rng, 3, 1, K)
+    bad = np.array([1, 9, 2], dtype=np.uint32)
+    good = np.array([0, 3, 2], dtype=np.uint32)
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    announce("index flags of two streams")
+    with torch.cuda.stream(sa):
+        _run(gpu, x, w, s, b, bad)
+    with torch.cuda.stream(sb):
+        _run(gpu, x, w, s, b, good)
+        ops.device_error()  # nothing on this stream
+    with torch.cuda.stream(sa):
+        with pytest.raises(FmxqError) as ei:
+            ops.device_error()
+        assert ei.value.code == 4
+        ops.device_error()  # cleared
+
+
 @pytest.mark.parametrize("M", [1, 16])
 def test_config3_expert_projection(gpu, oracle, M):
     """Config 3 gate projection: 512 experts, 2048 -> 512, top-10 per token."""
