@@ -23,6 +23,7 @@ FMXQ_SYMBOLS = {
     "fmxq_last_error": (ctypes.c_char_p, []),
     "fmxq_dequantize": (_int, [_p, _p, _p, _p, _i64, _i64, _int, _int, _p]),
     "fmxq_dequantize_rows": (_int, [_p] * 5 + [_i64] * 3 + [_int, _int, _p]),
+    "fmxq_quantize": (_int, [_p, _p, _p, _p, _i64, _i64, _int, _int, _p]),
     "fmxq_quantized_matmul": (_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _bool, _int, _int, _p]),
     "fmxq_quantized_matmul_bias": (_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _bool, _int,
                                           _int, _p]),
@@ -106,6 +107,11 @@ FMX_SYMBOLS = {
     "fmx_view": (_int, [_Ap, _A, _int, _S]),
     "fmx_stack": (_int, [_Ap, ctypes.POINTER(_A), _sz, _int, _S]),
     "fmx_scale_neg8": (_int, [_Ap, _A, _S]),
+    "fmx_quantize": (_int, [_Ap, _Ap, _Ap, _A, _int, _int, _S]),
+    "fmx_reshape": (_int, [_Ap, _A, ctypes.POINTER(_int), _sz, _S]),
+    "fmx_split": (_int, [_Ap, _sz, _A, ctypes.POINTER(_int), _sz, _int, _S]),
+    "fmx_swapaxes": (_int, [_Ap, _A, _int, _int, _S]),
+    "fmx_contiguous": (_int, [_Ap, _A, _bool, _S]),
 }
 
 STATUS = {

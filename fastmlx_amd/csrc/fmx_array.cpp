@@ -1153,4 +1153,203 @@ int fmx_scale_neg8(fmx_array* res, const fmx_array scale, const fmx_stream s) {
   return commit(res, r, rc);
 }
 
+// ---- the array ops of the kv_b_proj absorption (deepseekv3.go:609-679) ----
+// Arrays here are always row-major and contiguous, so the view-producing MLX
+// ops (reshape, split, swapaxes) return contiguous copies and contiguous is a
+// copy; the values are the same as MLX's.
+
+namespace {
+int norm_axis(int axis, size_t ndim, const char* op, int* out) {
+  const int n = (int)ndim;
+  if (axis < -n || axis >= n)
+    return fail(FMXQ_ERR_SHAPE, "%s: axis %d out of range for %d dimensions", op, axis, n);
+  *out = axis < 0 ? axis + n : axis;
+  return FMXQ_OK;
+}
+
+int copy_op(fmx_array* res, Array* A, std::vector<int64_t> shape, const fmx_stream s,
+            const char* op) {
+  Launch L;
+  if (int rc = begin(L, s, {A})) return rc;
+  Array* r = nullptr;
+  if (int rc = new_result(L, std::move(shape), A->dtype, &r)) return rc;
+  int rc = FMXQ_OK;
+  if (r->nbytes())
+    rc = hip_status(hipMemcpyAsync(r->data, A->data, r->nbytes(), hipMemcpyDeviceToDevice, L.s),
+                    op);
+  finish(L);
+  return commit(res, r, rc);
+}
+}  // namespace
+
+// mlx_quantize (mlxgo/binding_cgo.go:684-697): w [..., K] bf16 -> res_0 packed
+// [..., K*bits/32] uint32, res_1 scales and res_2 biases [..., K/group] bf16.
+int fmx_quantize(fmx_array* res_0, fmx_array* res_1, fmx_array* res_2, const fmx_array w,
+                 int group_size, int bits, const fmx_stream s) {
+  const char* op = "quantize";
+  if (!res_0 || !res_1 || !res_2) return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: null result", op);
+  Array* W;
+  if (int rc = need(w, op, "w", &W)) return rc;
+  if (W->dtype != FMX_BFLOAT16)
+    return fail(FMXQ_ERR_UNSUPPORTED, "%s: w has dtype %s (bfloat16 only)", op,
+                dtype_name(W->dtype));
+  if (W->shape.size() < 2)
+    return fail(FMXQ_ERR_SHAPE, "%s: w must have at least 2 dimensions, got %s", op,
+                shape_str(W->shape).c_str());
+  const int64_t K = W->shape.back();
+  if (int rc = check_quant(group_size, bits, K, true, op)) return rc;
+  const int64_t rows = prod(W->shape, 0, W->shape.size() - 1);
+  std::vector<int64_t> qshape = W->shape, sshape = W->shape;
+  qshape.back() = K * bits / 32;
+  sshape.back() = K / group_size;
+  Launch L;
+  if (int rc = begin(L, s, {W})) return rc;
+  Array *rq = nullptr, *rs = nullptr, *rb = nullptr;
+  if (int rc = new_result(L, qshape, FMX_UINT32, &rq)) return rc;
+  if (int rc = new_result(L, sshape, FMX_BFLOAT16, &rs)) {
+    commit(res_0, rq, rc);
+    return rc;
+  }
+  if (int rc = new_result(L, sshape, FMX_BFLOAT16, &rb)) {
+    commit(res_0, rq, rc);
+    commit(res_1, rs, rc);
+    return rc;
+  }
+  int rc = fmxq_quantize(static_cast<const uint16_t*>(W->data), static_cast<uint32_t*>(rq->data),
+                         static_cast<uint16_t*>(rs->data), static_cast<uint16_t*>(rb->data), rows,
+                         K, group_size, bits, L.s);
+  finish(L);
+  if (rc) {
+    commit(res_0, rq, rc);
+    commit(res_1, rs, rc);
+    return commit(res_2, rb, rc);
+  }
+  commit(res_0, rq, 0);
+  commit(res_1, rs, 0);
+  return commit(res_2, rb, 0);
+}
+
+// mlx_reshape (binding_cgo.go:398-406); one entry may be -1.
+int fmx_reshape(fmx_array* res, const fmx_array a, const int* shape, size_t ndim,
+                const fmx_stream s) {
+  const char* op = "reshape";
+  if (!res) return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: null result", op);
+  if (ndim && !shape) return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: null shape", op);
+  Array* A;
+  if (int rc = need(a, op, "a", &A)) return rc;
+  std::vector<int64_t> out(ndim);
+  int infer = -1;
+  int64_t known = 1;
+  for (size_t i = 0; i < ndim; ++i) {
+    if (shape[i] == -1) {
+      if (infer >= 0) return fail(FMXQ_ERR_SHAPE, "%s: more than one -1 in the shape", op);
+      infer = (int)i;
+    } else if (shape[i] < 0) {
+      return fail(FMXQ_ERR_SHAPE, "%s: negative size %d", op, shape[i]);
+    } else {
+      out[i] = shape[i];
+      known *= shape[i];
+    }
+  }
+  const int64_t n = A->numel();
+  if (infer >= 0) {
+    if (known == 0 || n % known)
+      return fail(FMXQ_ERR_SHAPE, "%s: cannot infer -1 reshaping %s", op,
+                  shape_str(A->shape).c_str());
+    out[infer] = n / known;
+  } else if (known != n) {
+    return fail(FMXQ_ERR_SHAPE, "%s: %s has %lld elements, the new shape %lld", op,
+                shape_str(A->shape).c_str(), (long long)n, (long long)known);
+  }
+  return copy_op(res, A, std::move(out), s, op);
+}
+
+// mlx_split with explicit indices (binding_cgo.go:463-483): res holds n_res =
+// num_indices + 1 handles, part i covering [indices[i-1], indices[i]) of axis
+// (indices ascending within [0, dim]).  On failure no handle is touched.
+int fmx_split(fmx_array* res, size_t n_res, const fmx_array a, const int* indices,
+              size_t num_indices, int axis, const fmx_stream s) {
+  const char* op = "split";
+  if (!res) return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: null result", op);
+  if (num_indices && !indices) return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: null indices", op);
+  if (n_res != num_indices + 1)
+    return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: %zu result handles for %zu indices (want %zu)",
+                op, n_res, num_indices, num_indices + 1);
+  Array* A;
+  if (int rc = need(a, op, "a", &A)) return rc;
+  int ax = 0;
+  if (int rc = norm_axis(axis, A->shape.size(), op, &ax)) return rc;
+  const int64_t dim = A->shape[ax];
+  std::vector<int64_t> cut{0};
+  for (size_t i = 0; i < num_indices; ++i) {
+    if (indices[i] < cut.back() || indices[i] > dim)
+      return fail(FMXQ_ERR_SHAPE, "%s: index %d out of order or beyond axis size %lld", op,
+                  indices[i], (long long)dim);
+    cut.push_back(indices[i]);
+  }
+  cut.push_back(dim);
+  const int64_t outer = prod(A->shape, 0, ax);
+  const size_t inner = (size_t)prod(A->shape, ax + 1) * dtype_size(A->dtype);
+  Launch L;
+  if (int rc = begin(L, s, {A})) return rc;
+  std::vector<Array*> parts(n_res, nullptr);
+  int rc = FMXQ_OK;
+  for (size_t i = 0; i < n_res && !rc; ++i) {
+    std::vector<int64_t> shape = A->shape;
+    shape[ax] = cut[i + 1] - cut[i];
+    rc = new_result(L, shape, A->dtype, &parts[i]);
+    if (!rc && parts[i]->nbytes()) {
+      const size_t width = (size_t)shape[ax] * inner;
+      rc = hip_status(hipMemcpy2DAsync(parts[i]->data, width,
+                                       static_cast<const char*>(A->data) + cut[i] * inner,
+                                       (size_t)dim * inner, width, (size_t)outer,
+                                       hipMemcpyDeviceToDevice, L.s),
+                      "split: copy");
+    }
+  }
+  finish(L);
+  for (size_t i = 0; i < n_res; ++i)
+    if (parts[i]) commit(&res[i], parts[i], rc);
+  return rc;
+}
+
+// mlx_swapaxes (binding_cgo.go:715-722).
+int fmx_swapaxes(fmx_array* res, const fmx_array a, int axis1, int axis2, const fmx_stream s) {
+  const char* op = "swapaxes";
+  if (!res) return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: null result", op);
+  Array* A;
+  if (int rc = need(a, op, "a", &A)) return rc;
+  int a1 = 0, a2 = 0;
+  if (int rc = norm_axis(axis1, A->shape.size(), op, &a1)) return rc;
+  if (int rc = norm_axis(axis2, A->shape.size(), op, &a2)) return rc;
+  if (a1 > a2) std::swap(a1, a2);
+  std::vector<int64_t> shape = A->shape;
+  std::swap(shape[a1], shape[a2]);
+  if (a1 == a2) return copy_op(res, A, shape, s, op);
+  const size_t es = dtype_size(A->dtype);
+  if (es != 1 && es != 2 && es != 4 && es != 8)
+    return fail(FMXQ_ERR_UNSUPPORTED, "%s: dtype %s", op, dtype_name(A->dtype));
+  Launch L;
+  if (int rc = begin(L, s, {A})) return rc;
+  Array* r = nullptr;
+  if (int rc = new_result(L, shape, A->dtype, &r)) return rc;
+  int rc = hip_status(
+      fmxq::launch_swap_axes(A->data, r->data, prod(A->shape, 0, a1), A->shape[a1],
+                             prod(A->shape, a1 + 1, a2), A->shape[a2], prod(A->shape, a2 + 1),
+                             (int)es, L.s),
+      op);
+  finish(L);
+  return commit(res, r, rc);
+}
+
+// mlx_contiguous (binding_cgo.go:724-731): a row-major copy.
+int fmx_contiguous(fmx_array* res, const fmx_array a, bool allow_col_major, const fmx_stream s) {
+  (void)allow_col_major;
+  const char* op = "contiguous";
+  if (!res) return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: null result", op);
+  Array* A;
+  if (int rc = need(a, op, "a", &A)) return rc;
+  return copy_op(res, A, A->shape, s, op);
+}
+
 }  // extern "C"

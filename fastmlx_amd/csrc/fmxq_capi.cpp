@@ -400,6 +400,20 @@ int fmxq_dequantize(const uint32_t* w, const uint16_t* scales, const uint16_t* b
                     "dequantize");
 }
 
+int fmxq_quantize(const uint16_t* w, uint32_t* wq, uint16_t* scales, uint16_t* biases,
+                  int64_t rows, int64_t K, int group_size, int bits, void* stream) {
+  if (int rc = check_quant(group_size, bits, K, true, "quantize")) return rc;
+  if (rows < 0) return fail(FMXQ_ERR_SHAPE, "quantize: negative rows");
+  if (rows == 0) return FMXQ_OK;
+  if (!w || !wq || !scales || !biases)
+    return fail(FMXQ_ERR_INVALID_ARGUMENT, "quantize: null operand");
+  if (!aligned16(w) || !aligned16(wq))
+    return fail(FMXQ_ERR_INVALID_ARGUMENT, "quantize: w and wq must be 16-byte aligned");
+  return hip_status(fmxq::launch_quantize(w, wq, scales, biases, rows, K, group_size, bits,
+                                          static_cast<hipStream_t>(stream)),
+                    "quantize");
+}
+
 int fmxq_dequantize_rows(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                          const uint32_t* idx, uint16_t* out, int64_t n_idx, int64_t table_rows,
                          int64_t K, int group_size, int bits, void* stream) {

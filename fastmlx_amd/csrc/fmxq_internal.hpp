@@ -192,6 +192,19 @@ hipError_t launch_route(const RouteArgs& a, bool group, hipStream_t stream);
 // (kind 0 bf16, 1 f16, 2 f32).
 hipError_t launch_scale_neg8(const void* src, void* dst, int64_t n, int kind, hipStream_t stream);
 
+// dst = src with axes d1 and d2 of the row-major view [A, d1, B, d2, C] swapped:
+// dst [A, d2, B, d1, C].  elem_bytes is 1, 2, 4 or 8 (fmx_ingest.hip).
+hipError_t launch_swap_axes(const void* src, void* dst, int64_t A, int64_t d1, int64_t B,
+                            int64_t d2, int64_t C, int elem_bytes, hipStream_t stream);
+
+// MLX affine quantization of bf16 w [rows, K] into packed words wq [rows,
+// K*bits/32] and bf16 scales / biases [rows, K/group_size] (fmxq_quantize.hip).
+// The caller checks bits in {4, 8}, group_size in {32, 64, 128} and
+// K % group_size == 0.
+hipError_t launch_quantize(const uint16_t* w, uint32_t* wq, uint16_t* scales, uint16_t* biases,
+                           int64_t rows, int64_t K, int group_size, int bits,
+                           hipStream_t stream);
+
 // Grouped int4 (group 64, K a multiple of 256) product over expert segments of
 // a sorted slot order (fmxq_moe_gemm.hip).  w/s/b hold NMAT stacks [E, N, .]
 // (gate and up for NMAT = 2, which writes silu(gate) * up); slot s reads x row

@@ -7,6 +7,7 @@ Mirrors, name for name:
     mlxgoDtype, TensorBytes, LoadTensors, MergeTensors     (compute/loader.go)
     LoadCheckpoint, shardFiles                             (compute/checkpoint.go)
     remapInt4, scaleNeg8, stackExperts                     (compute/models/deepseekv3.go:486-592)
+    absorbKVB                                              (compute/models/deepseekv3.go:609-679)
 
 The container header is parsed by libfmxq's native parser
 (fmx_safetensors_parse); tensor bytes go to the device unchanged through
@@ -25,7 +26,8 @@ from typing import Dict, List, Optional, Tuple
 import numpy as np
 
 from ._lib import FmxArray, load
-from .mlxgo import Array, Dtype, MLXError, Stream, _check, scale_neg8, stack, view
+from .mlxgo import (Array, Dtype, MLXError, Stream, _check, contiguous, dequantize, quantize,
+                    reshape, scale_neg8, split_sections, stack, swapaxes, view)
 
 
 class ErrShortBuffer(MLXError):
@@ -308,3 +310,48 @@ def stack_experts(weights: Dict[str, Array], num_layers: int, num_experts: int,
                 for e in range(num_experts):
                     del weights[f"model.layers.{layer}.mlp.experts.{e}.{proj}.{comp}"]
                 weights[f"model.layers.{layer}.mlp.switch_mlp.{proj}.{comp}"] = stacked
+
+
+def absorb_kvb(weights: Dict[str, Array], num_layers: int, num_attention_heads: int,
+               qk_nope_head_dim: int, v_head_dim: int, kv_lora_rank: int,
+               s: Optional[Stream] = None) -> None:
+    """absorbKVB (deepseekv3.go:609-679): each layer's self_attn.kv_b_proj
+    [heads * (nope + v), kv_lora] becomes embed_q [heads, kv_lora, nope] (the nope
+    band, transposed) and unembed_out [heads, v, kv_lora] (the value band).  A
+    quantized kv_b_proj is dequantized first, with bits and group size read off
+    the packed and scale shapes, and both results are requantized with them.
+    A layer without kv_b_proj (already absorbed) is left as it is."""
+    head_dim = qk_nope_head_dim + v_head_dim
+    for layer in range(num_layers):
+        prefix = f"model.layers.{layer}.self_attn"
+        v = weights.pop(prefix + ".kv_b_proj.weight", None)
+        if v is None:
+            continue
+        quantized = False
+        bits = group_size = 0
+        scales = weights.get(prefix + ".kv_b_proj.scales")
+        if scales is not None:
+            quantized = True
+            biases = weights.get(prefix + ".kv_b_proj.biases")
+            if biases is None:
+                raise MLXError(1, f"deepseekv3: kv_b_proj absorption missing "
+                                  f"{prefix + '.kv_b_proj.biases'!r}")
+            del weights[prefix + ".kv_b_proj.scales"]
+            del weights[prefix + ".kv_b_proj.biases"]
+            bits = (v.shape()[-1] * 32) // kv_lora_rank
+            group_size = kv_lora_rank // scales.shape()[-1]
+            v = dequantize(v, scales, biases, group_size, bits, s)
+        v = reshape(v, [num_attention_heads, head_dim, -1], s)
+        nope, val = split_sections(v, [qk_nope_head_dim], 1, s)
+        wk = contiguous(swapaxes(nope, -1, -2, s), s)
+        wv = contiguous(val, s)
+        if quantized:
+            wk_p, wk_s, wk_b = quantize(wk, group_size, bits, s)
+            wv_p, wv_s, wv_b = quantize(wv, group_size, bits, s)
+            weights[prefix + ".embed_q.scales"] = wk_s
+            weights[prefix + ".unembed_out.scales"] = wv_s
+            weights[prefix + ".embed_q.biases"] = wk_b
+            weights[prefix + ".unembed_out.biases"] = wv_b
+            wk, wv = wk_p, wv_p
+        weights[prefix + ".embed_q.weight"] = wk
+        weights[prefix + ".unembed_out.weight"] = wv

@@ -397,6 +397,40 @@ def stack(parts: Sequence[Array], axis: int = 0, s: Optional[Stream] = None) -> 
     return _op(load().fmx_stack, hs, len(parts), int(axis), _sh(s))
 
 
+def quantize(w: Array, group_size: int, bits: int, s: Optional[Stream] = None):
+    """Quantize (mlxgo/binding_cgo.go:684-697): (packed, scales, biases)."""
+    a, b, c = FmxArray(None), FmxArray(None), FmxArray(None)
+    _check(load().fmx_quantize(ctypes.byref(a), ctypes.byref(b), ctypes.byref(c), _ah(w),
+                               int(group_size), int(bits), _sh(s)))
+    return Array(a), Array(b), Array(c)
+
+
+def reshape(a: Array, shape: Sequence[int], s: Optional[Stream] = None) -> Array:
+    """Reshape (mlxgo/binding_cgo.go:398-406); one entry may be -1."""
+    dims = (ctypes.c_int * max(len(shape), 1))(*[int(v) for v in shape])
+    return _op(load().fmx_reshape, _ah(a), dims, len(shape), _sh(s))
+
+
+def split_sections(a: Array, indices: Sequence[int], axis: int,
+                   s: Optional[Stream] = None) -> list:
+    """SplitSections (mlxgo/binding_cgo.go:463-483): len(indices) + 1 parts."""
+    n = len(indices) + 1
+    outs = (FmxArray * n)()
+    idx = (ctypes.c_int * max(len(indices), 1))(*[int(v) for v in indices])
+    _check(load().fmx_split(outs, n, _ah(a), idx, len(indices), int(axis), _sh(s)))
+    return [Array(FmxArray(outs[i].ctx)) for i in range(n)]
+
+
+def swapaxes(a: Array, axis1: int, axis2: int, s: Optional[Stream] = None) -> Array:
+    """Swapaxes (mlxgo/binding_cgo.go:715-722)."""
+    return _op(load().fmx_swapaxes, _ah(a), int(axis1), int(axis2), _sh(s))
+
+
+def contiguous(a: Array, s: Optional[Stream] = None) -> Array:
+    """Contiguous (mlxgo/binding_cgo.go:724-731)."""
+    return _op(load().fmx_contiguous, _ah(a), False, _sh(s))
+
+
 def scale_neg8(scale: Array, s: Optional[Stream] = None) -> Array:
     """-8 * scale in the scale's dtype: Mul by the float32 scalar then Astype back
     (scaleNeg8, deepseekv3.go:539-551)."""

@@ -43,6 +43,23 @@ def dequantize(w, scales, biases, group_size: int = 64, bits: int = 4, out=None)
     return out
 
 
+def quantize(w, group_size: int = 64, bits: int = 4):
+    """MLX affine quantize: bf16 [..., K] -> (packed [..., K*bits/32] int32 words,
+    scales [..., K/group] bf16, biases [..., K/group] bf16)."""
+    K = w.shape[-1]
+    rows = w.numel() // max(K, 1)
+    if K % group_size:
+        raise ValueError(f"K={K} is not a multiple of group_size={group_size}")
+    wq = torch.empty(*w.shape[:-1], K * bits // 32, dtype=torch.int32, device=w.device)
+    scales = torch.empty(*w.shape[:-1], K // group_size, dtype=torch.bfloat16, device=w.device)
+    biases = torch.empty_like(scales)
+    check(load().fmxq_quantize(_dev(w, "w", _BF16_LIKE), _dev(wq, "wq", _U32_LIKE),
+                               _dev(scales, "scales", _BF16_LIKE),
+                               _dev(biases, "biases", _BF16_LIKE), rows, K, group_size, bits,
+                               _stream(w)))
+    return wq, scales, biases
+
+
 def quantized_matmul(x, w, scales, biases, transpose: bool = True, group_size: int = 64,
                      bits: int = 4, bias=None, out=None):
     """y = x @ deq(W)^T over x [..., K]; W [N, K*bits/32]; y [..., N] bf16."""

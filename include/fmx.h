@@ -13,6 +13,8 @@
  *   mlx_quantized_matmul                        binding_cgo.go:636-643
  *   mlx_gather_qmm                              binding_cgo.go:645-673
  *   mlx_dequantize                              binding_cgo.go:675-682
+ *   mlx_quantize, mlx_reshape, mlx_split, mlx_swapaxes, mlx_contiguous
+ *                                               binding_cgo.go:684-697,398-483,715-731
  *
  * Ownership: an op writes a newly allocated result into *res (created empty by
  * fmx_array_new); inputs are borrowed; optional operands (biases, lhs_indices,
@@ -202,6 +204,28 @@ int fmx_stack(fmx_array* res, const fmx_array* arrays, size_t n, int axis, const
 /* -8 * scale in the scale's dtype (bf16, f16, f32): the affine bias of an int4
  * checkpoint (scaleNeg8, compute/models/deepseekv3.go:539-551). */
 int fmx_scale_neg8(fmx_array* res, const fmx_array scale, const fmx_stream s);
+
+/* ---- the kv_b_proj absorption (absorbKVB, compute/models/deepseekv3.go:609-679) ---- */
+/* MLX affine quantization (fmxq_quantize has the arithmetic): w [..., K] bf16,
+ * at least 2-D -> res_0 packed [..., K*bits/32] uint32, res_1 scales and res_2
+ * biases [..., K/group_size] bf16.  Replaces mlx_quantize
+ * (mlxgo/binding_cgo.go:684-697). */
+int fmx_quantize(fmx_array* res_0, fmx_array* res_1, fmx_array* res_2, const fmx_array w,
+                 int group_size, int bits, const fmx_stream s);
+/* Arrays of this layer are always row-major and contiguous, so the next three
+ * return contiguous copies where MLX returns views; the values are MLX's. */
+/* mlx_reshape (binding_cgo.go:398-406): one entry of shape may be -1. */
+int fmx_reshape(fmx_array* res, const fmx_array a, const int* shape, size_t ndim,
+                const fmx_stream s);
+/* mlx_split at explicit indices (binding_cgo.go:463-483).  This ABI has no vector
+ * type: res points to n_res = num_indices + 1 handles, part i covering
+ * [indices[i-1], indices[i]) of axis; indices ascend within [0, dim]. */
+int fmx_split(fmx_array* res, size_t n_res, const fmx_array a, const int* indices,
+              size_t num_indices, int axis, const fmx_stream s);
+/* mlx_swapaxes (binding_cgo.go:715-722). */
+int fmx_swapaxes(fmx_array* res, const fmx_array a, int axis1, int axis2, const fmx_stream s);
+/* mlx_contiguous (binding_cgo.go:724-731): a row-major copy. */
+int fmx_contiguous(fmx_array* res, const fmx_array a, bool allow_col_major, const fmx_stream s);
 
 #ifdef __cplusplus
 }

@@ -10,6 +10,7 @@
  *   fmxq_quantized_matmul  <- mlx_quantized_matmul  (mlxgo/binding_cgo.go:636-643)
  *   fmxq_gather_qmm        <- mlx_gather_qmm        (mlxgo/binding_cgo.go:645-673)
  *   fmxq_dequantize        <- mlx_dequantize        (mlxgo/binding_cgo.go:675-682)
+ *   fmxq_quantize          <- mlx_quantize          (mlxgo/binding_cgo.go:684-697)
  * The array-handle layer with mlx-c's exact argument lists is in fmx.h.
  *
  * Data layout (MLX affine quantization):
@@ -57,6 +58,19 @@ const char* fmxq_last_error(void);
 int fmxq_dequantize(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                     uint16_t* out, int64_t rows, int64_t K, int group_size, int bits,
                     void* stream);
+
+/* MLX affine quantization, the inverse of fmxq_dequantize: w [rows, K] bf16 ->
+ * wq [rows, K*bits/32] uint32, scales and biases [rows, K/group_size] bf16.
+ * Per group of group_size values, in fp32: delta = max((max - min) /
+ * (2^bits - 1), 1e-7); the end of larger magnitude is the edge (min with scale
+ * +delta, else max with scale -delta); q0 = rint(edge / scale); when q0 != 0,
+ * scale = edge / q0 and bias = edge, else bias = 0; q = clamp(rint((w - bias) /
+ * scale), 0, 2^bits - 1).  scale and bias are rounded to nearest-even bf16.
+ * Scales can be negative.  Caller: the kv_b_proj absorption of DeepSeek-V3
+ * (compute/models/deepseekv3.go:662-669).
+ * Replaces mlx_quantize (mlxgo/binding_cgo.go:684-697). */
+int fmxq_quantize(const uint16_t* w, uint32_t* wq, uint16_t* scales, uint16_t* biases,
+                  int64_t rows, int64_t K, int group_size, int bits, void* stream);
 
 /* qembed over a quantized table (compute/models/quant.go:117-142: take rows idx
  * of w, scales and biases, then dequantize) in one kernel:

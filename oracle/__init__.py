@@ -43,6 +43,7 @@ def lib():
             build()
         L = ctypes.CDLL(_LIB)
         L.oracle_dequantize.argtypes = [_p, _p, _p, _p, _i64, _i64, _int, _int, _int]
+        L.oracle_quantize.argtypes = [_p, _p, _p, _p, _i64, _i64, _int, _int]
         L.oracle_qmm_f32.argtypes = [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _int, _int, _int]
         L.oracle_qmm_f64.argtypes = [_p, _p, _p, _p, _p, _i64, _i64, _i64, _int, _int, _int]
         L.oracle_gather_qmm.argtypes = [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64,
@@ -99,6 +100,18 @@ def dequantize(w, scales, biases, group_size=64, bits=4, mode=DEQ_MLX):
     _check(lib().oracle_dequantize(_ptr(w), _ptr(scales), _ptr(biases), _ptr(out),
                                    rows, K, group_size, bits, mode), "dequantize")
     return out
+
+
+def quantize(w, group_size=64, bits=4):
+    """MLX affine quantization of bf16 w [rows, K]: (wq, scales, biases)."""
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    rows, K = w.shape
+    wq = np.empty((rows, K * bits // 32), dtype=np.uint32)
+    scales = np.empty((rows, K // group_size), dtype=np.uint16)
+    biases = np.empty_like(scales)
+    _check(lib().oracle_quantize(_ptr(w), _ptr(wq), _ptr(scales), _ptr(biases), rows, K,
+                                 group_size, bits), "quantize")
+    return wq, scales, biases
 
 
 def qmm(x, w, scales, biases, group_size=64, bits=4, mode=DEQ_MLX, want_f32=False):

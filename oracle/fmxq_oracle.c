@@ -98,6 +98,69 @@ int oracle_dequantize(const uint32_t *w, const uint16_t *scales,
   return 0;
 }
 
+/* MLX affine quantization, the requantize step of absorbKVB
+ * (compute/models/deepseekv3.go:662-669 through mlxgo.Quantize ->
+ * mlx_quantize, mlxgo/binding_cgo.go:684-697; inverse of Dequantize per
+ * binding_stub.go:320-326).  MLX is not vendored, so the per-group steps are
+ * MLX's published affine algorithm, in fp32:
+ *   delta = max((max - min) / (2^bits - 1), 1e-7)
+ *   the end of larger magnitude is the edge: min with scale +delta, else max
+ *   with scale -delta (so q = 0 sits at the edge and q grows inward)
+ *   q0 = rint(edge / scale); if q0 != 0: scale = edge / q0, bias = edge
+ *   (the edge is hit exactly and zero lands on the grid point -q0), else bias 0
+ *   q = clamp(rint((w - bias) / scale), 0, 2^bits - 1)
+ * scales and biases are stored as bf16 (the input's dtype), rounded to
+ * nearest-even.  rint is round-half-to-even (MLX's round op). */
+static void quantize_group(const uint16_t *src, int group_size, int bits, uint32_t *qout,
+                           uint16_t *s_out, uint16_t *b_out) {
+  const float n_bins = (float)((1 << bits) - 1);
+  float mn = oracle_bf16_to_f32(src[0]), mx = mn;
+  for (int i = 1; i < group_size; ++i) {
+    const float v = oracle_bf16_to_f32(src[i]);
+    mn = fminf(mn, v);
+    mx = fmaxf(mx, v);
+  }
+  float delta = (mx - mn) / n_bins;
+  if (!(delta > 1e-7f)) delta = 1e-7f;
+  const int side = fabsf(mn) > fabsf(mx);
+  float scale = side ? delta : -delta;
+  const float edge = side ? mn : mx;
+  const float q0 = rintf(edge / scale);
+  float bias = 0.0f;
+  if (q0 != 0.0f) {
+    scale = edge / q0;
+    bias = edge;
+  }
+  for (int i = 0; i < group_size; ++i) {
+    float q = rintf((oracle_bf16_to_f32(src[i]) - bias) / scale);
+    q = q < 0.0f ? 0.0f : q > n_bins ? n_bins : q;
+    qout[i] = (uint32_t)q;
+  }
+  *s_out = oracle_f32_to_bf16(scale);
+  *b_out = oracle_f32_to_bf16(bias);
+}
+
+int oracle_quantize(const uint16_t *w, uint32_t *wq, uint16_t *scales, uint16_t *biases,
+                    int64_t rows, int64_t K, int group_size, int bits) {
+  if (!supported(group_size, bits, K) || rows < 0) return -1;
+  const int per = 32 / bits;
+  const int64_t wpr = K / per, gpr = K / group_size;
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    uint32_t q[128];
+    for (int64_t g = 0; g < gpr; ++g) {
+      quantize_group(w + r * K + g * group_size, group_size, bits, q, scales + r * gpr + g,
+                     biases + r * gpr + g);
+      for (int i = 0; i < group_size; i += per) {
+        uint32_t word = 0;
+        for (int j = 0; j < per; ++j) word |= q[i + j] << (j * bits);
+        wq[r * wpr + (g * group_size + i) / per] = word;
+      }
+    }
+  }
+  return 0;
+}
+
 int oracle_qmm_f32(const uint16_t *x, const uint32_t *w, const uint16_t *scales,
                    const uint16_t *biases, uint16_t *y, float *y_f32,
                    int64_t M, int64_t N, int64_t K, int group_size, int bits,

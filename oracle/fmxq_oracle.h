@@ -10,6 +10,7 @@
  *   mlxgo/binding_cgo.go:636-643   QuantizedMatMul -> mlx_quantized_matmul
  *   mlxgo/binding_cgo.go:645-673   GatherQMM       -> mlx_gather_qmm
  *   mlxgo/binding_cgo.go:675-682   Dequantize      -> mlx_dequantize
+ *   mlxgo/binding_cgo.go:684-697   Quantize        -> mlx_quantize
  *   compute/models/switch_glu.go:107-153  switchGLUCore choreography
  *   compute/models/qwen3next_forward.go:510-535, deepseekv3_forward.go:427-442
  *
@@ -48,6 +49,14 @@ uint32_t oracle_unpack(const uint32_t *row_words, int64_t k, int bits);
 int oracle_dequantize(const uint32_t *w, const uint16_t *scales,
                       const uint16_t *biases, uint16_t *out, int64_t rows,
                       int64_t K, int group_size, int bits, int mode);
+
+/* MLX affine quantization of w [rows, K] (bf16) into wq [rows, K*bits/32],
+ * scales and biases [rows, K/group] (bf16): the requantize step of absorbKVB
+ * (deepseekv3.go:662-669, mlx_quantize via mlxgo/binding_cgo.go:684-697).
+ * The per-group arithmetic is in fmxq_oracle.c.  Returns 0, or -1 on
+ * unsupported bits/group. */
+int oracle_quantize(const uint16_t *w, uint32_t *wq, uint16_t *scales, uint16_t *biases,
+                    int64_t rows, int64_t K, int group_size, int bits);
 
 /* y[m, n] = sum_k x[m,k] * deq(W)[n,k], accumulated in fp32 in ascending k,
  * rounded once to bf16.  y_f32 (optional) receives the unrounded sums.

@@ -93,6 +93,13 @@ def test_gather_and_dequantize_validation():
     assert _status(d(None, None, None, None, 4, 65, 64, 4, None)) == "FMXQ_ERR_SHAPE"
     assert _status(d(None, None, None, None, 4, 64, 64, 7, None)) == "FMXQ_ERR_UNSUPPORTED"
     assert d(None, None, None, None, 0, 64, 64, 4, None) == 0
+    q = lib.fmxq_quantize
+    assert _status(q(None, None, None, None, 4, 96, 64, 4, None)) == "FMXQ_ERR_SHAPE"
+    assert _status(q(None, None, None, None, 4, 64, 64, 2, None)) == "FMXQ_ERR_UNSUPPORTED"
+    assert _status(q(None, None, None, None, 4, 64, 48, 4, None)) == "FMXQ_ERR_UNSUPPORTED"
+    assert _status(q(None, None, None, None, -1, 64, 64, 4, None)) == "FMXQ_ERR_SHAPE"
+    assert _status(q(None, None, None, None, 4, 64, 64, 4, None)) == "FMXQ_ERR_INVALID_ARGUMENT"
+    assert q(None, None, None, None, 0, 64, 64, 4, None) == 0
 
 
 def test_switch_glu_and_combine_validation():

@@ -1,0 +1,171 @@
+"""GPU parity: MLX affine quantize (fmxq_quantize / fmx_quantize) against the
+oracle, bit for bit, and the kv_b_proj absorption of DeepSeek-V3 (absorbKVB,
+compute/models/deepseekv3.go:609-679) built from the array ops fmx_reshape,
+fmx_split, fmx_swapaxes, fmx_contiguous, fmx_dequantize and fmx_quantize.
+"""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import announce, to_dev, to_np
+from synth import make_quant
+
+pytestmark = pytest.mark.gpu
+
+
+def _special_rows(oracle, K):
+    """Rows whose groups hit each branch: exact grids with either edge, constant,
+    zero and sub-floor groups, and a snapped range."""
+    rows = []
+    base = np.linspace(-0.5, 0.4375, K, dtype=np.float32)
+    rows.append(base)                                   # min edge, exact grid steps
+    rows.append(base[::-1].copy() + np.float32(0.25))   # max edge
+    rows.append(np.full(K, 0.375, np.float32))          # constant
+    rows.append(np.zeros(K, np.float32))                # zeros
+    rows.append(np.full(K, 1e-30, np.float32))          # below the 1e-7 floor
+    snap = np.linspace(-1.0, 0.9, K, dtype=np.float32)
+    snap[K // 2] = 0.0
+    rows.append(snap)
+    rows.append(-np.abs(np.linspace(0.1, 3.0, K, dtype=np.float32)))  # all negative
+    return oracle.f32_to_bf16(np.stack(rows))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("group", [32, 64, 128])
+@pytest.mark.parametrize("rows,K", [(1, 128), (7, 384), (33, 1024), (300, 96 * 4)])
+def test_quantize_bit_exact(gpu, oracle, bits, group, rows, K):
+    from fastmlx_amd import ops
+
+    if K % group:
+        pytest.skip("K not a multiple of the group")
+    rng = np.random.default_rng(rows * 31 + K + bits + group)
+    w = oracle.f32_to_bf16((rng.standard_normal((rows, K)) *
+                            rng.uniform(0.01, 4.0, size=(rows, 1))).astype(np.float32))
+    special = _special_rows(oracle, K)
+    w[: min(rows, len(special))] = special[: min(rows, len(special))]
+    announce(f"quantize bits={bits} group={group} rows={rows} K={K}")
+    wq, s, b = ops.quantize(to_dev(w, gpu), group, bits)
+    torch.cuda.synchronize()
+    rq, rs, rb = oracle.quantize(w, group, bits)
+    assert np.array_equal(to_np(wq, np.uint32), rq)
+    assert np.array_equal(to_np(s), rs)
+    assert np.array_equal(to_np(b), rb)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_quantize_full_size_and_round_trip(gpu, oracle, bits):
+    """DeepSeek-V3's kv_b_proj shape (128 heads x 256 rows, kv_lora 512) and the
+    absorbed embed_q layout (128 x 512 rows of 128): bit-exact against the oracle,
+    and quantize -> dequantize on the device equals the oracle's round trip."""
+    from fastmlx_amd import ops
+
+    rng = np.random.default_rng(40 + bits)
+    for rows, K in ((32768, 512), (65536, 128)):
+        w = oracle.f32_to_bf16((rng.standard_normal((rows, K)) * 0.02).astype(np.float32))
+        announce(f"quantize full size bits={bits} {rows}x{K}")
+        wq, s, b = ops.quantize(to_dev(w, gpu), 64, bits)
+        deq = ops.dequantize(wq, s, b, 64, bits)
+        torch.cuda.synchronize()
+        rq, rs, rb = oracle.quantize(w, 64, bits)
+        assert np.array_equal(to_np(wq, np.uint32), rq)
+        assert np.array_equal(to_np(s), rs) and np.array_equal(to_np(b), rb)
+        assert np.array_equal(to_np(deq), oracle.dequantize(rq, rs, rb, 64, bits))
+
+
+def test_array_ops_match_numpy(gpu):
+    """reshape / split / swapaxes / contiguous against numpy on several dtypes,
+    including non-adjacent axes, negative axes and empty split parts."""
+    from fastmlx_amd.mlxgo import (Array, MLXError, contiguous, reshape, split_sections,
+                                   swapaxes)
+
+    rng = np.random.default_rng(8)
+    announce("array ops")
+    for dt in (np.uint8, np.uint16, np.float32, np.int64):
+        a = rng.integers(0, 100, size=(3, 4, 5, 6)).astype(dt)
+        A = Array.from_numpy(a)
+        r = reshape(A, [12, -1])
+        assert r.shape() == [12, 30] and np.array_equal(r.to_numpy(), a.reshape(12, 30))
+        for ax1, ax2 in ((0, 3), (1, 2), (-1, -2), (2, 2), (3, 0)):
+            got = swapaxes(A, ax1, ax2).to_numpy()
+            assert np.array_equal(got, np.swapaxes(a, ax1, ax2)), (dt, ax1, ax2)
+        for axis, idx in ((1, [1, 3]), (-1, [0, 2, 2, 6]), (0, [3])):
+            parts = split_sections(A, idx, axis)
+            want = np.split(a, idx, axis=axis)
+            assert len(parts) == len(want)
+            for p, w in zip(parts, want):
+                assert p.shape() == list(w.shape)
+                if w.size:
+                    assert np.array_equal(p.to_numpy(), w)
+        assert np.array_equal(contiguous(A).to_numpy(), a)
+    with pytest.raises(MLXError):
+        reshape(A, [7, -1])
+    with pytest.raises(MLXError):
+        split_sections(A, [4, 2], 1)
+    with pytest.raises(MLXError):
+        swapaxes(A, 0, 4)
+
+
+def _absorb_case(rng, heads, nope, vdim, kv_lora, group, bits, quantized):
+    from fastmlx_amd.mlxgo import Array
+
+    rows = heads * (nope + vdim)
+    prefix = "model.layers.0.self_attn"
+    if quantized:
+        w, s, b = make_quant(rng, (rows,), kv_lora, bits, group)
+        weights = {prefix + ".kv_b_proj.weight": Array.from_numpy(w),
+                   prefix + ".kv_b_proj.scales": Array.from_numpy(s, dtype=_bf16()),
+                   prefix + ".kv_b_proj.biases": Array.from_numpy(b, dtype=_bf16())}
+        return weights, (w, s, b)
+    dense = rng.integers(0, 1 << 16, size=(rows, kv_lora)).astype(np.uint16) & np.uint16(0xBFFF)
+    return {prefix + ".kv_b_proj.weight": Array.from_numpy(dense, dtype=_bf16())}, dense
+
+
+def _bf16():
+    from fastmlx_amd.mlxgo import Dtype
+    return Dtype.BFLOAT16
+
+
+@pytest.mark.parametrize("bits,group", [(4, 64), (8, 32), (4, 128)])
+def test_absorb_kvb_quantized(gpu, oracle, bits, group):
+    """A quantized kv_b_proj [heads*(nope+v), kv_lora]: bits and group size are read
+    off the packed and scale shapes; embed_q is the nope band transposed to
+    [heads, kv_lora, nope] and unembed_out the value band [heads, v, kv_lora],
+    each requantized -- compared bit for bit with the oracle's dequantize, numpy's
+    reshape / split / swapaxes and the oracle's quantize."""
+    from fastmlx_amd import loader
+
+    heads, nope, vdim, kv_lora = 4, 128, 64, 256
+    rng = np.random.default_rng(bits + group)
+    weights, (w, s, b) = _absorb_case(rng, heads, nope, vdim, kv_lora, group, bits, True)
+    announce(f"absorb_kvb quantized bits={bits} group={group}")
+    loader.absorb_kvb(weights, 1, heads, nope, vdim, kv_lora)
+    prefix = "model.layers.0.self_attn"
+    assert sorted(weights) == sorted(prefix + f".{p}.{c}" for p in ("embed_q", "unembed_out")
+                                     for c in ("weight", "scales", "biases"))
+    v = oracle.dequantize(w, s, b, group, bits).reshape(heads, nope + vdim, kv_lora)
+    wk = np.ascontiguousarray(np.swapaxes(v[:, :nope], -1, -2))   # [heads, kv_lora, nope]
+    wv = np.ascontiguousarray(v[:, nope:])                         # [heads, v, kv_lora]
+    for name, ref in (("embed_q", wk), ("unembed_out", wv)):
+        rq, rs, rb = oracle.quantize(ref.reshape(-1, ref.shape[-1]), group, bits)
+        got_w = weights[f"{prefix}.{name}.weight"]
+        assert got_w.shape() == list(ref.shape[:-1]) + [ref.shape[-1] * bits // 32]
+        assert np.array_equal(got_w.to_numpy().reshape(rq.shape), rq)
+        assert np.array_equal(weights[f"{prefix}.{name}.scales"].to_numpy().reshape(rs.shape), rs)
+        assert np.array_equal(weights[f"{prefix}.{name}.biases"].to_numpy().reshape(rb.shape), rb)
+
+
+def test_absorb_kvb_dense(gpu):
+    """A bf16 kv_b_proj is split and transposed, not quantized."""
+    from fastmlx_amd import loader
+
+    heads, nope, vdim, kv_lora = 3, 32, 16, 64
+    rng = np.random.default_rng(2)
+    weights, dense = _absorb_case(rng, heads, nope, vdim, kv_lora, 0, 0, False)
+    announce("absorb_kvb dense")
+    loader.absorb_kvb(weights, 1, heads, nope, vdim, kv_lora)
+    prefix = "model.layers.0.self_attn"
+    assert sorted(weights) == [prefix + ".embed_q.weight", prefix + ".unembed_out.weight"]
+    v = dense.reshape(heads, nope + vdim, kv_lora)
+    assert np.array_equal(weights[prefix + ".embed_q.weight"].to_numpy(),
+                          np.swapaxes(v[:, :nope], -1, -2))
+    assert np.array_equal(weights[prefix + ".unembed_out.weight"].to_numpy(), v[:, nope:])

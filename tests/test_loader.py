@@ -194,3 +194,19 @@ def test_stack_experts_host_rules():
                "model.layers.0.mlp.experts.1.gate_proj.weight": 0}
     with pytest.raises(MLXError):
         loader.stack_experts(missing, 1, 3)
+
+
+def test_absorb_kvb_host_rules():
+    """TestAbsorbKVB's host-side cases (deepseekv3_test.go:398-447): a quantized
+    kv_b_proj without biases is a missing-key error raised before any device op,
+    and a checkpoint already carrying embed_q / unembed_out (no kv_b_proj) passes
+    through untouched."""
+    prefix = "model.layers.0.self_attn"
+    missing = {prefix + ".kv_b_proj.weight": 0, prefix + ".kv_b_proj.scales": 0}
+    with pytest.raises(MLXError) as ei:
+        loader.absorb_kvb(missing, 1, 4, 64, 32, 128)
+    assert "kv_b_proj.biases" in str(ei.value)
+    absorbed = {prefix + ".embed_q.weight": 0, prefix + ".unembed_out.weight": 0}
+    loader.absorb_kvb(absorbed, 1, 4, 64, 32, 128)
+    assert sorted(absorbed) == [prefix + ".embed_q.weight", prefix + ".unembed_out.weight"]
+    assert absorbed[prefix + ".embed_q.weight"] == 0

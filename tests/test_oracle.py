@@ -127,6 +127,168 @@ def test_dequant_vs_fp64_brute_force(oracle):
     assert not np.all(np.abs(qs - exact) <= bound)
 
 
+# ---------------------------------------------------------------- quantize
+# The requantize of absorbKVB (deepseekv3.go:662-669).  MLX's algorithm is not in
+# the image and no reference fixture holds a quantized number, so the pins are
+# what the algorithm fixes by construction: exact grids come back exactly (with
+# the edge branch deciding the sign of the scale), the snap puts zero on the
+# grid, constant groups reproduce, and the round-trip error of random data stays
+# within a grid step.
+
+
+def _grid(rng, rows, K, group, bits, base):
+    """Rows whose every group is base + q * 2^-(bits) with q covering 0 .. 2^bits - 1
+    at random positions: every value, product and sum is exact in bf16."""
+    n = (1 << bits) - 1
+    q = rng.integers(0, n + 1, size=(rows, K)).astype(np.uint32)
+    for g in range(K // group):
+        for r in range(rows):
+            i, j = rng.choice(group, size=2, replace=False)
+            q[r, g * group + i] = 0
+            q[r, g * group + j] = n
+    step = np.float32(2.0 ** -bits)
+    w = np.float32(base) + q.astype(np.float32) * step
+    w16 = oracle_f32_to_bf16(w)
+    assert np.array_equal(oracle_bf16_to_f32(w16), w)
+    return q, w16, step
+
+
+def oracle_f32_to_bf16(f):
+    from oracle import f32_to_bf16
+    return f32_to_bf16(np.asarray(f, dtype=np.float32))
+
+
+def oracle_bf16_to_f32(h):
+    from oracle import bf16_to_f32
+    return bf16_to_f32(h)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("group", [32, 64, 128])
+def test_quantize_exact_grid_min_edge(oracle, bits, group):
+    """|min| > |max|: the edge is the minimum, the scale is +step, q is the grid."""
+    rng = np.random.default_rng(bits * 7 + group)
+    q, w, step = _grid(rng, 6, 256, group, bits, -0.5)
+    wq, s, b = oracle.quantize(w, group, bits)
+    assert np.array_equal(wq, pack(q, bits))
+    assert np.all(s == oracle_f32_to_bf16(step)) and np.all(b == oracle_f32_to_bf16(-0.5))
+    assert np.array_equal(oracle.dequantize(wq, s, b, group, bits), w)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("group", [32, 64, 128])
+def test_quantize_exact_grid_max_edge(oracle, bits, group):
+    """|max| >= |min|: the edge is the maximum, the scale is -step and q counts down
+    from it (q' = n - q), so the values still come back exactly."""
+    rng = np.random.default_rng(bits * 11 + group)
+    n = (1 << bits) - 1
+    q, w, step = _grid(rng, 6, 256, group, bits, -0.25)
+    wq, s, b = oracle.quantize(w, group, bits)
+    assert np.array_equal(wq, pack(n - q, bits))
+    assert np.all(s == oracle_f32_to_bf16(-step))
+    assert np.all(b == oracle_f32_to_bf16(np.float32(-0.25) + n * step))
+    assert np.array_equal(oracle.dequantize(wq, s, b, group, bits), w)
+
+
+@pytest.mark.parametrize("bits,hi,scale,qmax", [(4, 0.9, 0.125, 15), (8, 0.99, 2.0 ** -7, 254)])
+def test_quantize_snaps_zero_onto_the_grid(oracle, bits, hi, scale, qmax):
+    """min -1, max just below 1: delta = range / n is off the powers of two, but
+    q0 = rint(-1 / delta) is a power of two, so the snapped scale -1 / q0 is exact
+    and the edge -1 and the zero element come back exactly.  Without the snap
+    (scale = delta) zero would not.  The maximum: (0.8984375 + 1) * 8 = 15.19 -> 15;
+    (0.98828125 + 1) * 128 = 254.5, a tie, -> 254 (rint rounds half to even)."""
+    rng = np.random.default_rng(bits)
+    K = 64
+    n = (1 << bits) - 1
+    v = rng.uniform(-0.9, 0.8, size=K).astype(np.float32)
+    v[3], v[17], v[40] = -1.0, hi, 0.0
+    w = oracle_f32_to_bf16(v).reshape(1, K)
+    wq, s, b = oracle.quantize(w, 64, bits)
+    assert oracle_bf16_to_f32(s)[0, 0] == np.float32(scale)
+    assert oracle_bf16_to_f32(b)[0, 0] == np.float32(-1.0)
+    got = oracle_bf16_to_f32(oracle.dequantize(wq, s, b, 64, bits))[0]
+    assert got[3] == -1.0 and got[40] == 0.0
+    assert unpack(wq, bits)[0, 17] == qmax
+    # the unsnapped scale misses zero
+    x = oracle_bf16_to_f32(w)[0]
+    delta = np.float32((x.max() - x.min()) / np.float32(n))
+    qz = np.rint(np.float32(1.0) / delta)
+    assert qz * oracle_bf16_to_f32(oracle_f32_to_bf16(delta)) - 1.0 != 0.0
+
+
+def test_quantize_constant_and_zero_groups(oracle):
+    """A constant group has range 0: the scale is the 1e-7 floor with the max-edge
+    sign, every q is 0 and the bias is the value itself.  A group of zeros, or of
+    values below half the floor (1e-30 here), has q0 = 0: no snap, bias 0, and the
+    group dequantizes to zeros."""
+    K = 128
+    w = oracle_f32_to_bf16(np.concatenate([np.full(32, 0.375), np.full(32, -2.5),
+                                           np.zeros(32), np.full(32, 1e-30)]).astype(np.float32)
+                           ).reshape(1, K)
+    for bits in (4, 8):
+        wq, s, b = oracle.quantize(w, 32, bits)
+        assert np.all(wq == 0)
+        sf, bf = oracle_bf16_to_f32(s)[0], oracle_bf16_to_f32(b)[0]
+        assert bf.tolist() == [0.375, -2.5, 0.0, 0.0]
+        assert sf[2] == sf[3] == oracle_bf16_to_f32(oracle_f32_to_bf16(np.float32(-1e-7)))
+        assert np.all(sf < 0)
+        want = w.copy()
+        want[0, 96:] = 0
+        assert np.array_equal(oracle.dequantize(wq, s, b, 32, bits), want)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("group", [32, 64, 128])
+def test_quantize_round_trip_error(oracle, bits, group):
+    """Random data: every element comes back within one snapped grid step (the far
+    end can sit up to one step past the last point before the clamp) plus the bf16
+    roundings of scale, bias and the dequantized value; the mean error is a quarter
+    step, as for rounding to a uniform grid, plus at 8 bits the bf16 roundings,
+    which are then a sizeable part of a step (a q off by one would make it ~1)."""
+    rng = np.random.default_rng(bits + group)
+    n = (1 << bits) - 1
+    w = oracle_f32_to_bf16(rng.standard_normal((40, 512)).astype(np.float32) *
+                           np.float32(0.05))
+    wq, s, b = oracle.quantize(w, group, bits)
+    q = unpack(wq, bits)
+    assert q.max() <= n
+    x = oracle_bf16_to_f32(w).astype(np.float64)
+    got = oracle_bf16_to_f32(oracle.dequantize(wq, s, b, group, bits)).astype(np.float64)
+    sr = np.repeat(np.abs(oracle_bf16_to_f32(s)), group, axis=1).astype(np.float64)
+    br = np.repeat(np.abs(oracle_bf16_to_f32(b)), group, axis=1).astype(np.float64)
+    err = np.abs(got - x)
+    assert np.all(err <= sr + 2.0 ** -8 * (n * sr + br + np.abs(x)))
+    lo, hi = (0.2, 0.3) if bits == 4 else (0.25, 0.5)
+    assert lo < np.mean(err / sr) < hi
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("group", [32, 64, 128])
+def test_quantize_matches_independent_numpy(oracle, bits, group):
+    """The same steps vectorised in numpy float32 (grouping, branch selection and
+    packing done independently): catches indexing and packing slips in the C
+    loops."""
+    rng = np.random.default_rng(3 * bits + group)
+    n = np.float32((1 << bits) - 1)
+    w = oracle_f32_to_bf16(rng.standard_normal((17, 384)).astype(np.float32))
+    x = oracle_bf16_to_f32(w).reshape(17, -1, group)
+    mn, mx = x.min(axis=-1, keepdims=True), x.max(axis=-1, keepdims=True)
+    delta = (mx - mn) / n
+    delta = np.where(delta > np.float32(1e-7), delta, np.float32(1e-7)).astype(np.float32)
+    side = np.abs(mn) > np.abs(mx)
+    scale = np.where(side, delta, -delta).astype(np.float32)
+    edge = np.where(side, mn, mx).astype(np.float32)
+    q0 = np.rint(edge / scale).astype(np.float32)
+    snap = q0 != 0
+    scale = np.where(snap, edge / np.where(snap, q0, np.float32(1)), scale).astype(np.float32)
+    bias = np.where(snap, edge, np.float32(0)).astype(np.float32)
+    q = np.clip(np.rint((x - bias) / scale), 0, n).astype(np.uint32).reshape(17, -1)
+    wq, s, b = oracle.quantize(w, group, bits)
+    assert np.array_equal(wq, pack(q, bits))
+    assert np.array_equal(s, oracle_f32_to_bf16(scale[..., 0]))
+    assert np.array_equal(b, oracle_f32_to_bf16(bias[..., 0]))
+
+
 # ---------------------------------------------------------------- quantized_matmul
 
 @pytest.mark.parametrize("bits", [4, 8])
