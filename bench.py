@@ -288,6 +288,49 @@ def dense_point(torch, ops, mats, M, N, K, bits, gen, dev):
             "distinct_copies": len(mats), "launches_per_graph": n}
 
 
+def ingest_points(torch, ops, gen, dev, cpu):
+    """quantize and dequantize at one DeepSeek-V3 kv_b_proj band: [128 heads x 256,
+    512] bf16, int4 group 64 (the requantize and the dequantize of absorbKVB,
+    deepseekv3.go:633,662-669), over 16 distinct copies (a graph of 64 launches).
+    HBM bytes per call: the bf16 values, the packed words and the scale/bias pairs."""
+    from fastmlx_amd.roofline import HBM_PEAK_GBS
+
+    rows, K, bits = 32768, 512, 4
+    by = rows * K * 2 + rows * K * bits // 8 + rows * (K // GROUP) * 4
+    src = [(torch.randn(rows, K, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+           for _ in range(16)]
+    trips = [ops.quantize(t, GROUP, bits) for t in src]
+    deq = torch.empty(rows, K, device=dev, dtype=torch.bfloat16)
+    seq = list(range(len(src))) * 4
+
+    def fq():
+        for i in seq:
+            ops.quantize(src[i], GROUP, bits, out=trips[i])
+
+    def fd():
+        for i in seq:
+            ops.dequantize(*trips[i], GROUP, bits, out=deq)
+    out, cpu_out = {}, {}
+    for name, fn in (("quantize", fq), ("dequantize", fd)):
+        ms = time_graph(torch, capture(torch, fn), 10, 2) / len(seq)
+        gbps = by / (ms * 1e-3) / 1e9
+        out[f"ingest_{name}_32768x512_4bit"] = {
+            "us": round(ms * 1e3, 3), "GBps": round(gbps, 1),
+            "frac_hbm": round(gbps / HBM_PEAK_GBS, 4), "bytes_per_call": by,
+            "distinct_copies": len(src), "launches_per_graph": len(seq)}
+    if cpu:
+        import oracle
+
+        h = host_np(torch, src[0])
+        t0 = time.perf_counter()
+        oracle.quantize(h, GROUP, bits)
+        dt = time.perf_counter() - t0
+        cpu_out["ingest_quantize_32768x512_4bit"] = {
+            "value": round(by / dt / 1e9, 3), "unit": "GB/s", "cores": oracle.num_threads(),
+            "kind": "port", "sample": "one 32768x512 band, oracle_quantize (OpenMP)"}
+    return out, cpu_out
+
+
 def moe_points(torch, ops, gen, dev, cpu):
     """Configs 3 and 4: one MoE layer per step.
     - The step is switch_glu_combine: SwitchGLU over the routed experts and the
@@ -573,6 +616,9 @@ def main():
             cpu_points["c2_4bit_14336x4096_M2048"] = cpu_qmm_point(torch, w, s, b, 2048, 4096, 4)
             cpu_points["c2_4bit_14336x4096_M2048"]["gpu_over_cpu"] = round(
                 qm["TFLOPs"] / max(cpu_points["c2_4bit_14336x4096_M2048"]["value"], 1e-9), 1)
+        ing, ing_cpu = ingest_points(torch, ops, gen, dev, not args.no_cpu)
+        extra.update(ing)
+        cpu_points.update(ing_cpu)
         if not args.no_moe:
             moe, moe_cpu = moe_points(torch, ops, gen, dev, not args.no_cpu)
             extra.update(moe)

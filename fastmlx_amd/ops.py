@@ -43,16 +43,21 @@ def dequantize(w, scales, biases, group_size: int = 64, bits: int = 4, out=None)
     return out
 
 
-def quantize(w, group_size: int = 64, bits: int = 4):
+def quantize(w, group_size: int = 64, bits: int = 4, out=None):
     """MLX affine quantize: bf16 [..., K] -> (packed [..., K*bits/32] int32 words,
-    scales [..., K/group] bf16, biases [..., K/group] bf16)."""
+    scales [..., K/group] bf16, biases [..., K/group] bf16); ``out`` may hold the
+    three result tensors."""
     K = w.shape[-1]
     rows = w.numel() // max(K, 1)
     if K % group_size:
         raise ValueError(f"K={K} is not a multiple of group_size={group_size}")
-    wq = torch.empty(*w.shape[:-1], K * bits // 32, dtype=torch.int32, device=w.device)
-    scales = torch.empty(*w.shape[:-1], K // group_size, dtype=torch.bfloat16, device=w.device)
-    biases = torch.empty_like(scales)
+    if out is None:
+        wq = torch.empty(*w.shape[:-1], K * bits // 32, dtype=torch.int32, device=w.device)
+        scales = torch.empty(*w.shape[:-1], K // group_size, dtype=torch.bfloat16,
+                             device=w.device)
+        biases = torch.empty_like(scales)
+    else:
+        wq, scales, biases = out
     check(load().fmxq_quantize(_dev(w, "w", _BF16_LIKE), _dev(wq, "wq", _U32_LIKE),
                                _dev(scales, "scales", _BF16_LIKE),
                                _dev(biases, "biases", _BF16_LIKE), rows, K, group_size, bits,
