@@ -439,7 +439,8 @@ def probe(args):
     Dense cases rotate --copies weight copies (16 copies of a 29 MB matrix exceed
     the 256 MB last-level cache); moe_c3 / moe_c4 run one SwitchGLU per launch at
     --tokens (with --combine, switch_glu_combine with softmax routing weights, the
-    call the bench times); copy is a plain device copy of --mib MiB, which reads
+    call the bench times); quantize / dequantize run one DeepSeek-V3 kv_b_proj band
+    (32768 x 512, int4 group 64) per launch; copy is a plain device copy of --mib MiB, which reads
     and writes exactly that many bytes per dispatch (the byte counters'
     calibration)."""
     import torch
@@ -459,6 +460,21 @@ def probe(args):
         for _ in range(args.launches):
             dst.copy_(src)
         info.update(read_bytes=n, write_bytes=n)
+    elif args.probe in ("quantize", "dequantize"):
+        rows, K, bits = 32768, 512, 4
+        src = [(torch.randn(rows, K, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+               for _ in range(args.copies)]
+        trips = [ops.quantize(t, GROUP, bits) for t in src]
+        deq = torch.empty(rows, K, device=dev, dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        for i in range(args.launches):
+            j = i % args.copies
+            if args.probe == "quantize":
+                ops.quantize(src[j], GROUP, bits, out=trips[j])
+            else:
+                ops.dequantize(*trips[j], GROUP, bits, out=deq)
+        info.update(rows=rows, K=K, bits=bits, copies=args.copies,
+                    algorithmic_bytes=rows * K * 2 + rows * K * bits // 8 + rows * (K // GROUP) * 4)
     elif args.probe in ("moe_c3", "moe_c4"):
         c3 = args.probe == "moe_c3"
         E, D, I, k = (512, 2048, 512, 10) if c3 else (256, 7168, 2048, 8)
@@ -517,7 +533,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="skip the secondary points")
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE layer points")
-    ap.add_argument("--probe", choices=sorted(PROBES) + ["moe_c3", "moe_c4", "copy"],
+    ap.add_argument("--probe", choices=sorted(PROBES) + ["moe_c3", "moe_c4", "copy", "quantize",
+                                                         "dequantize"],
                     help="run one workload for a profiler instead of the benchmark")
     ap.add_argument("--launches", type=int, default=64)
     ap.add_argument("--copies", type=int, default=16)

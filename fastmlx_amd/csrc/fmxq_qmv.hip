@@ -311,23 +311,30 @@ static hipError_t launch_qmv1(const QmmArgs& a, hipStream_t stream) {
 // weight loads of a wave are in flight at once, and the lane's x chunk serves all
 // RW rows.  Loads are issued x, scales and biases, then weights, so the x pairs
 // and the scale/bias table are built while the weights are on their way:
-//   - the scales (and the biases) of the block's RG * RW rows are one contiguous
-//     run of the array: thread t loads its 16-byte piece t of each, so the run
-//     reaches memory as whole coalesced lines rather than as each wave's 64-byte
-//     slice of every row (4096 x 4096: 3.97 -> 3.87 us, 1024 x 4096: 2.71 -> 2.65
-//     us); the pieces are interleaved into (scale | bias << 16) words in a block
-//     LDS table [rows][K / 64], from which lane l of slice ks reads group
-//     32 ks + l / 2 of each row after one barrier;
+//   - with two slices (4096-deep rows) the scales (and the biases) of the block's
+//     RG * RW rows are one contiguous run of the array: thread t loads its
+//     16-byte piece t of each, so the run reaches memory as whole coalesced lines
+//     rather than as each wave's 64-byte slice of every row (4096 x 4096: 3.97 ->
+//     3.87 us, 1024 x 4096: 2.71 -> 2.65 us); the pieces are interleaved into
+//     (scale | bias << 16) words in a block LDS table [rows][K / 64], from which
+//     lane l of slice ks reads group 32 ks + l / 2 of each row after one barrier;
+//   - longer rows keep per-wave pieces (lane L -> row L / 4, groups 8 (L % 4) ..
+//     +7 of the slice) in a wave-private table [RW][32], no barrier;
 //   - a block is RG row groups x KS slices; the slices meet in LDS.
 // Arithmetic as in qmv1_kernel.
 template <int RW, int KS, int RG>
 __global__ __launch_bounds__(KS * RG * 64) void qmv1_slice_kernel(QmmArgs a) {
   constexpr int LV = __builtin_ctz(RW);
+  // Two-slice (4096-deep) rows load the block's scales as contiguous runs into a
+  // shared table; longer rows keep each wave's own pieces (measured no faster as
+  // runs on 4096 x 14336).
+  constexpr bool BS = KS <= 2;
   constexpr int PPR = KS * 4;             // 16-byte scale pieces per row (K / 512)
   constexpr int NPC = RG * RW * PPR;      // pieces of the block's rows
-  static_assert(NPC <= KS * RG * 64, "one piece per thread");
+  constexpr int NP = (RW * 4 + 63) / 64;  // per-wave form: piece loads per lane
+  static_assert(!BS || NPC <= KS * RG * 64, "one piece per thread");
   __shared__ float part[RG][KS][RW];
-  __shared__ __attribute__((aligned(16))) uint32_t sbt[RG * RW][KS * 32];
+  __shared__ __attribute__((aligned(16))) uint32_t sbt[BS ? RG * RW : KS * RG][BS ? KS * 32 : RW * 32];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int rg = wave / KS, ks = wave % KS;
@@ -346,17 +353,33 @@ __global__ __launch_bounds__(KS * RG * 64) void qmv1_slice_kernel(QmmArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) xr[j] = xs[j];
   }
-  // The scales and biases of the block's rows are one contiguous run of each
-  // array: thread t loads 16-byte piece t of both (rows past N re-read row N - 1).
+  // Block form: the scales and biases of the block's rows are one contiguous run
+  // of each array, thread t loading 16-byte piece t of both.  Per-wave form: lane
+  // L loads piece L % 4 of the wave's slice of row L / 4.  Rows past N re-read
+  // row N - 1.
   const int tid = threadIdx.x;
-  const int prow = tid / PPR, ppc = tid % PPR;
-  u32x4 ps, pb;
-  if (tid < NPC) {
-    const int n = min(__builtin_amdgcn_readfirstlane((int)((int64_t)blockIdx.x * RG * RW)) + prow,
-                      nlast);
-    const int64_t off = (int64_t)n * gpr + ppc * 8;
-    ps = *reinterpret_cast<const u32x4*>(a.scales + off);
-    pb = *reinterpret_cast<const u32x4*>(a.biases + off);
+  const int prow = BS ? tid / PPR : 0, ppc = BS ? tid % PPR : 0;
+  u32x4 ps[NP], pb[NP];
+  if constexpr (BS) {
+    if (tid < NPC) {
+      const int n =
+          min(__builtin_amdgcn_readfirstlane((int)((int64_t)blockIdx.x * RG * RW)) + prow, nlast);
+      const int64_t off = (int64_t)n * gpr + ppc * 8;
+      ps[0] = *reinterpret_cast<const u32x4*>(a.scales + off);
+      pb[0] = *reinterpret_cast<const u32x4*>(a.biases + off);
+    }
+  } else {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int L = lane + 64 * p;
+      const int r = L >> 2, pc = L & 3;
+      if (r < RW) {
+        const int n = min(nb32 + r, nlast);
+        const int64_t off = (int64_t)n * gpr + ks * 32 + pc * 8;
+        ps[p] = *reinterpret_cast<const u32x4*>(a.scales + off);
+        pb[p] = *reinterpret_cast<const u32x4*>(a.biases + off);
+      }
+    }
   }
   // Keep the weight loads behind x and the pieces: the wait for those then does
   // not hold on the weights.
@@ -382,25 +405,37 @@ __global__ __launch_bounds__(KS * RG * 64) void qmv1_slice_kernel(QmmArgs a) {
     }
     xc.sum = s;
   }
-  // (scale | bias << 16) table of the block's rows, shared by its waves.
-  if (tid < NPC) {
+  // (scale | bias << 16) words: the block's table (after one barrier), or the
+  // wave's own [RW][32] table, written and read by that wave only (LDS operations
+  // of one wave complete in order, so no barrier).
+  auto interleave = [&](int p, uint32_t* dst) {
     u32x4 o0, o1;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      o0[2 * h] = __builtin_amdgcn_perm(pb[h], ps[h], 0x05040100u);
-      o0[2 * h + 1] = __builtin_amdgcn_perm(pb[h], ps[h], 0x07060302u);
-      o1[2 * h] = __builtin_amdgcn_perm(pb[2 + h], ps[2 + h], 0x05040100u);
-      o1[2 * h + 1] = __builtin_amdgcn_perm(pb[2 + h], ps[2 + h], 0x07060302u);
+      o0[2 * h] = __builtin_amdgcn_perm(pb[p][h], ps[p][h], 0x05040100u);
+      o0[2 * h + 1] = __builtin_amdgcn_perm(pb[p][h], ps[p][h], 0x07060302u);
+      o1[2 * h] = __builtin_amdgcn_perm(pb[p][2 + h], ps[p][2 + h], 0x05040100u);
+      o1[2 * h + 1] = __builtin_amdgcn_perm(pb[p][2 + h], ps[p][2 + h], 0x07060302u);
     }
-    *reinterpret_cast<u32x4*>(&sbt[prow][ppc * 8]) = o0;
-    *reinterpret_cast<u32x4*>(&sbt[prow][ppc * 8 + 4]) = o1;
+    *reinterpret_cast<u32x4*>(dst) = o0;
+    *reinterpret_cast<u32x4*>(dst + 4) = o1;
+  };
+  if constexpr (BS) {
+    if (tid < NPC) interleave(0, &sbt[prow][ppc * 8]);
+    __syncthreads();
+  } else {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int L = lane + 64 * p;
+      const int r = L >> 2, pc = L & 3;
+      if (r < RW) interleave(p, &sbt[wave][r * 32 + pc * 8]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
   }
-  __syncthreads();
-  const int gl = ks * 32 + (lane >> 1);
   float res[RW];
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
-    const uint32_t sb = sbt[rg * RW + r][gl];
+    const uint32_t sb = BS ? sbt[rg * RW + r][ks * 32 + (lane >> 1)] : sbt[wave][r * 32 + (lane >> 1)];
     const float s = bf16_lo(sb);
     const float bo = __builtin_fmaf(-magic_offset<4>(), s, bf16_hi(sb));
     res[r] = __builtin_fmaf(s, chunk_dot<4>(wv[r], xc), bo * xc.sum);
