@@ -138,8 +138,10 @@ hipError_t launch_qmm_prefill(const QmmArgs& a, hipStream_t stream);
 // per-stream bf16 workspace with the prefill kernel's single rounding
 // (launch_dequant_fused), then a library bf16 GEMM.  Taken for bias-free int4 /
 // int8 products with M >= kDeqGemmMinM and N K <= kDeqGemmMaxElems (the
-// workspace is 2 N K bytes).
-constexpr int64_t kDeqGemmMinM = 1024;
+// workspace is 2 N K bytes).  At M = 768 the two passes already win on every
+// Llama shape (14336 x 4096 131 -> 111 us, 4096 x 14336 156 -> 123 us); at
+// M = 512 the fused kernel still does (82 against 90, 94 against 110 us).
+constexpr int64_t kDeqGemmMinM = 768;
 constexpr int64_t kDeqGemmMaxElems = int64_t(1) << 26;
 hipError_t launch_dequant_fused(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                                 uint16_t* out, int64_t N, int64_t K, int group_size, int bits,

@@ -228,14 +228,15 @@ def test_qmvw_parts_and_walks(gpu, oracle, M, N, K, bias):
 
 
 @pytest.mark.parametrize("M,N,K,bits,group", [
-    (1024, 1024, 1024, 4, 64),   # the threshold M
+    (768, 1024, 1024, 4, 64),    # the threshold M
+    (1024, 1024, 1024, 4, 64),
     (1500, 4104, 2048, 4, 32),   # ragged M, N not a multiple of the GEMM tiles
     (1024, 2048, 4096, 4, 128),
     (1100, 1032, 3072, 8, 64),
     (2048, 4096, 1024, 8, 32),
 ])
 def test_deq_gemm_shapes(gpu, oracle, M, N, K, bits, group):
-    """Bias-free products at M >= 1024: W dequantized once with the prefill
+    """Bias-free products at M >= 768: W dequantized once with the prefill
     kernel's single rounding, then the library bf16 GEMM (fp32 accumulation); the
     per-element bound against the fp64 oracle holds as for the fused kernels."""
     rows = np.unique(np.array([0, 1, M // 3, M // 2, M - 2, M - 1]))
