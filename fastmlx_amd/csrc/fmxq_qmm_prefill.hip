@@ -510,44 +510,32 @@ TileShape prefill_tile(const QmmArgs& a) {
 // dequant_words8), for the dequantize-then-GEMM path at large M.  The work is cut
 // into units of 8 consecutive values (one int4 word, two int8 words), 16 output
 // bytes each; the rows are contiguous, so unit u's group is 8 u >> log2(group)
-// over the whole matrix.  Thread (wave w, lane l) of block b takes units
-// b 1024 + w 256 + 64 j + l, j = 0..3: every load and every 16-byte store
-// instruction of a wave covers one contiguous span (1 KiB of output), where one
-// 64-byte run per thread had each store touch 64 segments.
+// over the whole matrix.  One unit per thread: each load and each 16-byte store
+// instruction of a wave covers one contiguous span.  Measured on 14336 x 4096
+// (4-bit): 27.2 us with one unit per thread against 29.3 / 31.4 / 29.0 / 37.1 us
+// with 2 / 4 / 8 / 16 (64 apart per thread), 27.4-28.2 us for a grid-stride loop
+// that loads the next unit first, and 44 us for 16-byte loads of four units with
+// 64-byte runs of stores per thread.  The same pass without the weight loads
+// takes 19.2 us: the 117 MB of writes alone set most of the time.  (In the
+// full dequantize-then-GEMM call the change measured within noise.)
 template <int BITS>
 __global__ __launch_bounds__(256) void dequant_fused_kernel(const uint32_t* __restrict__ w,
                                                             const uint16_t* __restrict__ scales,
                                                             const uint16_t* __restrict__ biases,
                                                             uint16_t* __restrict__ out,
                                                             uint32_t units, int gshift) {
-  const uint32_t base = blockIdx.x * 1024u + (threadIdx.x >> 6) * 256u + (threadIdx.x & 63);
-  uint32_t wv[4][BITS / 4];
-  float sv[4], bv[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t u = base + 64u * j;
-    if (u < units) {
-      if constexpr (BITS == 4) {
-        wv[j][0] = __builtin_nontemporal_load(w + u);
-      } else {
-        const u32x2 p = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(w) + u);
-        wv[j][0] = p[0];
-        wv[j][1] = p[1];
-      }
-      const uint32_t g = (u * 8u) >> gshift;
-      sv[j] = bf16_bits_to_f32(scales[g]);
-      bv[j] = bf16_bits_to_f32(biases[g]);
-    }
+  const uint32_t u = blockIdx.x * 256u + threadIdx.x;
+  if (u >= units) return;
+  uint32_t o[4];
+  const uint32_t g = (u * 8u) >> gshift;
+  const float s = bf16_bits_to_f32(scales[g]), b = bf16_bits_to_f32(biases[g]);
+  if constexpr (BITS == 4) {
+    dequant_word4(w[u], s, b, o);
+  } else {
+    const u32x2 p = reinterpret_cast<const u32x2*>(w)[u];
+    dequant_words8(p[0], p[1], s, b, o);
   }
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t u = base + 64u * j;
-    if (u >= units) continue;
-    uint32_t o[4];
-    if constexpr (BITS == 4) dequant_word4(wv[j][0], sv[j], bv[j], o);
-    else dequant_words8(wv[j][0], wv[j][1], sv[j], bv[j], o);
-    reinterpret_cast<u32x4*>(out)[u] = u32x4{o[0], o[1], o[2], o[3]};
-  }
+  reinterpret_cast<u32x4*>(out)[u] = u32x4{o[0], o[1], o[2], o[3]};
 }
 
 }  // namespace
@@ -624,7 +612,7 @@ hipError_t launch_dequant_fused(const uint32_t* w, const uint16_t* scales, const
       K % group_size || K % 8 || units * 8 >= (int64_t(1) << 32))
     return hipErrorInvalidValue;
   const int gshift = __builtin_ctz((unsigned)group_size);
-  const unsigned blocks = (unsigned)((units + 1023) / 1024);
+  const unsigned blocks = (unsigned)((units + 255) / 256);
   if (bits == 4)
     dequant_fused_kernel<4><<<blocks, 256, 0, stream>>>(w, scales, biases, out, (uint32_t)units,
                                                         gshift);
