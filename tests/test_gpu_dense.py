@@ -323,9 +323,9 @@ def test_graph_replay_matches_eager(gpu):
 
     rng = np.random.default_rng(77)
     # M=1 / 4 GEMVs, qmvs (M=16, narrow), qmvw with K parts and its fixup (M=32),
-    # the prefill GEMM (M=96) and the dequantize-then-GEMM path (M=1024).
+    # the prefill GEMM (M=96) and the dequantize-then-GEMM path (M=1024, 2048).
     shapes = [(1, 4096, 4096), (4, 1024, 4096), (16, 2048, 2048), (32, 4096, 4096),
-              (96, 512, 1024), (1024, 1024, 1024)]
+              (96, 512, 1024), (1024, 1024, 1024), (2048, 4096, 1024)]
     tensors = []
     for M, N, K in shapes:
         w, s, b = make_quant(rng, (N,), K, 4, 64)
