@@ -734,9 +734,9 @@ extern "C" int fmxq_switch_glu_combine(
     return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: x and weights must be 16-byte aligned", op);
   if (S > 0x7fffffffLL) return fail(FMXQ_ERR_SHAPE, "%s: too many slots", op);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // Decode-sized batches: gate and up into h (no sort), then one kernel for the
-  // down projection and the combine.
-  if (S <= fmxq::kMoeUnsortedMaxSlots &&
+  // Decode-sized batches, and batches whose slots rarely share an expert: gate and
+  // up into h (no sort), then one kernel for the down projection and the combine.
+  if (fmxq::moe_combine_unsorted(S, E) &&
       fmxq::moe_down_combine_supported(T, topk, D, I, bits, group_size) &&
       fmxq::moe_qmvs_supported(I, D, bits, group_size) && aligned16(s_gate) &&
       aligned16(b_gate) && aligned16(s_up) && aligned16(b_up)) {

@@ -229,6 +229,17 @@ struct MoeArgs {
 // Slot counts up to which the MoE products skip the sort: every slot is its own
 // segment (a sort saves weight reads only when slots share an expert).
 constexpr int64_t kMoeUnsortedMaxSlots = 16;
+// SwitchGLU with the top-k combine (fmxq_switch_glu_combine) stays unsorted, with
+// the combine fused into the down projection, up to 256 slots routed over at least
+// twice as many experts: few slots then share an expert, and skipping the sort
+// and combine launches outweighs the re-reads (configuration 3 at M = 16, 160
+// slots over 512 experts: 77.5 -> 72.5 us).  Where many slots share experts
+// (configuration 4 at M = 32, 256 slots over 256 experts, Zipf routing) the
+// re-reads double the time, so those batches sort.
+constexpr int64_t kMoeUnsortedCombineMaxSlots = 256;
+inline bool moe_combine_unsorted(int64_t S, int64_t E) {
+  return S <= kMoeUnsortedMaxSlots || (S <= kMoeUnsortedCombineMaxSlots && 2 * S <= E);
+}
 bool moe_qmvs_supported(int64_t N, int64_t K, int bits, int group_size);
 int moe_window(int64_t S, int64_t E);
 int64_t moe_max_segments(int64_t S, int64_t E, int window);

@@ -520,8 +520,10 @@ def test_gather_qmm_long_runs_bad_row_and_id(gpu, oracle):
 @pytest.mark.parametrize("cfg,M", [("c3", 1), ("c3", 16), ("c4", 1), ("c4", 2), ("c4", 32)])
 def test_switch_glu_combine_configs(gpu, oracle, cfg, M):
     """The fused layer at configurations 3 and 4.
-    - Up to 16 slots run the down projection and the weighted sum as one kernel.
-    - More slots run SwitchGLU, then the combine.
+    - Up to 16 slots, and up to 256 slots over at least twice as many experts
+      (configuration 3 at M=16), run unsorted, the down projection and the
+      weighted sum as one kernel.
+    - Other batches run the sorted SwitchGLU, then the combine.
     - Configuration 4 adds its shared expert (computed by a one-expert SwitchGLU).
     Checked element by element against the oracle's op chain."""
     from fastmlx_amd import ops
@@ -563,15 +565,17 @@ def test_switch_glu_combine_configs(gpu, oracle, cfg, M):
                          shared=sh, what=f"switch_glu_combine {cfg} M={M}")
 
 
-@pytest.mark.parametrize("I,gated", [(512, True), (1024, False), (4096, True)])
-def test_switch_glu_combine_few_slots_shapes(gpu, oracle, I, gated):
+@pytest.mark.parametrize("I,gated,E,T,k", [(512, True, 9, 2, 6), (1024, False, 9, 2, 6),
+                                           (4096, True, 9, 2, 6), (512, True, 300, 12, 10)])
+def test_switch_glu_combine_few_slots_shapes(gpu, oracle, I, gated, E, T, k):
     """The fused down/combine kernel's other row forms (32 lanes per 1024-value row,
-    two chunks per lane at 4096), a sigmoid-gated shared term, and a bad expert id
-    (its slot contributes zero and the flag is raised)."""
+    two chunks per lane at 4096), a sigmoid-gated shared term, a bad expert id
+    (its slot contributes zero and the flag is raised), and 120 slots over 300
+    experts (unsorted beyond 16 slots)."""
     from fastmlx_amd import FmxqError, ops
 
-    rng = np.random.default_rng(I + gated)
-    E, D, T, k = 9, 512, 2, 6
+    rng = np.random.default_rng(I + gated + E)
+    D = 512
     gate, up, down = _stack(rng, E, D, I)
     x = make_x(rng, T, D)
     inds = topk_uniform(rng, T, E, k)
@@ -580,7 +584,7 @@ def test_switch_glu_combine_few_slots_shapes(gpu, oracle, I, gated):
     sh = make_x(rng, T, D)
     sg = make_x(rng, T) if gated else None
     dev = lambda t: to_dev(t, gpu)
-    announce(f"switch_glu_combine I={I} gated={gated}")
+    announce(f"switch_glu_combine I={I} gated={gated} E={E} slots={T * k}")
     out = ops.switch_glu_combine(dev(x), dev(inds.astype(np.uint32)), tuple(map(dev, gate)),
                                  tuple(map(dev, up)), tuple(map(dev, down)), dev(wts), dev(sh),
                                  None if sg is None else dev(sg))
