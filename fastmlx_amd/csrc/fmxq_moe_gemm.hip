@@ -437,9 +437,14 @@ static hipError_t launch_qmv1_nmat(const MoeArgs& a, int64_t segs, hipStream_t s
   const int64_t nch = a.K / 32;
   // Rows up to 4096 values: 2 rows per block of 1-2 waves, so the few-slot grid
   // has enough waves (configuration 3 at M = 1, K = 2048: 8 rows 13.4 us, 4 rows
-  // 12.1, 2 rows 11.5, 1 row 12.3 us per layer).  Longer rows keep 4 rows over
+  // 12.1, 2 rows 11.5, 1 row 12.3 us per layer).  With 64 or more segments the
+  // grid is large anyway, and 8 rows per wave load each x chunk for 4x the
+  // weights (configuration 3 at M = 16, 160 slots: 72.0 -> 67.7 us per layer; 4
+  // rows 68.8, 16 rows 71-73 us at 244 VGPRs).  Longer rows keep 4 rows over
   // 4-8 waves (configuration 4 at M = 1, K = 7168: 2 or 8 rows were slower).
-  if (nch <= 64) return launch_qmv1_ks<NMAT, 1, MM, 2>(a, segs, stream);
+  if (nch <= 64)
+    return segs >= 64 ? launch_qmv1_ks<NMAT, 1, MM, 8>(a, segs, stream)
+                      : launch_qmv1_ks<NMAT, 1, MM, 2>(a, segs, stream);
   if (nch <= 128) return launch_qmv1_ks<NMAT, 2, MM, 2>(a, segs, stream);
   if (nch <= 256) return launch_qmv1_ks<NMAT, 4, MM>(a, segs, stream);
   return launch_qmv1_ks<NMAT, 8, MM>(a, segs, stream);
@@ -569,8 +574,13 @@ hipError_t launch_moe_down_combine(const uint16_t* h, const uint32_t* inds, cons
   // Row tiles of 8 (I = 512) and 4 (I = 2048) columns: more blocks for the
   // one-token grids (configuration 3 at M = 1 11.5 -> 10.5-10.8 us with 8 rows
   // against 16; configuration 4 at M = 1 61.3 -> 58.3-58.9 us with 4 against 8).
+  // From 8 tokens the grid is large, and 32-row tiles load each h row for 4x the
+  // weights (configuration 3 at M = 16: 67.7 -> 64.5-66.3 us per layer; 64 rows
+  // were no better).
   switch (I) {
-    case 512: return launch_down_combine_cfg<8, 16, 1>(a, stream);
+    case 512:
+      return T >= 8 ? launch_down_combine_cfg<32, 16, 1>(a, stream)
+                    : launch_down_combine_cfg<8, 16, 1>(a, stream);
     case 1024: return launch_down_combine_cfg<16, 32, 1>(a, stream);
     case 2048: return launch_down_combine_cfg<4, 64, 1>(a, stream);
     case 4096: return launch_down_combine_cfg<8, 64, 2>(a, stream);
