@@ -116,6 +116,14 @@ def test_qmm_mfma_shapes(gpu, oracle, M, bits):
     _qmm_case(gpu, oracle, M, 1024 + 64, 2048, bits, 64, seed=2000 + M + bits)
 
 
+@pytest.mark.parametrize("M", [5, 8])
+@pytest.mark.parametrize("N,K", [(4096, 4096), (1024, 4096), (14336, 4096)])
+def test_int8_small_m_shapes(gpu, oracle, M, N, K):
+    """int8 at 5 <= M <= 8: the register GEMV up to 4096 output rows, the prefill
+    GEMM's 64-row tile beyond."""
+    _qmm_case(gpu, oracle, M, N, K, 8, 64, seed=14000 + M + N // 1024)
+
+
 def test_qmm_ragged_n(gpu, oracle):
     # N not a multiple of any tile, K a multiple of 32 only
     _qmm_case(gpu, oracle, 1, 333, 96, 4, 32, seed=5)
