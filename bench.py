@@ -333,9 +333,9 @@ def ingest_points(torch, ops, gen, dev, cpu):
 
 def moe_points(torch, ops, gen, dev, cpu):
     """Configs 3 and 4: one MoE layer per step.
-    - The step is switch_glu_combine: SwitchGLU over the routed experts and the
-      weighted top-k combine in one call (up to 16 slots, the down projection and
-      the combine are one kernel).  Configuration 4 adds its shared expert.
+    - Configuration 3's step is switch_glu_combine: SwitchGLU over the routed
+      experts and the weighted top-k combine in one call.  Configuration 4's is
+      moe_layer: the same plus its shared expert MLP, computed inside the call.
     - Each step of a replayed graph has its own routing, and for configuration 4
       its own shared expert, so consecutive steps do not find their experts in
       the 256 MB last-level cache."""
@@ -400,14 +400,11 @@ def moe_points(torch, ops, gen, dev, cpu):
             w = torch.sigmoid(torch.randn(M, k, device=dev, generator=gen))
             w = w / w.sum(dim=1, keepdim=True)
             routes.append((inds.to(torch.int32).contiguous(), w.to(torch.bfloat16)))
-        zero = torch.zeros(M, 1, device=dev, dtype=torch.int32)
-        ysh = torch.empty(M, 1, D, device=dev, dtype=torch.bfloat16)
         yo = torch.empty(M, D, device=dev, dtype=torch.bfloat16)
 
         def fn():
-            for (inds, w), (sg, su, sd) in zip(routes, shared):
-                ops.switch_glu(x, zero, sg, su, sd, GROUP, 4, out=ysh)
-                ops.switch_glu_combine(x, inds, gate, up, down, w, shared=ysh.view(M, D), out=yo)
+            for (inds, w), sh in zip(routes, shared):
+                ops.moe_layer(x, inds, gate, up, down, w, sh, out=yo)
         g = capture(torch, fn)
         per = time_graph(torch, g, 6, 1) / R
         hit = sum(int(torch.unique(r[0]).numel()) for r in routes) / R
@@ -496,15 +493,21 @@ def probe(args):
               for _ in range(R)]
         ys = torch.empty(M, k, D, device=dev, dtype=torch.bfloat16)
         yo = torch.empty(M, D, device=dev, dtype=torch.bfloat16)
+        # configuration 4's layer call carries its shared expert (moe_layer)
+        sh = None if c3 or not args.combine else tuple(
+            gen_quant_stack(torch, 1, n, kk, gen, dev) for n, kk in ((I, D), (I, D), (D, I)))
         torch.cuda.synchronize()
         for i in range(args.launches):
-            if args.combine:
+            if sh is not None:
+                ops.moe_layer(x, routes[i % R], gate, up, down, ws[i % R], sh, out=yo)
+            elif args.combine:
                 ops.switch_glu_combine(x, routes[i % R], gate, up, down, ws[i % R], out=yo)
             else:
                 ops.switch_glu(x, routes[i % R], gate, up, down, GROUP, 4, out=ys)
         hit = sum(int(torch.unique(r).numel()) for r in routes) / R
-        info.update(algorithmic_bytes=moe_bytes(M, D, I, k, int(round(hit)), 4, GROUP),
-                    experts_hit=hit, combine=bool(args.combine))
+        info.update(algorithmic_bytes=moe_bytes(M, D, I, k, int(round(hit)), 4, GROUP,
+                                                **({} if sh is None else {"shared_I": I})),
+                    experts_hit=hit, combine=bool(args.combine), shared_expert=sh is not None)
     else:
         M, N, K, bits = PROBES[args.probe]
         copies = args.copies if M <= 32 else 1
@@ -603,6 +606,26 @@ def main():
         del c0
         nd = extra["qmv_4096x14336_M1"]
         by_dn = qmm_bytes(1, 4096, 14336, 4, GROUP)
+        # The same kernel on taller matrices of the same 14336-deep shape: the
+        # increment between 16384 and 32768 rows is its steady-state streaming
+        # rate, and what the 4096-row launch takes beyond its bytes at that rate is
+        # the per-launch cost that does not scale with the bytes.
+        sweep = {}
+        for rows, copies in ((16384, 4), (32768, 2)):
+            big = [gen_quant(torch, rows, 14336, 4, gen, dev) for _ in range(copies)]
+            sweep[rows] = dense_point(torch, ops, big, 1, rows, 14336, 4, gen, dev)
+            del big
+        by16, by32 = qmm_bytes(1, 16384, 14336, 4, GROUP), qmm_bytes(1, 32768, 14336, 4, GROUP)
+        dt = (sweep[32768]["us"] - sweep[16384]["us"]) * 1e-6
+        marginal = (by32 - by16) / dt / 1e9 if dt > 0 else None
+        extra["qmv_K14336_size_sweep"] = {
+            "rows": [4096, 16384, 32768],
+            "us": [nd["us"], sweep[16384]["us"], sweep[32768]["us"]],
+            "frac_hbm": [nd["frac_hbm"], sweep[16384]["frac_hbm"], sweep[32768]["frac_hbm"]],
+            "marginal_GBps": None if marginal is None else round(marginal, 1),
+            "marginal_frac_hbm": None if marginal is None else round(marginal / HBM_PEAK_GBS, 4),
+            "fixed_us_per_launch": None if marginal is None else
+            round(nd["us"] - by_dn / (marginal * 1e9) * 1e6, 3)}
         traffic = profile_value(ROOF_PMC, "traffic_bytes_per_launch")
         roof = {"bound": "hbm", "achieved": nd["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": nd["frac_hbm"], "traffic": None if traffic is None else int(traffic),

@@ -33,6 +33,7 @@ FMXQ_SYMBOLS = {
     "fmxq_switch_glu": (_int, [_p] * 12 + [_i64] * 5 + [_int, _int, _p]),
     "fmxq_switch_glu_noalloc": (_int, [_p] * 12 + [_i64] * 5 + [_int, _int, _p]),
     "fmxq_switch_glu_combine": (_int, [_p] * 15 + [_i64] * 5 + [_int, _int, _p]),
+    "fmxq_moe_layer": (_int, [_p] * 23 + [_i64] * 5 + [_int, _int, _p]),
     "fmxq_moe_combine": (_int, [_p] * 5 + [_i64] * 3 + [_p]),
     "fmxq_route_softmax_topk": (_int, [_p, _int, _i64, _i64, _int, _bool, _p, _p, _int, _p]),
     "fmxq_route_group_topk": (_int, [_p, _int, _p, _i64, _i64, _int, _int, _int, ctypes.c_float,

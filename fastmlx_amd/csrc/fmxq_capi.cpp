@@ -770,6 +770,78 @@ extern "C" int fmxq_switch_glu_combine(
                     "switch_glu_combine: combine");
 }
 
+extern "C" int fmxq_moe_layer(
+    const uint16_t* x, const uint32_t* inds, const uint32_t* w_gate, const uint16_t* s_gate,
+    const uint16_t* b_gate, const uint32_t* w_up, const uint16_t* s_up, const uint16_t* b_up,
+    const uint32_t* w_down, const uint16_t* s_down, const uint16_t* b_down,
+    const uint16_t* weights, const uint32_t* sw_gate, const uint16_t* ss_gate,
+    const uint16_t* sb_gate, const uint32_t* sw_up, const uint16_t* ss_up, const uint16_t* sb_up,
+    const uint32_t* sw_down, const uint16_t* ss_down, const uint16_t* sb_down,
+    const uint16_t* shared_gate, uint16_t* out, int64_t T, int64_t topk, int64_t E, int64_t D,
+    int64_t I, int group_size, int bits, void* stream) {
+  const char* op = "moe_layer";
+  if (int rc = check_quant(group_size, bits, D, true, op)) return rc;
+  if (int rc = check_quant(group_size, bits, I, true, op)) return rc;
+  if (T < 0 || topk < 1 || E < 1 || D % 2 != 0)
+    return fail(FMXQ_ERR_SHAPE, "%s: need T >= 0, top_k >= 1, E >= 1 and an even D", op);
+  const int64_t S = T * topk;
+  if (S == 0) return FMXQ_OK;
+  if (!x || !inds || !w_gate || !s_gate || !b_gate || !w_up || !s_up || !b_up || !w_down ||
+      !s_down || !b_down || !weights || !sw_gate || !ss_gate || !sb_gate || !sw_up || !ss_up ||
+      !sb_up || !sw_down || !ss_down || !sb_down || !out)
+    return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: null operand", op);
+  if (!aligned16(x) || !aligned16(w_gate) || !aligned16(w_up) || !aligned16(w_down) ||
+      !aligned16(sw_gate) || !aligned16(sw_up) || !aligned16(sw_down))
+    return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: x and weights must be 16-byte aligned", op);
+  if (S + T > 0x7fffffffLL) return fail(FMXQ_ERR_SHAPE, "%s: too many slots", op);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // One token (decode): the shared expert rides along as one more gate/up segment
+  // and one more wave of each down/combine block, two launches for the layer.
+  if (T == 1 && topk <= 15 && fmxq::moe_combine_unsorted(S, E) && D >= 2048 && D <= 16384 &&
+      fmxq::moe_down_combine_supported(T, topk, D, I, bits, group_size) &&
+      fmxq::moe_qmvs_supported(I, D, bits, group_size) && aligned16(s_gate) &&
+      aligned16(b_gate) && aligned16(s_up) && aligned16(b_up) && aligned16(ss_gate) &&
+      aligned16(sb_gate) && aligned16(ss_up) && aligned16(sb_up)) {
+    uint32_t* flag = nullptr;
+    if (int rc = device_flag(s, &flag)) return rc;
+    MoeScratch m;
+    if (int rc = moe_scratch(s, S + T, I, 1, &m, op)) return rc;
+    fmxq::MoeArgs gu{x, nullptr, {w_gate, w_up}, {s_gate, s_up}, {b_gate, b_up}, inds, nullptr,
+                     nullptr, m.h, nullptr, S, I, D, E, T, flag, topk};
+    gu.sh_w[0] = sw_gate;
+    gu.sh_w[1] = sw_up;
+    gu.sh_s[0] = ss_gate;
+    gu.sh_s[1] = ss_up;
+    gu.sh_b[0] = sb_gate;
+    gu.sh_b[1] = sb_up;
+    gu.sh_T = T;
+    if (int rc = hip_status(fmxq::launch_moe_qmvs(gu, 2, 16, S, s), "moe_layer: gate/up"))
+      return rc;
+    return hip_status(fmxq::launch_moe_down_combine(m.h, inds, w_down, s_down, b_down, weights,
+                                                    nullptr, shared_gate, out, T, topk, E, D, I,
+                                                    flag, s, sw_down, ss_down, sb_down),
+                      "moe_layer: down/combine");
+  }
+  // Otherwise the shared expert as a one-expert SwitchGLU over every token (its
+  // rows and the all-zero expert ids in the arena's slot 2), then the routed part
+  // with those rows as the shared term.
+  const size_t zb = align_up((size_t)T * sizeof(uint32_t));
+  void* arena = nullptr;
+  if (int rc = stream_arena(s, zb + align_up((size_t)T * D * sizeof(uint16_t)), &arena, op, 2))
+    return rc;
+  uint32_t* zinds = static_cast<uint32_t*>(arena);
+  uint16_t* rows = reinterpret_cast<uint16_t*>(static_cast<char*>(arena) + zb);
+  if (int rc = hip_status(fmxq::launch_fill_u32(zinds, 0u, T, s), "moe_layer: shared ids"))
+    return rc;
+  if (int rc = switch_glu_impl(x, zinds, sw_gate, ss_gate, sb_gate, sw_up, ss_up, sb_up, sw_down,
+                               ss_down, sb_down, rows, T, 1, 1, D, I, group_size, bits, stream,
+                               ScratchSource(), op))
+    return rc;
+  return fmxq_switch_glu_combine(x, inds, w_gate, s_gate, b_gate, w_up, s_up, b_up, w_down,
+                                 s_down, b_down, weights, rows, shared_gate, out, T, topk, E, D,
+                                 I, group_size, bits, stream);
+}
+
 namespace {
 int route_common(const void* logits, int logits_bf16, const float* bias, int64_t T, int64_t E,
                  int top_k, int n_group, int topk_group, float scale, bool norm, uint32_t* inds,

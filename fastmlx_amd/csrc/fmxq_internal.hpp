@@ -225,6 +225,13 @@ struct MoeArgs {
   int64_t S, N, K, E, x_rows;
   uint32_t* err_flag;
   int64_t lhs_div = 1;      // x row of slot s is lhs[s], or s / lhs_div without lhs
+  // Few-slot GEMV form only (no segment table, no yrow): sh_T more segments after
+  // the S slots, segment S + t the shared expert (sh_w / sh_s / sh_b, one [N, .]
+  // matrix each) on x row t, written to output row S + t.
+  const uint32_t* sh_w[2] = {nullptr, nullptr};
+  const uint16_t* sh_s[2] = {nullptr, nullptr};
+  const uint16_t* sh_b[2] = {nullptr, nullptr};
+  int64_t sh_T = 0;
 };
 // Slot counts up to which the MoE products skip the sort: every slot is its own
 // segment (a sort saves weight reads only when slots share an expert).
@@ -250,11 +257,19 @@ hipError_t launch_moe_qmvs(const MoeArgs& a, int nmat, int window, int64_t max_s
 // tile and token, one wave per slot): out [T, D] from the h rows [T k, I].
 bool moe_down_combine_supported(int64_t T, int64_t k, int64_t D, int64_t I, int bits,
                                 int group_size);
+// With sh_w (the shared expert's down matrix [D, I*bits/32] and its scales and
+// biases), one more wave per block computes that expert's down product for the
+// token from h row T k + t and adds it (sigmoid-gated by sgate) in place of the
+// precomputed `shared` rows; then k <= 15.
 hipError_t launch_moe_down_combine(const uint16_t* h, const uint32_t* inds, const uint32_t* w,
                                    const uint16_t* s, const uint16_t* b, const uint16_t* weights,
                                    const uint16_t* shared, const uint16_t* sgate, uint16_t* out,
                                    int64_t T, int64_t k, int64_t E, int64_t D, int64_t I,
-                                   uint32_t* err_flag, hipStream_t stream);
+                                   uint32_t* err_flag, hipStream_t stream,
+                                   const uint32_t* sh_w = nullptr, const uint16_t* sh_s = nullptr,
+                                   const uint16_t* sh_b = nullptr);
+// Fill n uint32 words with v (a kernel, so it can sit in a captured graph).
+hipError_t launch_fill_u32(uint32_t* p, uint32_t v, int64_t n, hipStream_t stream);
 
 // Grouped MFMA gather for expert-sorted batches (int4 group_size >= 64, int8 >= 32).
 constexpr int64_t kGroupedMinSlots = 32;

@@ -138,6 +138,12 @@ __global__ __launch_bounds__(1024) void sort_slots_kernel(const uint32_t* __rest
 
 __device__ __forceinline__ float r16(float v) { return bf16_bits_to_f32(f32_to_bf16_rne(v)); }
 
+__global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* __restrict__ p, uint32_t v,
+                                                       int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
 // 8 elements per thread; n is a multiple of 8.
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ g,
                                                        const uint16_t* __restrict__ u,
@@ -284,6 +290,12 @@ hipError_t launch_moe_combine(const uint16_t* y, const uint16_t* w, const uint16
                               int64_t D, hipStream_t stream) {
   moe_combine_kernel<<<grid_for(T * (D / 2), 256), 256, 0, stream>>>(y, w, shared, sgate, out, T,
                                                                      topk, D);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_u32(uint32_t* p, uint32_t v, int64_t n, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  fill_u32_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(p, v, n);
   return hipGetLastError();
 }
 

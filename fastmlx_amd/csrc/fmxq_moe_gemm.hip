@@ -302,7 +302,7 @@ static hipError_t launch_wc(const MoeArgs& a, int wc, int64_t max_seg, hipStream
 // dense GEMV, fmxq_qmv.hip).  The slices meet in LDS and wave 0 stores RW output
 // columns per slot (silu(g) * u with the op chain's roundings for NMAT = 2).
 // Segments longer than MM are left to the MFMA walk above.
-template <int NMAT, int RW, int KS, int MM>
+template <int NMAT, int RW, int KS, int MM, bool SH>
 __global__ __launch_bounds__(KS * 64) void moe_qmv1_kernel(MoeArgs a) {
   constexpr int V = NMAT * RW * MM;  // partials per lane: index (p RW + r) MM + m
   constexpr int LV = __builtin_ctz(V);
@@ -319,18 +319,30 @@ __global__ __launch_bounds__(KS * 64) void moe_qmv1_kernel(MoeArgs a) {
     if (len > MM) return;
   }
   const int64_t nbase = (int64_t)blockIdx.x * RW;
-  const uint32_t e = a.rhs[start];
+  // SH: segments past the S slots (sh_T of them, no segment table) are the shared
+  // expert on x row sg - S, written to row sg.
+  const bool shs = SH && sg >= a.S;
+  const uint32_t e = shs ? 0u : a.rhs[start];
+  const uint32_t* wp[NMAT];
+  const uint16_t* sp[NMAT];
+  const uint16_t* bp[NMAT];
+#pragma unroll
+  for (int p = 0; p < NMAT; ++p) {
+    wp[p] = shs ? a.sh_w[p] : a.w[p];
+    sp[p] = shs ? a.sh_s[p] : a.s[p];
+    bp[p] = shs ? a.sh_b[p] : a.b[p];
+  }
   int64_t xr[MM], orow[MM];
   bool rbad[MM];
 #pragma unroll
   for (int m = 0; m < MM; ++m) {
     const int64_t slot = start + (m < len ? m : 0);
-    const int64_t r = a.lhs ? (int64_t)a.lhs[slot] : slot / a.lhs_div;
+    const int64_t r = shs ? sg - a.S : a.lhs ? (int64_t)a.lhs[slot] : slot / a.lhs_div;
     rbad[m] = r >= a.x_rows;
     xr[m] = rbad[m] ? 0 : r;
     orow[m] = a.yrow ? (int64_t)a.yrow[slot] : slot;
   }
-  if ((int64_t)e >= a.E) {
+  if (!shs && (int64_t)e >= a.E) {
     if (ks == 0) {
 #pragma unroll
       for (int m = 0; m < MM; ++m)
@@ -355,9 +367,9 @@ __global__ __launch_bounds__(KS * 64) void moe_qmv1_kernel(MoeArgs a) {
       int64_t n = nbase + r;
       n = n < a.N ? n : a.N - 1;  // rows past N re-read row N-1; not stored
       const int64_t row = (int64_t)e * a.N + n;
-      wv[p][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.w[p] + row * wpr) + cc);
-      sv[p][r] = a.s[p][row * gpr + g];
-      bv[p][r] = a.b[p][row * gpr + g];
+      wv[p][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp[p] + row * wpr) + cc);
+      sv[p][r] = sp[p][row * gpr + g];
+      bv[p][r] = bp[p][row * gpr + g];
     }
   // The weight requests go out before x is read and paired.
   __builtin_amdgcn_sched_barrier(0);
@@ -428,7 +440,10 @@ __global__ __launch_bounds__(KS * 64) void moe_qmv1_kernel(MoeArgs a) {
 template <int NMAT, int KS, int MM, int RW = 4>
 static hipError_t launch_qmv1_ks(const MoeArgs& a, int64_t segs, hipStream_t stream) {
   dim3 grid((unsigned)((a.N + RW - 1) / RW), (unsigned)segs);
-  moe_qmv1_kernel<NMAT, RW, KS, MM><<<grid, KS * 64, 0, stream>>>(a);
+  if (a.sh_T > 0)
+    moe_qmv1_kernel<NMAT, RW, KS, MM, true><<<grid, KS * 64, 0, stream>>>(a);
+  else
+    moe_qmv1_kernel<NMAT, RW, KS, MM, false><<<grid, KS * 64, 0, stream>>>(a);
   return hipGetLastError();
 }
 
@@ -473,19 +488,29 @@ struct DownCombineArgs {
   uint16_t* out;             // [T, D]
   int64_t T, k, E, D, I;
   uint32_t* err_flag;
+  // The shared expert's down matrix [D, I/8] (and scales, biases), or null: wave k
+  // of each block computes that expert's output for the token from h row T k + t.
+  const uint32_t* sh_w = nullptr;
+  const uint16_t* sh_s = nullptr;
+  const uint16_t* sh_b = nullptr;
 };
 
-template <int RW, int LPR, int CPL>
+template <int RW, int LPR, int CPL, bool SH>
 __global__ __launch_bounds__(1024) void moe_down_combine_kernel(DownCombineArgs a) {
   constexpr int RPP = 64 / LPR, PASSES = RW / RPP;
   static_assert(RW % RPP == 0, "rows per pass");
-  __shared__ float part[16][RW];
+  __shared__ float part[SH ? 17 : 16][RW];
   const int lane = threadIdx.x & 63;
   const int j = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t t = blockIdx.y, n0 = (int64_t)blockIdx.x * RW;
-  const int64_t slot = t * a.k + j;
-  const uint32_t e = a.inds[slot];
-  const bool bad = (int64_t)e >= a.E;
+  // SH: wave k is the shared expert, h row T k + t, its own matrices.
+  const bool shw = SH && j == a.k;
+  const int64_t slot = shw ? a.T * a.k + t : t * a.k + j;
+  const uint32_t e = shw ? 0u : a.inds[slot];
+  const bool bad = !shw && (int64_t)e >= a.E;
+  const uint32_t* wm = shw ? a.sh_w : a.w;
+  const uint16_t* sm = shw ? a.sh_s : a.s;
+  const uint16_t* bm = shw ? a.sh_b : a.b;
   const int rsub = lane / LPR, cl = lane % LPR;
   const int64_t wpr = a.I / 8, gpr = a.I / 64;
   float res[PASSES];
@@ -502,9 +527,9 @@ __global__ __launch_bounds__(1024) void moe_down_combine_kernel(DownCombineArgs 
 #pragma unroll
       for (int i = 0; i < CPL; ++i) {
         const int c = cl + LPR * i;
-        wv[p][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.w + row * wpr) + c);
-        sv[p][i] = a.s[row * gpr + (c >> 1)];
-        bv[p][i] = a.b[row * gpr + (c >> 1)];
+        wv[p][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wm + row * wpr) + c);
+        sv[p][i] = sm[row * gpr + (c >> 1)];
+        bv[p][i] = bm[row * gpr + (c >> 1)];
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -526,7 +551,8 @@ __global__ __launch_bounds__(1024) void moe_down_combine_kernel(DownCombineArgs 
 #pragma unroll
     for (int off = LPR / 2; off >= 1; off >>= 1) res[p] += __shfl_xor(res[p], off, 64);
   if (cl == 0) {
-    const float wj = bf16_bits_to_f32(a.weights[slot]);
+    // The shared expert's output is its bf16 product (no routing weight).
+    const float wj = shw ? 1.f : bf16_bits_to_f32(a.weights[slot]);
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) part[j][p * RPP + rsub] = bad ? 0.f : r16(r16(res[p]) * wj);
   }
@@ -539,8 +565,8 @@ __global__ __launch_bounds__(1024) void moe_down_combine_kernel(DownCombineArgs 
       float acc = 0.f;
       for (int jj = 0; jj < a.k; ++jj) acc += part[jj][r];
       acc = r16(acc);
-      if (a.shared) {
-        float sh = bf16_bits_to_f32(a.shared[t * a.D + n]);
+      if (SH || a.shared) {
+        float sh = SH ? part[SH ? a.k : 0][r] : bf16_bits_to_f32(a.shared[t * a.D + n]);
         if (a.sgate) sh = r16(r16(1.f / (1.f + __expf(-bf16_bits_to_f32(a.sgate[t])))) * sh);
         acc = r16(acc + sh);
       }
@@ -552,7 +578,10 @@ __global__ __launch_bounds__(1024) void moe_down_combine_kernel(DownCombineArgs 
 template <int RW, int LPR, int CPL>
 static hipError_t launch_down_combine_cfg(const DownCombineArgs& a, hipStream_t stream) {
   dim3 grid((unsigned)((a.D + RW - 1) / RW), (unsigned)a.T);
-  moe_down_combine_kernel<RW, LPR, CPL><<<grid, (unsigned)(a.k * 64), 0, stream>>>(a);
+  if (a.sh_w)
+    moe_down_combine_kernel<RW, LPR, CPL, true><<<grid, (unsigned)((a.k + 1) * 64), 0, stream>>>(a);
+  else
+    moe_down_combine_kernel<RW, LPR, CPL, false><<<grid, (unsigned)(a.k * 64), 0, stream>>>(a);
   return hipGetLastError();
 }
 
@@ -568,9 +597,14 @@ hipError_t launch_moe_down_combine(const uint16_t* h, const uint32_t* inds, cons
                                    const uint16_t* s, const uint16_t* b, const uint16_t* weights,
                                    const uint16_t* shared, const uint16_t* sgate, uint16_t* out,
                                    int64_t T, int64_t k, int64_t E, int64_t D, int64_t I,
-                                   uint32_t* err_flag, hipStream_t stream) {
-  if (!moe_down_combine_supported(T, k, D, I, 4, 64)) return hipErrorInvalidValue;
-  const DownCombineArgs a{h, inds, w, s, b, weights, shared, sgate, out, T, k, E, D, I, err_flag};
+                                   uint32_t* err_flag, hipStream_t stream, const uint32_t* sh_w,
+                                   const uint16_t* sh_s, const uint16_t* sh_b) {
+  if (!moe_down_combine_supported(T, k, D, I, 4, 64) || (sh_w && (k > 15 || !sh_s || !sh_b)))
+    return hipErrorInvalidValue;
+  DownCombineArgs a{h, inds, w, s, b, weights, shared, sgate, out, T, k, E, D, I, err_flag};
+  a.sh_w = sh_w;
+  a.sh_s = sh_s;
+  a.sh_b = sh_b;
   // Row tiles of 8 (I = 512) and 4 (I = 2048) columns: more blocks for the
   // one-token grids (configuration 3 at M = 1 11.5 -> 10.5-10.8 us with 8 rows
   // against 16; configuration 4 at M = 1 61.3 -> 58.3-58.9 us with 4 against 8).
@@ -622,9 +656,14 @@ hipError_t launch_moe_qmvs(const MoeArgs& a, int nmat, int window, int64_t max_s
   // segments or faster (configuration 3 at M=16 86 -> 81 us, at M=128 248 -> 239
   // us), without the GEMV grid's blocks for every other segment.
   MoeArgs b = a;
-  if (a.K >= 2048 && a.K <= 16384 && !a.seg)
-    return nmat == 2 ? launch_qmv1_nmat<2, 1>(a, a.S, stream)
-                     : launch_qmv1_nmat<1, 1>(a, a.S, stream);
+  const bool gemv = a.K >= 2048 && a.K <= 16384 && !a.seg;
+  // Shared-expert segments exist only in the GEMV form, without an output row map.
+  if (a.sh_T > 0 && (!gemv || a.yrow || !a.sh_w[0] || !a.sh_s[0] || !a.sh_b[0] ||
+                     (nmat == 2 && (!a.sh_w[1] || !a.sh_s[1] || !a.sh_b[1]))))
+    return hipErrorInvalidValue;
+  if (gemv)
+    return nmat == 2 ? launch_qmv1_nmat<2, 1>(a, a.S + a.sh_T, stream)
+                     : launch_qmv1_nmat<1, 1>(a, a.S + a.sh_T, stream);
   // K slices per block; the remaining waves of the block take further column
   // groups.  One slice: the four waves walk the same K range and share the
   // segment's x rows through LDS (moe_qmvw_kernel; measured against about four

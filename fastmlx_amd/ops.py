@@ -156,6 +156,31 @@ def switch_glu_combine(x, inds, gate, up, down, weights, shared=None, shared_gat
     return out
 
 
+def moe_layer(x, inds, gate, up, down, weights, shared_expert, shared_gate=None,
+              group_size: int = 64, bits: int = 4, out=None):
+    """switch_glu_combine with the shared expert computed in the same call.
+
+    shared_expert = (gate, up, down) triples of a one-expert stack; shared_gate [T]
+    (optional) sigmoid-gates its output.  Returns [T, D] bf16."""
+    T, D = x.shape
+    topk = inds.shape[-1]
+    E, I = gate[0].shape[0], gate[0].shape[1]
+    if out is None:
+        out = torch.empty(T, D, dtype=torch.bfloat16, device=x.device)
+    p = [_dev(x, "x", _BF16_LIKE), _dev(inds, "inds", _U32_LIKE)]
+    for name, (w, s, b) in (("gate", gate), ("up", up), ("down", down)):
+        p += [_dev(w, f"{name}.w", _U32_LIKE), _dev(s, f"{name}.scales", _BF16_LIKE),
+              _dev(b, f"{name}.biases", _BF16_LIKE)]
+    p.append(_dev(weights, "weights", _BF16_LIKE))
+    for name, (w, s, b) in zip(("shared.gate", "shared.up", "shared.down"), shared_expert):
+        p += [_dev(w, f"{name}.w", _U32_LIKE), _dev(s, f"{name}.scales", _BF16_LIKE),
+              _dev(b, f"{name}.biases", _BF16_LIKE)]
+    gp = None if shared_gate is None else _dev(shared_gate, "shared_gate", _BF16_LIKE)
+    check(load().fmxq_moe_layer(*p, gp, _dev(out, "out", _BF16_LIKE), T, topk, E, D, I,
+                                group_size, bits, _stream(x)))
+    return out
+
+
 def moe_combine(y, weights, shared=None, shared_gate=None, out=None):
     """sum_j y[:, j] * weights[:, j] (+ shared, optionally sigmoid-gated); y [T, k, D]."""
     T, topk, D = y.shape

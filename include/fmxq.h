@@ -151,6 +151,29 @@ int fmxq_switch_glu_combine(const uint16_t* x, const uint32_t* inds, const uint3
                             int64_t T, int64_t top_k, int64_t E, int64_t D, int64_t I,
                             int group_size, int bits, void* stream);
 
+/* One MoE layer with its shared expert: out [T, D] = sum_j bf16(y[t, j] *
+ * weights[t, j]) plus the shared expert MLP of x (sigmoid-gated by shared_gate
+ * [T] when given), deepseekv3_forward.go:427-442 (shared = mlp(x), added) and
+ * qwen3next_forward.go:510-525 (sigmoid(shared_expert_gate(x)) * shared_expert(x)).
+ * The routed arguments are those of fmxq_switch_glu_combine; sw_ / ss_ / sb_ are
+ * the shared expert's gate, up and down triples laid out as one-expert stacks
+ * ([1, I, D*bits/32], [1, D, I*bits/32], ...), with the routed experts' I.  The
+ * shared expert's op chain and roundings are those of a one-expert SwitchGLU.
+ * For one token (decode) the shared expert runs inside the routed kernels (one
+ * more gate/up segment, one more wave per down/combine block; top_k <= 15);
+ * otherwise it runs as fmxq_switch_glu on every token, then
+ * fmxq_switch_glu_combine adds its rows.  Extends fmxq_switch_glu_combine; the
+ * reference computes the shared expert with its own qlinear calls. */
+int fmxq_moe_layer(const uint16_t* x, const uint32_t* inds, const uint32_t* w_gate,
+                   const uint16_t* s_gate, const uint16_t* b_gate, const uint32_t* w_up,
+                   const uint16_t* s_up, const uint16_t* b_up, const uint32_t* w_down,
+                   const uint16_t* s_down, const uint16_t* b_down, const uint16_t* weights,
+                   const uint32_t* sw_gate, const uint16_t* ss_gate, const uint16_t* sb_gate,
+                   const uint32_t* sw_up, const uint16_t* ss_up, const uint16_t* sb_up,
+                   const uint32_t* sw_down, const uint16_t* ss_down, const uint16_t* sb_down,
+                   const uint16_t* shared_gate, uint16_t* out, int64_t T, int64_t top_k,
+                   int64_t E, int64_t D, int64_t I, int group_size, int bits, void* stream);
+
 /* Bytes of device memory each GPU holds, from library load to process exit, for
  * fmxq_switch_glu_noalloc's scratch (a file-scope __device__ array). */
 #define FMXQ_NOALLOC_SCRATCH_BYTES (32u << 20)

@@ -605,3 +605,108 @@ def test_switch_glu_combine_few_slots_shapes(gpu, oracle, I, gated, E, T, k):
         shv = r16(gt[:, None] * shv)
     parity.combine_check(got, near, allow, wts, shared=(shv, 2.0 ** -8 * np.abs(shv)),
                          what=f"switch_glu_combine I={I}")
+
+
+# --- moe_layer: routed experts, weighted sum and the shared expert in one call ---
+
+@pytest.mark.parametrize("M", [1, 3, 32])
+def test_moe_layer_shared_expert_c4(gpu, oracle, M):
+    """Configuration 4 with its shared expert computed inside the call
+    (deepseekv3_forward.go:436-440: routed sum + mlp(x)).  One token runs the
+    shared expert as one more gate/up segment and one more down/combine wave; more
+    tokens run it as a one-expert SwitchGLU first.  Checked element by element
+    against the oracle's routed experts and shared MLP."""
+    from fastmlx_amd import ops
+
+    (gate, up, down), dstack, shared, dshared = _layer_weights(gpu, "c4")
+    rng = np.random.default_rng(950 + M)
+    E, D = gate[0].shape[0], down[0].shape[1]
+    k = 8
+    inds = topk_zipf(rng, M, E, k)
+    g = 1 / (1 + np.exp(-rng.standard_normal((M, k))))
+    w16 = oracle.f32_to_bf16((g / g.sum(1, keepdims=True)).astype(np.float32))
+    x = make_x(rng, M, D)
+    announce(f"moe_layer c4 M={M} slots={M * k} + shared expert")
+    out = ops.moe_layer(to_dev(x, gpu), to_dev(inds.astype(np.uint32), gpu), *dstack,
+                        to_dev(w16, gpu), dshared)
+    torch.cuda.synchronize()
+    got = to_np(out)
+    sel = np.unique(np.concatenate([[0, M - 1], rng.choice(M, size=min(M, 3), replace=False)]))
+    sref = parity.SwitchRef(x, inds, gate, up, down, token_sel=sel, fused=False)
+    near = sref.refs[0]
+    zi = np.zeros((M, 1), dtype=np.int32)
+    ssref = parity.SwitchRef(x, zi, *shared, token_sel=sel, fused=False)
+    sv = ssref.refs[0]
+    sa = parity.switch_bound(sv, sv, ssref.hscale)
+    parity.combine_check(got[sel], near, parity.switch_bound(near, near, sref.hscale), w16[sel],
+                         shared=(sv[:, 0], sa[:, 0]), what=f"moe_layer c4 M={M}")
+
+
+@pytest.mark.parametrize("T", [1, 2])
+def test_moe_layer_gated_shared_expert(gpu, oracle, T):
+    """A Qwen3-Next-style layer (qwen3next_forward.go:519-524): the shared expert's
+    output scaled by sigmoid(shared_gate) before it is added; one token fused,
+    two tokens through the one-expert SwitchGLU."""
+    from fastmlx_amd import ops
+
+    rng = np.random.default_rng(960 + T)
+    E, D, I, k = 300, 2048, 512, 10
+    gate, up, down = _stack(rng, E, D, I)
+    sh = _stack(rng, 1, D, I)
+    x = make_x(rng, T, D)
+    inds = topk_uniform(rng, T, E, k)
+    w16 = oracle.f32_to_bf16(rng.dirichlet(np.ones(k), size=T).astype(np.float32))
+    sg = make_x(rng, T)
+    dev = lambda t: to_dev(t, gpu)
+    announce(f"moe_layer gated shared T={T}")
+    out = ops.moe_layer(dev(x), dev(inds.astype(np.uint32)), tuple(map(dev, gate)),
+                        tuple(map(dev, up)), tuple(map(dev, down)), dev(w16),
+                        tuple(tuple(map(dev, q)) for q in sh), dev(sg))
+    torch.cuda.synchronize()
+    got = to_np(out)
+    sref = parity.SwitchRef(x, inds, gate, up, down, fused=False)
+    near = sref.refs[0]
+    ssref = parity.SwitchRef(x, np.zeros((T, 1), dtype=np.int32), *sh, fused=False)
+    sv = ssref.refs[0][:, 0]
+    sa = parity.switch_bound(ssref.refs[0], ssref.refs[0], ssref.hscale)[:, 0]
+    r16 = lambda v: oracle.bf16_to_f32(oracle.f32_to_bf16(np.asarray(v, np.float32))).astype(np.float64)
+    gt = r16(1 / (1 + np.exp(-oracle.bf16_to_f32(sg).astype(np.float64))))[:, None]
+    shv = r16(gt * sv)
+    parity.combine_check(got, near, parity.switch_bound(near, near, sref.hscale), w16,
+                         shared=(shv, gt * sa + 2.0 ** -8 * np.abs(shv)),
+                         what=f"moe_layer gated T={T}")
+
+
+def test_moe_layer_bad_expert_id(gpu, oracle):
+    """A bad routed id in the fused one-token form: its slot contributes zero, the
+    shared expert and the other slots still add up, and the flag is raised."""
+    from fastmlx_amd import FmxqError, ops
+
+    rng = np.random.default_rng(971)
+    E, D, I, k = 40, 2048, 512, 6
+    gate, up, down = _stack(rng, E, D, I)
+    sh = _stack(rng, 1, D, I)
+    x = make_x(rng, 1, D)
+    inds = topk_uniform(rng, 1, E, k)
+    inds[0, 2] = E + 7
+    w16 = oracle.f32_to_bf16(rng.dirichlet(np.ones(k), size=1).astype(np.float32))
+    dev = lambda t: to_dev(t, gpu)
+    announce("moe_layer bad id")
+    out = ops.moe_layer(dev(x), dev(inds.astype(np.uint32)), tuple(map(dev, gate)),
+                        tuple(map(dev, up)), tuple(map(dev, down)), dev(w16),
+                        tuple(tuple(map(dev, q)) for q in sh))
+    torch.cuda.synchronize()
+    got = to_np(out)
+    with pytest.raises(FmxqError):
+        ops.device_error()
+    safe = np.where(inds >= E, 0, inds)
+    sref = parity.SwitchRef(x, safe, gate, up, down, fused=False)
+    near = sref.refs[0].copy()
+    near[0, 2] = 0.0
+    allow = parity.switch_bound(near, near, sref.hscale)
+    allow[0, 2] = 0.0
+    ssref = parity.SwitchRef(x, np.zeros((1, 1), dtype=np.int32), *sh, fused=False)
+    sv = ssref.refs[0]
+    sa = parity.switch_bound(sv, sv, ssref.hscale)
+    parity.combine_check(got, near, allow, w16, shared=(sv[:, 0], sa[:, 0]),
+                         what="moe_layer bad id")
