@@ -190,6 +190,8 @@ int device_cus(int* out) {
 // (fmxq_switch_glu_combine), while slot 0 serves the SwitchGLU itself.
 std::mutex g_arena_mu;
 std::map<std::tuple<int, hipStream_t, int>, std::pair<void*, size_t>> g_arena;
+// Words of a zero-id buffer (fmxq_moe_layer, arena slot 3) already filled.
+std::map<const void*, int64_t> g_zero_filled;
 
 int stream_arena(hipStream_t s, size_t bytes, void** out, const char* op, int slot = 0) {
   int dev = 0;
@@ -823,16 +825,31 @@ extern "C" int fmxq_moe_layer(
                       "moe_layer: down/combine");
   }
   // Otherwise the shared expert as a one-expert SwitchGLU over every token (its
-  // rows and the all-zero expert ids in the arena's slot 2), then the routed part
-  // with those rows as the shared term.
-  const size_t zb = align_up((size_t)T * sizeof(uint32_t));
+  // rows in the arena's slot 2), then the routed part with those rows as the
+  // shared term.  Its all-zero expert ids live in slot 3, which only ever holds
+  // zeros: a buffer is filled once, as far as the calls on it have needed.
   void* arena = nullptr;
-  if (int rc = stream_arena(s, zb + align_up((size_t)T * D * sizeof(uint16_t)), &arena, op, 2))
+  if (int rc = stream_arena(s, align_up((size_t)T * D * sizeof(uint16_t)), &arena, op, 2))
     return rc;
-  uint32_t* zinds = static_cast<uint32_t*>(arena);
-  uint16_t* rows = reinterpret_cast<uint16_t*>(static_cast<char*>(arena) + zb);
-  if (int rc = hip_status(fmxq::launch_fill_u32(zinds, 0u, T, s), "moe_layer: shared ids"))
-    return rc;
+  uint16_t* rows = static_cast<uint16_t*>(arena);
+  void* zarena = nullptr;
+  if (int rc = stream_arena(s, align_up((size_t)T * sizeof(uint32_t)), &zarena, op, 3)) return rc;
+  uint32_t* zinds = static_cast<uint32_t*>(zarena);
+  // A fill recorded into a graph under capture has not run yet, so only an eager
+  // fill counts.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  const bool capturing =
+      hipStreamIsCapturing(s, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone;
+  bool filled = false;
+  {
+    std::lock_guard<std::mutex> lk(g_arena_mu);
+    auto& z = g_zero_filled[zinds];
+    filled = z >= T;
+    if (!filled && !capturing) z = T;
+  }
+  if (!filled)
+    if (int rc = hip_status(fmxq::launch_fill_u32(zinds, 0u, T, s), "moe_layer: shared ids"))
+      return rc;
   if (int rc = switch_glu_impl(x, zinds, sw_gate, ss_gate, sb_gate, sw_up, ss_up, sb_up, sw_down,
                                ss_down, sb_down, rows, T, 1, 1, D, I, group_size, bits, stream,
                                ScratchSource(), op))

@@ -710,3 +710,49 @@ def test_moe_layer_bad_expert_id(gpu, oracle):
     sa = parity.switch_bound(sv, sv, ssref.hscale)
     parity.combine_check(got, near, allow, w16, shared=(sv[:, 0], sa[:, 0]),
                          what="moe_layer bad id")
+
+
+def test_moe_layer_graph_replay(gpu, oracle):
+    """moe_layer under HIP graph capture: the one-token form and the several-token
+    form (whose shared expert ids come from a zero buffer filled once per buffer)
+    replay to the eager result every time, with eager calls of other sizes on the
+    same stream in between."""
+    from fastmlx_amd import ops
+
+    (gate, up, down), dstack, shared, dshared = _layer_weights(gpu, "c4")
+    rng = np.random.default_rng(990)
+    E, D = gate[0].shape[0], down[0].shape[1]
+    k = 8
+    cases = []
+    for T in (1, 4):
+        inds = topk_zipf(rng, T, E, k)
+        g = 1 / (1 + np.exp(-rng.standard_normal((T, k))))
+        w16 = oracle.f32_to_bf16((g / g.sum(1, keepdims=True)).astype(np.float32))
+        cases.append((to_dev(make_x(rng, T, D), gpu), to_dev(inds.astype(np.uint32), gpu),
+                      to_dev(w16, gpu), torch.empty(T, D, dtype=torch.bfloat16, device=gpu)))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+
+    def step():
+        for x, inds, w, out in cases:
+            ops.moe_layer(x, inds, *dstack, w, dshared, out=out)
+
+    announce("moe_layer graph capture")
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.synchronize()
+    eager = [to_np(c[-1]).copy() for c in cases]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        step()
+    xo, io, wo, oo = cases[1]
+    for rep in range(3):
+        for c in cases:
+            c[-1].zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for c, e in zip(cases, eager):
+            assert np.array_equal(to_np(c[-1]), e), f"replay {rep} differs from eager"
+        with torch.cuda.stream(side):  # eager work of another size between replays
+            ops.moe_layer(xo[:2], io[:2], *dstack, wo[:2], dshared)
+        torch.cuda.synchronize()
