@@ -112,6 +112,22 @@ def test_switch_glu_and_combine_validation():
     assert _status(sg(topk=0)) == "FMXQ_ERR_SHAPE"
     assert _status(sg()) == "FMXQ_ERR_INVALID_ARGUMENT"
     assert sg(T=0) == 0
+    ml = lambda ptrs, **k: lib.fmxq_moe_layer(*ptrs, k.get("T", 1), k.get("topk", 2),
+                                              k.get("E", 4), k.get("D", 64), k.get("I", 64),
+                                              k.get("group", 64), k.get("bits", 4), None)
+    fake = ctypes.c_void_p(0x1000)
+    full = [fake] * 21 + [None, fake]  # routed + weights + shared triples, no gate, out
+    assert _status(ml([None] * 23, bits=2)) == "FMXQ_ERR_UNSUPPORTED"
+    assert _status(ml([None] * 23, D=100)) == "FMXQ_ERR_SHAPE"
+    assert _status(ml([None] * 23, topk=0)) == "FMXQ_ERR_SHAPE"
+    assert ml([None] * 23, T=0) == 0
+    for i in range(12, 21):  # each of the shared expert's pointers is required
+        ptrs = list(full)
+        ptrs[i] = None
+        assert _status(ml(ptrs)) == "FMXQ_ERR_INVALID_ARGUMENT", i
+    ptrs = list(full)
+    ptrs[18] = ctypes.c_void_p(0x1008)  # shared down weights not 16-byte aligned
+    assert _status(ml(ptrs)) == "FMXQ_ERR_INVALID_ARGUMENT"
     mc = lib.fmxq_moe_combine
     assert _status(mc(None, None, None, None, None, 2, 2, 7, None)) == "FMXQ_ERR_SHAPE"
     assert _status(mc(None, None, None, None, None, 2, 2, 8, None)) == "FMXQ_ERR_INVALID_ARGUMENT"
