@@ -357,12 +357,14 @@ int qmm_common(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
   if (skinny) return hip_status(fmxq::launch_qmvs(a, s), op);
   // 5 <= M <= 32 shapes qmvs does not take (int8, other group sizes) run on the
   // prefill GEMM's 64-row tile; M <= 4 stays on the dot2 GEMV, and so do int8
-  // products with M <= 8 and at most 4096 rows where the x rows fit in registers
-  // (M = 5, int8: 4096x4096 16.0 -> 12.8 us, 1024x4096 12.2 -> 5.8 us; at
-  // 14336x4096 the two measure the same).
-  const bool small_gemm = M > fmxq::kQmvMaxM && M <= fmxq::kSkinnyMaxM &&
-                          !fmxq::qmvs_supported(a) && fmxq::qmm_prefill_supported(a) &&
-                          !(bits == 8 && M <= 8 && N <= 4096 && fmxq::qmv_supported(a));
+  // products where the x rows fit in registers: M <= 6 on any output width, M = 7
+  // and 8 up to 4096 rows (int8 M = 5 against the prefill tile: 4096x4096 16.0 ->
+  // 9.6 us, 14336x4096 35.7 -> 25.0 us, 28672x4096 60.3 -> 46.2 us; M = 8 at
+  // 14336x4096 36.1 against 37.3 us stays on the tile).
+  const bool small_gemm =
+      M > fmxq::kQmvMaxM && M <= fmxq::kSkinnyMaxM && !fmxq::qmvs_supported(a) &&
+      fmxq::qmm_prefill_supported(a) &&
+      !(bits == 8 && (M <= 6 || (M <= 8 && N <= 4096)) && fmxq::qmv_supported(a));
   if (!small_gemm && fmxq::qmv_supported(a)) return hip_status(fmxq::launch_qmv(a, s), op);
   if (!small_gemm && M <= fmxq::kSkinnyMaxM && fmxq::qmv_mfma_supported(a))
     return hip_status(fmxq::launch_qmv_mfma(a, s), op);

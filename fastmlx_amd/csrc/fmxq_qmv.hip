@@ -47,8 +47,10 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 // 1 KiB contiguous per row.  Each packed word is unpacked once (exponent trick, 7
 // VALU) and dotted against every x row (4 v_dot2 each); a 3-op group correction
 // per chunk and row follows.  The RPW x MM partial sums are reduced together at
-// the end (wave_sum_multi).
-template <int BITS, int MM, int CPL, int R, int RPW, int KS, int WAVES = 4>
+// the end (wave_sum_multi).  MM is M padded to a power of two; only the first MX
+// x rows are built and dotted (MX = M for M = 5..7: M = 5 on 1024x4096 took 5.5
+// us with all 8 rows, 4.6 us with 5), the padding rows' partials being zero.
+template <int BITS, int MM, int CPL, int R, int RPW, int KS, int WAVES = 4, int MX = MM>
 __global__ __launch_bounds__(WAVES * 64) void qmvx_kernel(QmmArgs a) {
   constexpr int CH = 128 / BITS;  // values per 16-byte chunk
   constexpr int RG = WAVES / KS;
@@ -77,7 +79,7 @@ __global__ __launch_bounds__(WAVES * 64) void qmvx_kernel(QmmArgs a) {
     cc[i] = live[i] ? c : c0;
   }
 
-  XChunk<BITS> xc[MM][CPL];
+  XChunk<BITS> xc[MX][CPL];
   u32x4 wv0[R][CPL], wv1[R][CPL];
   // Scale and bias bits stay in separate registers until the arithmetic: packing
   // them at load time would make the compiler wait for each load right away.
@@ -117,7 +119,7 @@ __global__ __launch_bounds__(WAVES * 64) void qmvx_kernel(QmmArgs a) {
           uint32_t p[16];
           unpack_chunk(wv[r][i], p);
 #pragma unroll
-          for (int m = 0; m < MM; ++m) {
+          for (int m = 0; m < MX; ++m) {
             const float t = __builtin_fmaf(s, dot_pairs<BITS>(p, xc[m][i]), bo * xc[m][i].sum);
             acc[m] += live[i] ? t : 0.f;
           }
@@ -142,7 +144,7 @@ __global__ __launch_bounds__(WAVES * 64) void qmvx_kernel(QmmArgs a) {
   // reuse x's registers.
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int m = 0; m < MM; ++m) {
+  for (int m = 0; m < MX; ++m) {
     const uint16_t* xr = a.x + (int64_t)(m < a.M ? m : a.M - 1) * a.ldx;
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
@@ -520,25 +522,25 @@ static QmvxShape pick_qmvx_shape(int64_t nch, int64_t N, int mm) {
   return sh;
 }
 
-template <int BITS, int MM, int CPL, int RPW, int KS, int WAVES, int R = 2>
+template <int BITS, int MM, int CPL, int RPW, int KS, int WAVES, int R = 2, int MX = MM>
 static hipError_t launch_qmvx_cfg(const QmmArgs& a, hipStream_t stream) {
   constexpr int64_t rows_per_block = (WAVES / KS) * RPW;
   const unsigned blocks = (unsigned)((a.N + rows_per_block - 1) / rows_per_block);
-  qmvx_kernel<BITS, MM, CPL, R, RPW, KS, WAVES><<<blocks, WAVES * 64, 0, stream>>>(a);
+  qmvx_kernel<BITS, MM, CPL, R, RPW, KS, WAVES, MX><<<blocks, WAVES * 64, 0, stream>>>(a);
   return hipGetLastError();
 }
 
-template <int BITS, int MM, int CPL, int KS, int WAVES = 4>
+template <int BITS, int MM, int CPL, int KS, int WAVES = 4, int MX = MM>
 static hipError_t launch_qmvx_rpw(const QmmArgs& a, int rpw, hipStream_t stream, int r = 2) {
   if constexpr (MM == 1 && CPL == 1) {
-    if (rpw == 4 && r == 4) return launch_qmvx_cfg<BITS, MM, CPL, 4, KS, WAVES, 4>(a, stream);
+    if (rpw == 4 && r == 4) return launch_qmvx_cfg<BITS, MM, CPL, 4, KS, WAVES, 4, MX>(a, stream);
   }
-  if (rpw == 2) return launch_qmvx_cfg<BITS, MM, CPL, 2, KS, WAVES>(a, stream);
+  if (rpw == 2) return launch_qmvx_cfg<BITS, MM, CPL, 2, KS, WAVES, 2, MX>(a, stream);
   if constexpr (MM <= 8) {
-    if (rpw == 4) return launch_qmvx_cfg<BITS, MM, CPL, 4, KS, WAVES>(a, stream);
+    if (rpw == 4) return launch_qmvx_cfg<BITS, MM, CPL, 4, KS, WAVES, 2, MX>(a, stream);
   }
-  if constexpr (MM <= 4) return launch_qmvx_cfg<BITS, MM, CPL, 8, KS, WAVES>(a, stream);
-  return launch_qmvx_cfg<BITS, MM, CPL, 4, KS, WAVES>(a, stream);
+  if constexpr (MM <= 4) return launch_qmvx_cfg<BITS, MM, CPL, 8, KS, WAVES, 2, MX>(a, stream);
+  return launch_qmvx_cfg<BITS, MM, CPL, 4, KS, WAVES, 2, MX>(a, stream);
 }
 
 // The M <= 8 rows of x padded to 1, 2, 4 or 8; shapes whose x chunks would not
@@ -551,20 +553,20 @@ static bool qmvx_supported(const QmmArgs& a, int bits) {
   return pick_qmvx_shape(nch, a.N, qmvx_mm(a.M)).cpl > 0;
 }
 
-template <int BITS, int MM>
+template <int BITS, int MM, int MX = MM>
 static hipError_t launch_qmvx_mm(const QmmArgs& a, hipStream_t stream) {
   const QmvxShape sh = pick_qmvx_shape(a.K / (128 / BITS), a.N, MM);
-  if (sh.ks == 8) return launch_qmvx_rpw<BITS, MM, 1, 8, 8>(a, sh.rpw, stream, sh.r);
-  if (sh.ks == 1) return launch_qmvx_rpw<BITS, MM, 1, 1>(a, sh.rpw, stream);
+  if (sh.ks == 8) return launch_qmvx_rpw<BITS, MM, 1, 8, 8, MX>(a, sh.rpw, stream, sh.r);
+  if (sh.ks == 1) return launch_qmvx_rpw<BITS, MM, 1, 1, 4, MX>(a, sh.rpw, stream);
   if (sh.ks == 2) {
-    if (sh.waves == 8) return launch_qmvx_rpw<BITS, MM, 1, 2, 8>(a, sh.rpw, stream, sh.r);
-    return launch_qmvx_rpw<BITS, MM, 1, 2>(a, sh.rpw, stream, sh.r);
+    if (sh.waves == 8) return launch_qmvx_rpw<BITS, MM, 1, 2, 8, MX>(a, sh.rpw, stream, sh.r);
+    return launch_qmvx_rpw<BITS, MM, 1, 2, 4, MX>(a, sh.rpw, stream, sh.r);
   }
-  if (sh.cpl == 1) return launch_qmvx_rpw<BITS, MM, 1, 4>(a, sh.rpw, stream);
+  if (sh.cpl == 1) return launch_qmvx_rpw<BITS, MM, 1, 4, 4, MX>(a, sh.rpw, stream);
   if constexpr (MM <= 4) {
-    if (sh.cpl == 2) return launch_qmvx_rpw<BITS, MM, 2, 4>(a, sh.rpw, stream);
+    if (sh.cpl == 2) return launch_qmvx_rpw<BITS, MM, 2, 4, 4, MX>(a, sh.rpw, stream);
   }
-  if constexpr (MM <= 2) return launch_qmvx_rpw<BITS, MM, 4, 4>(a, sh.rpw, stream);
+  if constexpr (MM <= 2) return launch_qmvx_rpw<BITS, MM, 4, 4, 4, MX>(a, sh.rpw, stream);
   return hipErrorInvalidValue;  // excluded by qmvx_supported
 }
 
@@ -574,7 +576,11 @@ static hipError_t launch_qmvx(const QmmArgs& a, hipStream_t stream) {
     case 1: return launch_qmvx_mm<BITS, 1>(a, stream);
     case 2: return launch_qmvx_mm<BITS, 2>(a, stream);
     case 4: return launch_qmvx_mm<BITS, 4>(a, stream);
-    default: return launch_qmvx_mm<BITS, 8>(a, stream);
+    default:
+      if (a.M == 5) return launch_qmvx_mm<BITS, 8, 5>(a, stream);
+      if (a.M == 6) return launch_qmvx_mm<BITS, 8, 6>(a, stream);
+      if (a.M == 7) return launch_qmvx_mm<BITS, 8, 7>(a, stream);
+      return launch_qmvx_mm<BITS, 8>(a, stream);
   }
 }
 

@@ -110,17 +110,18 @@ def test_qmv_other_groups(gpu, oracle, group):
     _qmm_case(gpu, oracle, 7, 384, 1024, 8, group, seed=37 + group)
 
 
-@pytest.mark.parametrize("M", [5, 8, 16, 32, 64, 100, 128, 300])
+@pytest.mark.parametrize("M", [5, 6, 7, 8, 16, 32, 64, 100, 128, 300])
 @pytest.mark.parametrize("bits", [4, 8])
 def test_qmm_mfma_shapes(gpu, oracle, M, bits):
     _qmm_case(gpu, oracle, M, 1024 + 64, 2048, bits, 64, seed=2000 + M + bits)
 
 
-@pytest.mark.parametrize("M", [5, 8])
+@pytest.mark.parametrize("M", [5, 6, 7, 8])
 @pytest.mark.parametrize("N,K", [(4096, 4096), (1024, 4096), (14336, 4096)])
 def test_int8_small_m_shapes(gpu, oracle, M, N, K):
-    """int8 at 5 <= M <= 8: the register GEMV up to 4096 output rows, the prefill
-    GEMM's 64-row tile beyond."""
+    """int8 at 5 <= M <= 8: the register GEMV (only M of its 8 x-row slots built)
+    for M <= 6 and up to 4096 output rows, the prefill GEMM's 64-row tile for
+    M = 7, 8 beyond."""
     _qmm_case(gpu, oracle, M, N, K, 8, 64, seed=14000 + M + N // 1024)
 
 
