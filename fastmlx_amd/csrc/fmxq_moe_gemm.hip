@@ -516,13 +516,16 @@ __global__ __launch_bounds__(1024) void moe_down_combine_kernel(DownCombineArgs 
   float res[PASSES];
 #pragma unroll
   for (int p = 0; p < PASSES; ++p) res[p] = 0.f;
-  if (!bad) {
+  if (!bad && RPP == 1) {
+    // One row per pass (whole-wave rows): plain loads, rows past D re-read row D - 1
+    // (not stored).  Buffer loads measured slower here (configuration 4 at M = 1:
+    // 55.4 -> 57.4 us).
     u32x4 wv[PASSES][CPL];
     uint32_t sv[PASSES][CPL], bv[PASSES][CPL];
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
       int64_t n = n0 + p * RPP + rsub;
-      n = n < a.D ? n : a.D - 1;  // rows past D re-read row D-1; not stored
+      n = n < a.D ? n : a.D - 1;
       const int64_t row = (int64_t)e * a.D + n;
 #pragma unroll
       for (int i = 0; i < CPL; ++i) {
@@ -530,6 +533,47 @@ __global__ __launch_bounds__(1024) void moe_down_combine_kernel(DownCombineArgs 
         wv[p][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wm + row * wpr) + c);
         sv[p][i] = sm[row * gpr + (c >> 1)];
         bv[p][i] = bm[row * gpr + (c >> 1)];
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    XChunk<4> xc[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) xc[i].load(a.h + slot * a.I, (int64_t)(cl + LPR * i) * 32);
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p)
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const float sc = bf16_bits_to_f32(sv[p][i]);
+        const float bo = __builtin_fmaf(-magic_offset<4>(), sc, bf16_bits_to_f32(bv[p][i]));
+        res[p] += __builtin_fmaf(sc, chunk_dot<4>(wv[p][i], xc[i]), bo * xc[i].sum);
+      }
+  } else if (!bad) {
+    // Several rows per pass: the expert's three arrays through buffer resources
+    // (each below 2^31 bytes, moe_down_combine_supported).  A lane's byte offsets
+    // are set once and step by a wave-uniform stride per pass, which saves the
+    // per-pass 64-bit row addressing (configuration 3 at M = 16: 67.6 -> 65.4 us);
+    // rows past D fall outside the resource and read zeros (not stored).
+    const int64_t erow = (int64_t)e * a.D;
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(wm + erow * wpr), (short)0, (int)(a.D * wpr * 4), 0x00020000);
+    const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(sm + erow * gpr), (short)0, (int)(a.D * gpr * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t bres = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(bm + erow * gpr), (short)0, (int)(a.D * gpr * 2), 0x00020000);
+    const int r0 = (int)(n0 + rsub);
+    const int wstep = RPP * (int)wpr * 4, sstep = RPP * (int)gpr * 2;
+    u32x4 wv[PASSES][CPL];
+    uint32_t sv[PASSES][CPL], bv[PASSES][CPL];
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const int c = cl + LPR * i;
+        const int wo = r0 * (int)wpr * 4 + c * 16 + p * wstep;
+        const int so = r0 * (int)gpr * 2 + (c >> 1) * 2 + p * sstep;
+        wv[p][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wres, wo, 0, 2));
+        sv[p][i] = __builtin_amdgcn_raw_buffer_load_b16(sres, so, 0, 0);
+        bv[p][i] = __builtin_amdgcn_raw_buffer_load_b16(bres, so, 0, 0);
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -589,8 +633,11 @@ static hipError_t launch_down_combine_cfg(const DownCombineArgs& a, hipStream_t 
 
 bool moe_down_combine_supported(int64_t T, int64_t k, int64_t D, int64_t I, int bits,
                                 int group_size) {
+  // One expert's down matrix (plus a row tile past its end) stays below 2^30 bytes:
+  // the kernel addresses it through a buffer resource with 32-bit offsets.
   return bits == 4 && group_size == 64 && k >= 1 && k <= 16 && T >= 1 && T <= 65535 &&
-         D >= 1 && (I == 512 || I == 1024 || I == 2048 || I == 4096 || I == 8192);
+         D >= 1 && (I == 512 || I == 1024 || I == 2048 || I == 4096 || I == 8192) &&
+         (D + 64) * (I / 2) < (int64_t(1) << 30);
 }
 
 hipError_t launch_moe_down_combine(const uint16_t* h, const uint32_t* inds, const uint32_t* w,
@@ -617,8 +664,10 @@ hipError_t launch_moe_down_combine(const uint16_t* h, const uint32_t* inds, cons
                     : launch_down_combine_cfg<8, 16, 1>(a, stream);
     case 1024: return launch_down_combine_cfg<16, 32, 1>(a, stream);
     case 2048: return launch_down_combine_cfg<4, 64, 1>(a, stream);
-    case 4096: return launch_down_combine_cfg<8, 64, 2>(a, stream);
-    default: return launch_down_combine_cfg<8, 64, 4>(a, stream);
+    // Longer rows keep fewer rows per block so that a 16-wave block (16 slots)
+    // fits its registers without spilling.
+    case 4096: return launch_down_combine_cfg<4, 64, 2>(a, stream);
+    default: return launch_down_combine_cfg<1, 64, 4>(a, stream);
   }
 }
 

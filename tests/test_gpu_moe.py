@@ -566,10 +566,11 @@ def test_switch_glu_combine_configs(gpu, oracle, cfg, M):
 
 
 @pytest.mark.parametrize("I,gated,E,T,k", [(512, True, 9, 2, 6), (1024, False, 9, 2, 6),
-                                           (4096, True, 9, 2, 6), (512, True, 300, 12, 10)])
+                                           (4096, True, 9, 2, 6), (8192, False, 9, 2, 6),
+                                           (512, True, 300, 12, 10)])
 def test_switch_glu_combine_few_slots_shapes(gpu, oracle, I, gated, E, T, k):
     """The fused down/combine kernel's other row forms (32 lanes per 1024-value row,
-    two chunks per lane at 4096), a sigmoid-gated shared term, a bad expert id
+    two and four chunks per lane at 4096 and 8192), a sigmoid-gated shared term, a bad expert id
     (its slot contributes zero and the flag is raised), and 120 slots over 300
     experts (unsorted beyond 16 slots)."""
     from fastmlx_amd import FmxqError, ops
