@@ -360,16 +360,32 @@ __global__ __launch_bounds__(KS * 64) void moe_qmv1_kernel(MoeArgs a) {
   const int64_t wpr = a.K / 8, gpr = a.K / 64;
   u32x4 wv[NMAT][RW];
   uint32_t sv[NMAT][RW], bv[NMAT][RW];
+  // The expert's matrices through buffer resources (each below 2^31 bytes,
+  // moe_qmvs_supported): the lane's offset is fixed (its chunk) and each row's is
+  // one wave-uniform scalar, so no per-row vector address math.  Rows in 32 bits,
+  // clamped on the scalar unit; rows past N re-read row N-1 and are not stored.
+  const int nb32 = __builtin_amdgcn_readfirstlane((int)nbase);
+  const int nlast = (int)a.N - 1;
+  __amdgpu_buffer_rsrc_t wres[NMAT], sres[NMAT], bres[NMAT];
+#pragma unroll
+  for (int p = 0; p < NMAT; ++p) {
+    const int64_t erow = (int64_t)e * a.N;
+    wres[p] = __builtin_amdgcn_make_buffer_rsrc((void*)(wp[p] + erow * wpr), (short)0,
+                                                (int)(a.N * wpr * 4), 0x00020000);
+    sres[p] = __builtin_amdgcn_make_buffer_rsrc((void*)(sp[p] + erow * gpr), (short)0,
+                                                (int)(a.N * gpr * 2), 0x00020000);
+    bres[p] = __builtin_amdgcn_make_buffer_rsrc((void*)(bp[p] + erow * gpr), (short)0,
+                                                (int)(a.N * gpr * 2), 0x00020000);
+  }
 #pragma unroll
   for (int p = 0; p < NMAT; ++p)
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
-      int64_t n = nbase + r;
-      n = n < a.N ? n : a.N - 1;  // rows past N re-read row N-1; not stored
-      const int64_t row = (int64_t)e * a.N + n;
-      wv[p][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp[p] + row * wpr) + cc);
-      sv[p][r] = sp[p][row * gpr + g];
-      bv[p][r] = bp[p][row * gpr + g];
+      const int n = __builtin_amdgcn_readfirstlane(min(nb32 + r, nlast));
+      wv[p][r] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(wres[p], cc * 16, n * (int)wpr * 4, 2));
+      sv[p][r] = __builtin_amdgcn_raw_buffer_load_b16(sres[p], g * 2, n * (int)gpr * 2, 0);
+      bv[p][r] = __builtin_amdgcn_raw_buffer_load_b16(bres[p], g * 2, n * (int)gpr * 2, 0);
     }
   // The weight requests go out before x is read and paired.
   __builtin_amdgcn_sched_barrier(0);
