@@ -643,15 +643,18 @@ def test_moe_layer_shared_expert_c4(gpu, oracle, M):
                          shared=(sv[:, 0], sa[:, 0]), what=f"moe_layer c4 M={M}")
 
 
-@pytest.mark.parametrize("T", [1, 2])
-def test_moe_layer_gated_shared_expert(gpu, oracle, T):
+@pytest.mark.parametrize("T,E,D,k", [(1, 300, 2048, 10), (2, 300, 2048, 10),
+                                     (1, 64, 2048, 16), (1, 40, 512, 6)])
+def test_moe_layer_gated_shared_expert(gpu, oracle, T, E, D, k):
     """A Qwen3-Next-style layer (qwen3next_forward.go:519-524): the shared expert's
-    output scaled by sigmoid(shared_gate) before it is added; one token fused,
-    two tokens through the one-expert SwitchGLU."""
+    output scaled by sigmoid(shared_gate) before it is added.  One token with up
+    to 15 slots and D >= 2048 runs fused; two tokens, 16 slots (a block would need
+    17 waves) and D = 512 (below the GEMV form's depth) run the one-expert
+    SwitchGLU first."""
     from fastmlx_amd import ops
 
-    rng = np.random.default_rng(960 + T)
-    E, D, I, k = 300, 2048, 512, 10
+    rng = np.random.default_rng(960 + T + k + D)
+    I = 512
     gate, up, down = _stack(rng, E, D, I)
     sh = _stack(rng, 1, D, I)
     x = make_x(rng, T, D)
@@ -659,7 +662,7 @@ def test_moe_layer_gated_shared_expert(gpu, oracle, T):
     w16 = oracle.f32_to_bf16(rng.dirichlet(np.ones(k), size=T).astype(np.float32))
     sg = make_x(rng, T)
     dev = lambda t: to_dev(t, gpu)
-    announce(f"moe_layer gated shared T={T}")
+    announce(f"moe_layer gated shared T={T} E={E} D={D} k={k}")
     out = ops.moe_layer(dev(x), dev(inds.astype(np.uint32)), tuple(map(dev, gate)),
                         tuple(map(dev, up)), tuple(map(dev, down)), dev(w16),
                         tuple(tuple(map(dev, q)) for q in sh), dev(sg))
