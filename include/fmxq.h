@@ -140,8 +140,10 @@ int fmxq_switch_glu(const uint16_t* x, const uint32_t* inds, const uint32_t* w_g
  * expert outputs y never leaving the chip for decode-sized batches
  * (qwen3next_forward.go:510-525, deepseekv3_forward.go:427-442).  Arguments are
  * those of the two calls; the op chain and its bf16 roundings are theirs.  Up to
- * 16 routing slots (int4, group 64) the down projection and the weighted sum run
- * as one kernel; otherwise the expert rows go through a per-stream buffer. */
+ * 16 routing slots, and up to 256 slots routed over at least twice as many
+ * experts (int4, group 64), the slots stay unsorted and the down projection and
+ * the weighted sum run as one kernel; otherwise the expert rows go through a
+ * per-stream buffer. */
 int fmxq_switch_glu_combine(const uint16_t* x, const uint32_t* inds, const uint32_t* w_gate,
                             const uint16_t* s_gate, const uint16_t* b_gate,
                             const uint32_t* w_up, const uint16_t* s_up, const uint16_t* b_up,
