@@ -125,6 +125,14 @@ def test_int8_small_m_shapes(gpu, oracle, M, N, K):
     _qmm_case(gpu, oracle, M, N, K, 8, 64, seed=14000 + M + N // 1024)
 
 
+@pytest.mark.parametrize("M,N,K,bits", [(6, 1024, 14336, 4), (7, 1000, 8192, 4),
+                                         (5, 2048, 8192, 8), (6, 3000, 4096, 8)])
+def test_register_gemv_partial_rows(gpu, oracle, M, N, K, bits):
+    """The register GEMV with 5..7 of its 8 x-row slots built, on the 8-slice form
+    of long rows and on ragged row counts."""
+    _qmm_case(gpu, oracle, M, N, K, bits, 64, seed=15000 + M * 7 + N + K + bits)
+
+
 def test_qmm_ragged_n(gpu, oracle):
     # N not a multiple of any tile, K a multiple of 32 only
     _qmm_case(gpu, oracle, 1, 333, 96, 4, 32, seed=5)
