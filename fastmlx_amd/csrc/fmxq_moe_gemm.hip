@@ -337,7 +337,10 @@ __global__ __launch_bounds__(KS * 64) void moe_qmv1_kernel(MoeArgs a) {
 #pragma unroll
   for (int m = 0; m < MM; ++m) {
     const int64_t slot = start + (m < len ? m : 0);
-    const int64_t r = shs ? sg - a.S : a.lhs ? (int64_t)a.lhs[slot] : slot / a.lhs_div;
+    // Slot counts stay below 2^31 (checked by the callers): a 32-bit division.
+    const int64_t r = shs ? sg - a.S
+                          : a.lhs ? (int64_t)a.lhs[slot]
+                                  : (int64_t)((uint32_t)slot / (uint32_t)a.lhs_div);
     rbad[m] = r >= a.x_rows;
     xr[m] = rbad[m] ? 0 : r;
     orow[m] = a.yrow ? (int64_t)a.yrow[slot] : slot;
