@@ -143,13 +143,13 @@ __global__ __launch_bounds__(256) void moe_qmvs_kernel(MoeArgs a) {
       for (int p = 0; p < NMAT; ++p)
 #pragma unroll
         for (int t = 0; t < NTT; ++t) acc1[p][0][t] = f32x4{};
-      qmvs_slice<1, NTT, SU, NMAT>(stage[wave], w, sc, bi, nb, a.N, a.K, x1, st0, st1, acc1);
+      qmvs_slice<1, NTT, SU, NMAT, true>(stage[wave], w, sc, bi, nb, a.N, a.K, x1, st0, st1, acc1);
 #pragma unroll
       for (int p = 0; p < NMAT; ++p)
 #pragma unroll
         for (int t = 0; t < NTT; ++t) acc[p][0][t] = acc1[p][0][t];
     } else {
-      qmvs_slice<MT, NTT, SU, NMAT>(stage[wave], w, sc, bi, nb, a.N, a.K, xrow, st0, st1, acc);
+      qmvs_slice<MT, NTT, SU, NMAT, true>(stage[wave], w, sc, bi, nb, a.N, a.K, xrow, st0, st1, acc);
     }
   }
 
@@ -254,7 +254,7 @@ __global__ __launch_bounds__(WV * 64) __attribute__((amdgpu_waves_per_eu(MT == 1
 #pragma unroll
         for (int t = 0; t < NTT; ++t) acc[0][0][t] = acc1[0][t];
       } else {
-        qmvs_walk_xlds<1, MT, NTT, NMAT, WV>(xs[0], xs[1], stage[wave], xres, xo, wave, len, w, sc,
+        qmvs_walk_xlds<1, MT, NTT, NMAT, WV, true>(xs[0], xs[1], stage[wave], xres, xo, wave, len, w, sc,
                                              bi, nb, a.N, a.K, 0, a.K / 256, acc);
       }
     } else {
@@ -264,7 +264,7 @@ __global__ __launch_bounds__(WV * 64) __attribute__((amdgpu_waves_per_eu(MT == 1
         qmvs_walk_xall<MT, NTT, WV, 2>(&xs[0][0], stage[wave], xres, xo, wave, w[0], sc[0], bi[0],
                                        nb, a.N, a.K, 0, a.K / 256, acc[0]);
       else
-        qmvs_walk_xlds<MT, MT, NTT, NMAT, WV>(xs[0], xs[1], stage[wave], xres, xo, wave, len, w,
+        qmvs_walk_xlds<MT, MT, NTT, NMAT, WV, true>(xs[0], xs[1], stage[wave], xres, xo, wave, len, w,
                                               sc, bi, nb, a.N, a.K, 0, a.K / 256, acc);
     }
   }

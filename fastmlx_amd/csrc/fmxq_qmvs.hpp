@@ -19,7 +19,11 @@
 //     lanes that use them through ds_bpermute.
 // A = x in the same k order (xfrag4 of two 16-byte pieces per unit), XD units
 // ahead.  Per group: P = sum x (128 + q), xs = sum x (MFMA against ones),
-// acc += s P + (b - 128 s) xs.
+// acc += s P + (b - 128 s) xs.  With FOLD the bias term of four groups goes in
+// as one fp32 MFMA (qmvs_bias4) instead of per-group FMAs: fewer VALU
+// operations, one more MFMA dependency on the accumulators.  The MoE walks (two
+// matrices per wave, VALU-bound) take it; the dense walks measured slower
+// with it and do not.
 //
 // The stage needs no barrier: a wave reads only what it wrote, and the LDS
 // operations of one wave complete in order.  Rows past N re-read row N-1 and
@@ -43,6 +47,36 @@ __device__ __forceinline__ int qmvs_pos(int c, int r) {
   else return c ^ (r & 15);
 }
 
+// The bias term of four consecutive units u = 0..3 (K order):
+// acc[m][c] += sum_u xs_m(u) bo_c(u), with xs_m(u) the sum of x row m over unit
+// u and bo_c(u) = b - 128 s of output column c in unit u, as one
+// v_mfma_f32_16x16x4_f32 whose A operand (lane l: row l % 16, k = l / 16) is the
+// x sum and B operand (lane l: k = l / 16, column l % 16) the column offset.
+// Each unit's values are computed in every lane and kept (qmvs_pick) by the
+// lanes whose l / 16 is the unit's position in its group of four.
+//
+// Sum of x row l % 16 over a unit (A fragment a): the x fragment as the B operand
+// of an MFMA against ones, so the result's column (l % 16) is the x row.
+__device__ __forceinline__ float qmvs_xsum(const bf16x8 (&a)[2]) {
+  const bf16x8 ones = as_bf16x8(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+  f32x4 s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, a[0], f32x4{}, 0, 0, 0);
+  s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, a[1], s, 0, 0, 0);
+  return s[0];
+}
+// Without the fold: the sums of x rows 4 (l / 16) + r (the accumulator's rows)
+// over a unit, x as the A operand against ones.
+__device__ __forceinline__ f32x4 qmvs_xsum_rows(const bf16x8 (&a)[2]) {
+  const bf16x8 ones = as_bf16x8(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+  f32x4 s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], ones, f32x4{}, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], ones, s, 0, 0, 0);
+}
+__device__ __forceinline__ float qmvs_pick(int j, float v, float held) {
+  return ((threadIdx.x & 63) >> 4) == (j & 3) ? v : held;
+}
+__device__ __forceinline__ f32x4 qmvs_bias4(float xs, float bo, f32x4 acc) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(xs, bo, acc, 0, 0, 0);
+}
+
 template <int NTT, int SU>
 struct QmvsGeom {
   static constexpr int ROWS = 16 * NTT;
@@ -55,7 +89,7 @@ struct QmvsGeom {
 
 // w, sc, bi: the NMAT matrices ([N, K/8] u32, [N, K/64] bf16 x2).  stage: this
 // wave's NMAT * STAGE bytes of LDS.  xrow: per-lane x row pointers (see above).
-template <int MT, int NTT, int SU, int NMAT>
+template <int MT, int NTT, int SU, int NMAT, bool FOLD>
 __device__ __forceinline__ void qmvs_slice(uint8_t* stage, const uint32_t* const (&w)[NMAT],
                                            const uint16_t* const (&sc)[NMAT],
                                            const uint16_t* const (&bi)[NMAT], int64_t nb,
@@ -133,7 +167,6 @@ __device__ __forceinline__ void qmvs_slice(uint8_t* stage, const uint32_t* const
       xv[d][mt][1] = xs[1];
     }
   };
-  const bf16x8 ones = as_bf16x8(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
 
   if (s1 <= s0) return;
   load_w(0, s0);
@@ -168,6 +201,9 @@ __device__ __forceinline__ void qmvs_slice(uint8_t* stage, const uint32_t* const
               sv[p][t][k] = (uint32_t)__shfl((int)mine[p][idx], (2 * hi) * ROWS + row, 64);
               bv[p][t][k] = (uint32_t)__shfl((int)mine[p][idx], (2 * hi + 1) * ROWS + row, 64);
             }
+        static_assert(!FOLD || SU % 4 == 0, "bias term per four units");
+        float xsel[MT] = {}, bsel[NMAT][NTT] = {};
+        f32x4 xr[MT];
 #pragma unroll
         for (int j = 0; j < SU; ++j) {
           const int xd = (e * SU + j) % XD;
@@ -178,11 +214,10 @@ __device__ __forceinline__ void qmvs_slice(uint8_t* stage, const uint32_t* const
             A[mt][1] = xfrag4(xv[xd][mt][1]);
           }
           load_x(xd, stp * SU + j + XD);
-          f32x4 xs[MT];
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
-            xs[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mt][0], ones, f32x4{}, 0, 0, 0);
-            xs[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mt][1], ones, xs[mt], 0, 0, 0);
+            if constexpr (FOLD) xsel[mt] = qmvs_pick(j, qmvs_xsum(A[mt]), xsel[mt]);
+            else xr[mt] = qmvs_xsum_rows(A[mt]);
           }
 #pragma unroll
           for (int p = 0; p < NMAT; ++p) {
@@ -205,13 +240,24 @@ __device__ __forceinline__ void qmvs_slice(uint8_t* stage, const uint32_t* const
               const float s = (j & 1) ? bf16_hi(sv[p][t][j >> 1]) : bf16_lo(sv[p][t][j >> 1]);
               const float b = (j & 1) ? bf16_hi(bv[p][t][j >> 1]) : bf16_lo(bv[p][t][j >> 1]);
               const float bo = __builtin_fmaf(-128.f, s, b);
+              if constexpr (FOLD) bsel[p][t] = qmvs_pick(j, bo, bsel[p][t]);
 #pragma unroll
               for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                  acc[p][mt][t][r] = __builtin_fmaf(s, P[mt][t][r],
-                                                    __builtin_fmaf(bo, xs[mt][r], acc[p][mt][t][r]));
+                  acc[p][mt][t][r] = __builtin_fmaf(
+                      s, P[mt][t][r],
+                      FOLD ? acc[p][mt][t][r] : __builtin_fmaf(bo, xr[mt][r], acc[p][mt][t][r]));
             }
+          }
+          if (FOLD && (j & 3) == 3) {
+#pragma unroll
+            for (int p = 0; p < NMAT; ++p)
+#pragma unroll
+              for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int t = 0; t < NTT; ++t)
+                  acc[p][mt][t] = qmvs_bias4(xsel[mt], bsel[p][t], acc[p][mt][t]);
           }
         }
       }
@@ -252,7 +298,7 @@ constexpr int kXStageRow = 512;
 // ahead, as in qmvs_slice) and runs the MFMAs.  Skipped DMA instructions change
 // no wait: the explicit wait counts only the weight loads issued after a step's
 // x.  Only acc[.][0, MTW) is touched.
-template <int MTW, int MT, int NTT, int NMAT, int WV>
+template <int MTW, int MT, int NTT, int NMAT, int WV, bool FOLD>
 __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8_t* stage,
                                                __amdgpu_buffer_rsrc_t xres,
                                                const uint32_t (&xo)[8 * MTW / WV], int wave,
@@ -355,7 +401,6 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
         __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (qmvs_lds_t*)(xs + (wave * AX + j) * 1024),
                                                  16, (int)xo[j], (int)(st * kXStageRow), 0, 0);
   };
-  const bf16x8 ones = as_bf16x8(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
 
   if (s1 <= s0) return;
   issue_x(s0, xs0);
@@ -429,6 +474,8 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
     __builtin_amdgcn_sched_barrier(0);
     load_w(e, stp + 2, e == 0);
     __builtin_amdgcn_sched_barrier(0);
+    float xsel[MTW] = {}, bsel[NMAT][NTT] = {};
+    f32x4 xr[MTW];
 #pragma unroll
     for (int j = 0; j < SU; ++j) {
       bf16x8 A[MTW][2];
@@ -437,11 +484,10 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
         A[mt][0] = xfrag4(*reinterpret_cast<const u32x4*>(xc + mt * 16 * kXStageRow + xa[j][0]));
         A[mt][1] = xfrag4(*reinterpret_cast<const u32x4*>(xc + mt * 16 * kXStageRow + xa[j][1]));
       }
-      f32x4 xsum[MTW];
 #pragma unroll
       for (int mt = 0; mt < MTW; ++mt) {
-        xsum[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mt][0], ones, f32x4{}, 0, 0, 0);
-        xsum[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mt][1], ones, xsum[mt], 0, 0, 0);
+        if constexpr (FOLD) xsel[mt] = qmvs_pick(j, qmvs_xsum(A[mt]), xsel[mt]);
+        else xr[mt] = qmvs_xsum_rows(A[mt]);
       }
 #pragma unroll
       for (int p = 0; p < NMAT; ++p) {
@@ -460,13 +506,24 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
           const float s = (j & 1) ? bf16_hi(sv[p][t][j >> 1]) : bf16_lo(sv[p][t][j >> 1]);
           const float b = (j & 1) ? bf16_hi(bv[p][t][j >> 1]) : bf16_lo(bv[p][t][j >> 1]);
           const float bo = __builtin_fmaf(-128.f, s, b);
+          if constexpr (FOLD) bsel[p][t] = qmvs_pick(j, bo, bsel[p][t]);
 #pragma unroll
           for (int mt = 0; mt < MTW; ++mt)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-              acc[p][mt][t][r] = __builtin_fmaf(s, P[mt][t][r],
-                                                __builtin_fmaf(bo, xsum[mt][r], acc[p][mt][t][r]));
+              acc[p][mt][t][r] = __builtin_fmaf(
+                  s, P[mt][t][r],
+                  FOLD ? acc[p][mt][t][r] : __builtin_fmaf(bo, xr[mt][r], acc[p][mt][t][r]));
         }
+      }
+      if (FOLD && (j & 3) == 3) {
+#pragma unroll
+        for (int p = 0; p < NMAT; ++p)
+#pragma unroll
+          for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+            for (int t = 0; t < NTT; ++t)
+              acc[p][mt][t] = qmvs_bias4(xsel[mt], bsel[p][t], acc[p][mt][t]);
       }
     }
   };

@@ -280,7 +280,7 @@ __global__ __launch_bounds__(kQmvsKS * 64) void qmvs_kernel(QmmArgs a) {
   const uint32_t* const w[1] = {a.w};
   const uint16_t* const sc[1] = {a.scales};
   const uint16_t* const bi[1] = {a.biases};
-  qmvs_slice<MT, NTT, SU, 1>(stage[wave], w, sc, bi, nb, a.N, a.K, xrow, wave * nst / KS,
+  qmvs_slice<MT, NTT, SU, 1, false>(stage[wave], w, sc, bi, nb, a.N, a.K, xrow, wave * nst / KS,
                              (wave + 1) * nst / KS, acc);
 
   if (wave > 0) {
@@ -407,7 +407,7 @@ void qmvw_kernel(QmmArgs a) {
     const uint32_t* const w[1] = {a.w};
     const uint16_t* const sc[1] = {a.scales};
     const uint16_t* const bi[1] = {a.biases};
-    qmvs_walk_xlds<MT, MT, NTT, 1, WV>(xs[0], xs[1], stage[wave], xres, xo, wave, a.M, w, sc, bi,
+    qmvs_walk_xlds<MT, MT, NTT, 1, WV, false>(xs[0], xs[1], stage[wave], xres, xo, wave, a.M, w, sc, bi,
                                        nb, a.N, a.K, s0, s1, acc);
   }
 
