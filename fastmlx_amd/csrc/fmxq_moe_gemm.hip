@@ -674,12 +674,13 @@ hipError_t launch_moe_down_combine(const uint16_t* h, const uint32_t* inds, cons
   // Row tiles of 8 (I = 512) and 4 (I = 2048) columns: more blocks for the
   // one-token grids (configuration 3 at M = 1 11.5 -> 10.5-10.8 us with 8 rows
   // against 16; configuration 4 at M = 1 61.3 -> 58.3-58.9 us with 4 against 8).
-  // From 8 tokens the grid is large, and 32-row tiles load each h row for 4x the
-  // weights (configuration 3 at M = 16: 67.7 -> 64.5-66.3 us per layer; 64 rows
-  // were no better).
+  // From 8 tokens the grid is large, and 16-row tiles load each h row for 2x the
+  // weights (configuration 3 at M = 16, whole layer: 8-row tiles 67.7 us, 32-row
+  // 59.4-59.8 us, 16-row 58.5-58.7 us; 64 rows 60.9-61.2 us, and 32-row tiles of
+  // 8 lanes x 2 chunks per row 59.6 us).
   switch (I) {
     case 512:
-      return T >= 8 ? launch_down_combine_cfg<32, 16, 1>(a, stream)
+      return T >= 8 ? launch_down_combine_cfg<16, 16, 1>(a, stream)
                     : launch_down_combine_cfg<8, 16, 1>(a, stream);
     case 1024: return launch_down_combine_cfg<16, 32, 1>(a, stream);
     case 2048: return launch_down_combine_cfg<4, 64, 1>(a, stream);
