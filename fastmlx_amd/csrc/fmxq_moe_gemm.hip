@@ -674,7 +674,8 @@ hipError_t launch_moe_down_combine(const uint16_t* h, const uint32_t* inds, cons
   // Row tiles of 8 (I = 512) and 4 (I = 2048) columns: more blocks for the
   // one-token grids (configuration 3 at M = 1 11.5 -> 10.5-10.8 us with 8 rows
   // against 16, and 10.2-10.3 against 10.6-10.9 us with 4; configuration 4 at
-  // M = 1 61.3 -> 58.3-58.9 us with 4 against 8, and 4 against 2 below).
+  // M = 1 61.3 -> 58.3-58.9 us with 4 against 8, and 48-50 against 54-57 us with
+  // 4 against 2).
   // From 8 tokens the grid is large, and 16-row tiles load each h row for 2x the
   // weights (configuration 3 at M = 16, whole layer: 8-row tiles 67.7 us, 32-row
   // 59.4-59.8 us, 16-row 58.5-58.7 us; 64 rows 60.9-61.2 us, and 32-row tiles of
