@@ -500,7 +500,7 @@ struct QmvxShape {
 // The fewest K slices (1, 2 or 4) that keep a lane at <= 2 chunks per row (x in
 // registers grows with MM), and more rows per wave for the longest rows, where
 // building x costs the most.  cpl 0 means the shape is not handled here.
-static QmvxShape pick_qmvx_shape(int64_t nch, int64_t N, int mm) {
+static QmvxShape pick_qmvx_shape(int64_t nch, int64_t N, int mm, int bits, int64_t m) {
   QmvxShape sh{4, (int)((nch + 255) / 256), 4, 4};
   if (nch <= 64) sh = {1, 1, 4, 4};
   else if (nch <= 128) sh = {2, 1, 4, 4};
@@ -517,6 +517,17 @@ static QmvxShape pick_qmvx_shape(int64_t nch, int64_t N, int mm) {
   if (mm == 8 && nch > 256 && nch <= 512) {
     sh.ks = 8;
     sh.cpl = 1;
+    sh.waves = 8;
+  }
+  // int8 rows up to 16384 values (twice the chunks of int4 at the same K) at
+  // M = 3 to 5: eight slices of at most two 9-register x chunks per lane and x
+  // row (M = 5, 4096x14336: 36.2 -> 33.4 us against the prefill tile, 1024x16384:
+  // 23.7 -> 13.0 us; at M = 6, 7, 8 the tile stays faster: 35.1 / 36.3 / 36.6
+  // against 36.9 / 40.5 / 48.2 us.  M = 4 against the general GEMV: 4096x14336
+  // 35.5 -> 29.4 us, 14336x14336 108.3 -> 97.2 us; M = 3 30.0 -> 29.5 us).
+  if (bits == 8 && (mm == 4 || (mm == 8 && m <= 5)) && nch > 512 && nch <= 1024) {
+    sh.ks = 8;
+    sh.cpl = 2;
     sh.waves = 8;
   }
   return sh;
@@ -550,12 +561,15 @@ static int qmvx_mm(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
 static bool qmvx_supported(const QmmArgs& a, int bits) {
   if (a.M < 1 || a.M > 8) return false;
   const int64_t nch = a.K / (128 / bits);
-  return pick_qmvx_shape(nch, a.N, qmvx_mm(a.M)).cpl > 0;
+  return pick_qmvx_shape(nch, a.N, qmvx_mm(a.M), bits, a.M).cpl > 0;
 }
 
 template <int BITS, int MM, int MX = MM>
 static hipError_t launch_qmvx_mm(const QmmArgs& a, hipStream_t stream) {
-  const QmvxShape sh = pick_qmvx_shape(a.K / (128 / BITS), a.N, MM);
+  const QmvxShape sh = pick_qmvx_shape(a.K / (128 / BITS), a.N, MM, BITS, a.M);
+  if constexpr (BITS == 8 && (MM == 4 || (MM == 8 && MX <= 5))) {
+    if (sh.ks == 8 && sh.cpl == 2) return launch_qmvx_rpw<BITS, MM, 2, 8, 8, MX>(a, sh.rpw, stream, sh.r);
+  }
   if (sh.ks == 8) return launch_qmvx_rpw<BITS, MM, 1, 8, 8, MX>(a, sh.rpw, stream, sh.r);
   if (sh.ks == 1) return launch_qmvx_rpw<BITS, MM, 1, 1, 4, MX>(a, sh.rpw, stream);
   if (sh.ks == 2) {
