@@ -519,6 +519,14 @@ static QmvxShape pick_qmvx_shape(int64_t nch, int64_t N, int mm, int bits, int64
     sh.cpl = 1;
     sh.waves = 8;
   }
+  // Two x rows, int4 rows of 8193-16384 values: eight slices of one chunk per
+  // lane (4096x14336: 11.1 -> 10.7 us, 14336x14336: 30.3 -> 28.0 us; at four x
+  // rows it lost: 4096x14336 15.0 -> 17.0 us).
+  if (mm == 2 && bits == 4 && nch > 256 && nch <= 512) {
+    sh.ks = 8;
+    sh.cpl = 1;
+    sh.waves = 8;
+  }
   // int8 rows up to 16384 values (twice the chunks of int4 at the same K) at
   // M = 3 to 5: eight slices of at most two 9-register x chunks per lane and x
   // row (M = 5, 4096x14336: 36.2 -> 33.4 us against the prefill tile, 1024x16384:

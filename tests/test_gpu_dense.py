@@ -288,7 +288,7 @@ def test_config2_full_shapes(gpu, oracle, N, K, bits, M):
 LLAMA_SHAPES = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]
 
 
-@pytest.mark.parametrize("M", [1, 4, 8, 16, 32])
+@pytest.mark.parametrize("M", [1, 2, 4, 8, 16, 32])
 @pytest.mark.parametrize("N,K", LLAMA_SHAPES)
 def test_config1_stack_shapes(gpu, oracle, M, N, K):
     """Config 1 at every batch the bench times, through the same dispatch
