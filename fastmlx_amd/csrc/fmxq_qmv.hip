@@ -523,6 +523,11 @@ static QmvxShape pick_qmvx_shape(int64_t nch, int64_t N, int mm, int bits, int64
   // wave (M = 4: 14336x4096 15.5 -> 15.1 us, 4096x4096 6.64 -> 6.27 us,
   // 28672x4096 26.8 -> 23.3 us; M = 3 on 14336x4096 14.9 -> 14.5 us).
   if (mm == 4 && bits == 4 && nch > 64 && nch <= 128 && N > 2048) sh.rpw = 8;
+  // Two x rows on the same rows, outputs past 4096 rows: 8 rows per wave as well
+  // (14336x4096 10.6 -> 10.4 us, 28672x4096 17.3 -> 15.5 us; 4096x4096 lost, 5.04
+  // -> 5.2 us, and 4 rows per wave below 2048 outputs at M = 3, 4 lost: 4.0 ->
+  // 4.5 us on 1024x4096).
+  if (mm == 2 && bits == 4 && nch > 64 && nch <= 128 && N > 4096) sh.rpw = 8;
   // Two x rows, int4 rows of 8193-16384 values: eight slices of one chunk per
   // lane (4096x14336: 11.1 -> 10.7 us, 14336x14336: 30.3 -> 28.0 us; at four x
   // rows it lost: 4096x14336 15.0 -> 17.0 us).
