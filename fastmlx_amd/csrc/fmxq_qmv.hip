@@ -537,12 +537,13 @@ static QmvxShape pick_qmvx_shape(int64_t nch, int64_t N, int mm, int bits, int64
     sh.waves = 8;
   }
   // int8 rows up to 16384 values (twice the chunks of int4 at the same K) at
-  // M = 3 to 5: eight slices of at most two 9-register x chunks per lane and x
-  // row (M = 5, 4096x14336: 36.2 -> 33.4 us against the prefill tile, 1024x16384:
+  // M = 1 to 5: eight slices of at most two 9-register x chunks per lane and x
+  // row (M = 1, 4096x14336: 20.2 -> 15.9 us; M = 2: 22.8 -> 21.0 us, 14336x14336
+  // 73.2 -> 67.5 us; M = 5, 4096x14336: 36.2 -> 33.4 us against the prefill tile, 1024x16384:
   // 23.7 -> 13.0 us; at M = 6, 7, 8 the tile stays faster: 35.1 / 36.3 / 36.6
   // against 36.9 / 40.5 / 48.2 us.  M = 4 against the general GEMV: 4096x14336
   // 35.5 -> 29.4 us, 14336x14336 108.3 -> 97.2 us; M = 3 30.0 -> 29.5 us).
-  if (bits == 8 && (mm == 4 || (mm == 8 && m <= 5)) && nch > 512 && nch <= 1024) {
+  if (bits == 8 && (mm <= 4 || (mm == 8 && m <= 5)) && nch > 512 && nch <= 1024) {
     sh.ks = 8;
     sh.cpl = 2;
     sh.waves = 8;
@@ -584,7 +585,7 @@ static bool qmvx_supported(const QmmArgs& a, int bits) {
 template <int BITS, int MM, int MX = MM>
 static hipError_t launch_qmvx_mm(const QmmArgs& a, hipStream_t stream) {
   const QmvxShape sh = pick_qmvx_shape(a.K / (128 / BITS), a.N, MM, BITS, a.M);
-  if constexpr (BITS == 8 && (MM == 4 || (MM == 8 && MX <= 5))) {
+  if constexpr (BITS == 8 && (MM <= 4 || (MM == 8 && MX <= 5))) {
     if (sh.ks == 8 && sh.cpl == 2) return launch_qmvx_rpw<BITS, MM, 2, 8, 8, MX>(a, sh.rpw, stream, sh.r);
   }
   if (sh.ks == 8) return launch_qmvx_rpw<BITS, MM, 1, 8, 8, MX>(a, sh.rpw, stream, sh.r);

@@ -116,13 +116,13 @@ def test_qmm_mfma_shapes(gpu, oracle, M, bits):
     _qmm_case(gpu, oracle, M, 1024 + 64, 2048, bits, 64, seed=2000 + M + bits)
 
 
-@pytest.mark.parametrize("M", [3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 6, 7, 8])
 @pytest.mark.parametrize("N,K", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (1024, 16384)])
 def test_int8_small_m_shapes(gpu, oracle, M, N, K):
-    """int8 at 3 <= M <= 8: the register GEMV (only M of its 8 x-row slots built)
-    for M <= 6 and up to 4096 output rows, the prefill GEMM's 64-row tile for
-    M = 7, 8 beyond; rows of 14336 and 16384 values take the register GEMV's
-    eight-slice, two-chunk form at M = 3 to 5 and the tile at M = 6 to 8."""
+    """int8 at 1 <= M <= 8: the register GEMV (at M >= 5 only M of its 8 x-row
+    slots built) for M <= 6 and up to 4096 output rows, the prefill GEMM's 64-row
+    tile for M = 7, 8 beyond; rows of 14336 and 16384 values take the register
+    GEMV's eight-slice, two-chunk form at M = 1 to 5 and the tile at M = 6 to 8."""
     _qmm_case(gpu, oracle, M, N, K, 8, 64, seed=14000 + M + N // 1024)
 
 
