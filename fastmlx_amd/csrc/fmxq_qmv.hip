@@ -528,6 +528,11 @@ static QmvxShape pick_qmvx_shape(int64_t nch, int64_t N, int mm, int bits, int64
   // -> 5.2 us, and 4 rows per wave below 2048 outputs at M = 3, 4 lost: 4.0 ->
   // 4.5 us on 1024x4096).
   if (mm == 2 && bits == 4 && nch > 64 && nch <= 128 && N > 4096) sh.rpw = 8;
+  // int8, two or four x rows, rows of 2049-4096 values, outputs past 2048 rows: 8
+  // rows per wave (M = 2, 14336x4096: 15.6 -> 15.2 us; M = 4: 21.0 -> 20.5 us,
+  // 4096x4096 8.37 -> 8.0 us; at M = 1 it did not help, 4096x4096 5.38 -> 5.51 us;
+  // eight K slices there lost 40-70%).
+  if (bits == 8 && (mm == 2 || mm == 4) && nch > 128 && nch <= 256 && N > 2048) sh.rpw = 8;
   // Two x rows, int4 rows of 8193-16384 values: eight slices of one chunk per
   // lane (4096x14336: 11.1 -> 10.7 us, 14336x14336: 30.3 -> 28.0 us; at four x
   // rows it lost: 4096x14336 15.0 -> 17.0 us).
