@@ -541,6 +541,10 @@ static QmvxShape pick_qmvx_shape(int64_t nch, int64_t N, int mm, int bits, int64
     sh.cpl = 1;
     sh.waves = 8;
   }
+  // Three or four x rows on int4 rows of 8193-16384 values with at most 2048
+  // outputs: 4 rows per wave rather than 2 (1024x14336 8.4 -> 6.7 us; with 4096
+  // outputs 4 rather than 8 lost, 15.2 -> 18.2 us, and so did 4 at two x rows).
+  if (mm == 4 && bits == 4 && nch > 256 && nch <= 512 && N <= 2048) sh.rpw = 4;
   // int8 rows up to 16384 values (twice the chunks of int4 at the same K) at
   // M = 1 to 5: eight slices of at most two 9-register x chunks per lane and x
   // row (M = 1, 4096x14336: 20.2 -> 15.9 us; M = 2: 22.8 -> 21.0 us, 14336x14336

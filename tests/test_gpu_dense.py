@@ -104,6 +104,14 @@ def test_qmv_config0_shape(gpu, oracle, M, bits):
     _qmm_case(gpu, oracle, M, 2048, 2048, bits, 64, seed=1000 + M + bits)
 
 
+@pytest.mark.parametrize("M", [2, 3, 4])
+@pytest.mark.parametrize("N", [1024, 4096])
+def test_qmv_long_rows_small_m(gpu, oracle, M, N):
+    """int4 at M = 2-4 on 14336-deep rows: the register GEMV's shapes for narrow
+    (<= 2048) and wide outputs."""
+    _qmm_case(gpu, oracle, M, N, 14336, 4, 64, seed=1100 + M + N)
+
+
 @pytest.mark.parametrize("group", [32, 128])
 def test_qmv_other_groups(gpu, oracle, group):
     _qmm_case(gpu, oracle, 1, 384, 1024, 4, group, seed=31 + group)
