@@ -55,7 +55,7 @@ LLAMA_PROJ = [  # name, N (out), K (in): llama.go:403-428
 GROUP = 64
 PROFILES = os.path.join(ROOT, "profiles")
 ROOF_PMC = os.path.join(PROFILES, "qmv1_down_4096x14336_M1_traffic.md")
-QMM_PMC = os.path.join(PROFILES, "qmm_deq_gemm_14336x4096_M2048_counters.md")
+QMM_PMC = os.path.join(PROFILES, "qmm_wide_14336x4096_M2048_counters.md")
 
 
 def gen_quant(torch, N, K, bits, gen, dev):
@@ -651,6 +651,16 @@ def main():
         qm = extra["c2_4bit_14336x4096_M2048"]
         busy = profile_value(QMM_PMC, "mfma_busy")
         extra["qmm_M2048_mfma_busy_rocprof"] = busy
+        # The qmm headline: the hand-written MFMA kernel that quantized_matmul runs
+        # at M >= 768 (dequantization in registers, no vendor GEMM, no workspace
+        # the size of W); both Config 2 orientations, int4 group 64.
+        qd = extra["c2_4bit_4096x14336_M2048"]
+        extra["qmm_M2048"] = {
+            "kernel": "fmxq::qmm_wide_kernel<4,8,256> (hand-written HIP, bf16 MFMA 32x32x16)",
+            "us": {"14336x4096": qm["us"], "4096x14336": qd["us"]},
+            "TFLOPs": {"14336x4096": qm["TFLOPs"], "4096x14336": qd["TFLOPs"]},
+            "frac_mfma": {"14336x4096": qm["frac_mfma"], "4096x14336": qd["frac_mfma"]},
+            "peak_TFLOPs": 2500.0}
         if not args.no_cpu:
             w, s, b = stack[0]["gate"]
             cpu_points["c2_4bit_14336x4096_M2048"] = cpu_qmm_point(torch, w, s, b, 2048, 4096, 4)

@@ -55,7 +55,7 @@ def build(verbose: bool = True) -> str:
     tmp = LIB + ".tmp"
     rocm_lib = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs,
-           f"-L{rocm_lib}", f"-Wl,-rpath,{rocm_lib}", "-lhipblaslt"]
+           f"-L{rocm_lib}", f"-Wl,-rpath,{rocm_lib}"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")

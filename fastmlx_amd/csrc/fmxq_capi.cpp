@@ -65,10 +65,8 @@ struct SplitWs {
   int64_t ws_floats = 0;
   uint32_t* counters = nullptr;
   int64_t n_counters = 0;
-  float* pf = nullptr;  // prefill K-split partials (overwritten by every call, no zero state)
+  float* pf = nullptr;  // K-split partials (overwritten by every call, no zero state)
   int64_t pf_floats = 0;
-  uint16_t* dq = nullptr;  // dequantized weights of the dequantize-then-GEMM path
-  int64_t dq_elems = 0;
 };
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, SplitWs> g_ws;
@@ -135,32 +133,6 @@ int prefill_workspace(hipStream_t s, int64_t floats, float** out) {
     w.pf_floats = floats;
   }
   *out = w.pf;
-  return FMXQ_OK;
-}
-
-// The bf16 weight workspace of the dequantize-then-GEMM path (no zero state),
-// grown like the prefill partials.
-int deq_workspace(hipStream_t s, int64_t elems, uint16_t** out) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return fail(FMXQ_ERR_DEVICE, "hipGetDevice failed");
-  std::lock_guard<std::mutex> lk(g_ws_mu);
-  SplitWs& w = g_ws[{dev, s}];
-  if (w.dq_elems < elems) {
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(s, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
-      return fail(FMXQ_ERR_INVALID_ARGUMENT,
-                  "quantized_matmul: the dequantized-weight workspace must grow to %lld values "
-                  "during graph capture; run the same shape once outside capture first",
-                  (long long)elems);
-    if (int rc = hip_status(hipStreamSynchronize(s), "dequant workspace: synchronize")) return rc;
-    uint16_t* p = nullptr;
-    if (int rc = hip_status(hipMalloc(&p, elems * sizeof(uint16_t)), "dequant workspace: hipMalloc"))
-      return rc;
-    if (w.dq) g_retired.push_back(w.dq);
-    w.dq = p;
-    w.dq_elems = elems;
-  }
-  *out = w.dq;
   return FMXQ_OK;
 }
 
@@ -322,20 +294,21 @@ int qmm_common(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
     return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: x and w must be 16-byte aligned", op);
   fmxq::QmmArgs a{x, w, scales, biases, bias, y, M, N, K, K, N, group_size, bits};
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // Prefill sizes without a bias: dequantize W once, then the library bf16 GEMM.
-  int deq_rc = FMXQ_ERR_UNSUPPORTED;
-  if (!bias && M >= fmxq::kDeqGemmMinM && N % 8 == 0 && N * K <= fmxq::kDeqGemmMaxElems &&
-      group_size >= 32 && K % 64 == 0) {
-    deq_rc = fmxq::gemm_bf16_plan(M, N, K, K, N, s);
-    if (deq_rc != FMXQ_OK && deq_rc != FMXQ_ERR_UNSUPPORTED) return deq_rc;
-  }
-  if (deq_rc == FMXQ_OK) {
-    uint16_t* wd = nullptr;
-    if (int rc = deq_workspace(s, N * K, &wd)) return rc;
-    if (int rc = hip_status(
-            fmxq::launch_dequant_fused(w, scales, biases, wd, N, K, group_size, bits, s), op))
-      return rc;
-    return fmxq::gemm_bf16_xwt(x, K, wd, y, N, M, N, K, s);
+  // Prefill sizes: the wide GEMM (256 x 256 tiles, weights dequantized in
+  // registers, stream-K over the tiles past the last whole wave of blocks).
+  if (M >= fmxq::kWideMinM && fmxq::qmm_wide_supported(a)) {
+    int cus = 0;
+    if (int rc = device_cus(&cus)) return rc;
+    const fmxq::WidePlan wp = fmxq::qmm_wide_plan(M, N, K, cus);
+    uint32_t* flag = nullptr;
+    if (wp.sk_len > 0) {
+      if (int rc = prefill_workspace(s, wp.ws_floats, &a.ws)) return rc;
+      float* unused = nullptr;
+      if (int rc = split_workspace(s, fmxq::QmmPlan{2, 0, wp.tiles}, &unused, &a.tile_count))
+        return rc;
+      if (int rc = device_flag(s, &flag)) return rc;
+    }
+    return hip_status(fmxq::launch_qmm_wide(a, wp, flag, s), op);
   }
   // 9 <= M <= 64 (int4 group 64): qmvw, x shared through LDS and K split over
   // blocks; at M <= 16 only for wide outputs or long rows, where it beats qmvs.
@@ -543,6 +516,10 @@ int fmxq_device_error(void* stream) {
   if (v == 0) return FMXQ_OK;
   if (int rc = hip_status(hipMemset(flag, 0, sizeof(uint32_t)), "device_error: clear flag"))
     return rc;
+  if (v & 2u)
+    return fail(FMXQ_ERR_DEVICE,
+                "quantized_matmul: a block of the wide GEMM gave up waiting for another "
+                "block's partial sums (outputs of that tile are incomplete)");
   return fail(FMXQ_ERR_INDEX, "gather_qmm: an index was out of range (outputs zeroed)");
 }
 

@@ -134,18 +134,28 @@ struct PrefillPlan {
 };
 PrefillPlan qmm_prefill_plan(const QmmArgs& a, int cus);
 hipError_t launch_qmm_prefill(const QmmArgs& a, hipStream_t stream);
-// Dequantize-then-GEMM for large M (fmxq_capi.cpp): W dequantized once into a
-// per-stream bf16 workspace with the prefill kernel's single rounding
-// (launch_dequant_fused), then a library bf16 GEMM.  Taken for bias-free int4 /
-// int8 products with M >= kDeqGemmMinM and N K <= kDeqGemmMaxElems (the
-// workspace is 2 N K bytes).  At M = 768 the two passes already win on every
-// Llama shape (14336 x 4096 131 -> 111 us, 4096 x 14336 156 -> 123 us); at
-// M = 512 the fused kernel still does (82 against 90, 94 against 110 us).
-constexpr int64_t kDeqGemmMinM = 768;
-constexpr int64_t kDeqGemmMaxElems = int64_t(1) << 26;
-hipError_t launch_dequant_fused(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
-                                uint16_t* out, int64_t N, int64_t K, int group_size, int bits,
-                                hipStream_t stream);
+// Wide GEMM (fmxq_qmm_wide.hip): 256 (or 128) x 256 tiles, weights dequantized in
+// registers, stream-K over the tiles that do not fill a whole wave of blocks.
+// The plan deals `dp` whole tiles to each of `blocks` blocks, then sk_len
+// iterations (64-deep K steps) of the remaining sk_iters; pieces that do not end
+// their tile leave fp32 partials in ws (ws_floats, one bm x 256 slot per block)
+// and bump tile_count (tiles counters, zero between calls; the kernel clears
+// them again).
+constexpr int64_t kWideMinM = 768;
+constexpr int kWideMinPiece = 16;
+struct WidePlan {
+  int bm, tm, nk, dp, sk_len, blocks;
+  int64_t sk_iters, tiles, ws_floats;
+};
+struct WideArgs {
+  QmmArgs q;
+  int tm, nk, dp, sk_len;
+  int64_t sk_iters;
+  uint32_t* err;  // raised (bit 2) when a wait for another block's partial gives up
+};
+WidePlan qmm_wide_plan(int64_t M, int64_t N, int64_t K, int cus);
+bool qmm_wide_supported(const QmmArgs& a);
+hipError_t launch_qmm_wide(const QmmArgs& a, const WidePlan& p, uint32_t* err, hipStream_t stream);
 // Grouped form (QmmArgs::g_*): grid = N tiles x max_tiles work-list entries.
 constexpr int kGroupedTileRows = 128;
 bool qmm_grouped_supported(int64_t N, int64_t K, int64_t x_rows, int bits, int group_size);

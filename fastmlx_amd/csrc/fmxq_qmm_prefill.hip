@@ -505,39 +505,6 @@ TileShape prefill_tile(const QmmArgs& a) {
   return {128, 256};
 }
 
-// dequant_fused_kernel: W [N, K] packed -> [N, K] bf16 with the prefill GEMM's own
-// dequantization (w = bf16(fma(s, q, b)), one rounding: dequant_word4 /
-// dequant_words8), for the dequantize-then-GEMM path at large M.  The work is cut
-// into units of 8 consecutive values (one int4 word, two int8 words), 16 output
-// bytes each; the rows are contiguous, so unit u's group is 8 u >> log2(group)
-// over the whole matrix.  One unit per thread: each load and each 16-byte store
-// instruction of a wave covers one contiguous span.  Measured on 14336 x 4096
-// (4-bit): 27.2 us with one unit per thread against 29.3 / 31.4 / 29.0 / 37.1 us
-// with 2 / 4 / 8 / 16 (64 apart per thread), 27.4-28.2 us for a grid-stride loop
-// that loads the next unit first, and 44 us for 16-byte loads of four units with
-// 64-byte runs of stores per thread.  The same pass without the weight loads
-// takes 19.2 us: the 117 MB of writes alone set most of the time.  (In the
-// full dequantize-then-GEMM call the change measured within noise.)
-template <int BITS>
-__global__ __launch_bounds__(256) void dequant_fused_kernel(const uint32_t* __restrict__ w,
-                                                            const uint16_t* __restrict__ scales,
-                                                            const uint16_t* __restrict__ biases,
-                                                            uint16_t* __restrict__ out,
-                                                            uint32_t units, int gshift) {
-  const uint32_t u = blockIdx.x * 256u + threadIdx.x;
-  if (u >= units) return;
-  uint32_t o[4];
-  const uint32_t g = (u * 8u) >> gshift;
-  const float s = bf16_bits_to_f32(scales[g]), b = bf16_bits_to_f32(biases[g]);
-  if constexpr (BITS == 4) {
-    dequant_word4(w[u], s, b, o);
-  } else {
-    const u32x2 p = reinterpret_cast<const u32x2*>(w)[u];
-    dequant_words8(p[0], p[1], s, b, o);
-  }
-  reinterpret_cast<u32x4*>(out)[u] = u32x4{o[0], o[1], o[2], o[3]};
-}
-
 }  // namespace
 
 PrefillPlan qmm_prefill_plan(const QmmArgs& a, int cus) {
@@ -599,27 +566,6 @@ hipError_t launch_qmm_prefill(const QmmArgs& a, hipStream_t stream) {
   if (a.bits == 8) return launch_tile<8, 256, 128, 4, 2>(a, stream);
   if (ts.bm == 256) return launch_tile<4, 256, 128, 4, 2>(a, stream);
   return launch_tile<4, 128, 256, 2, 4>(a, stream);
-}
-
-hipError_t launch_dequant_fused(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
-                                uint16_t* out, int64_t N, int64_t K, int group_size, int bits,
-                                hipStream_t stream) {
-  const int64_t units = N * K / 8;
-  if (units == 0) return hipSuccess;
-  // Units of 8 values inside one group (group_size >= 8, a power of two), and
-  // unit * 8 below 2^32.
-  if ((bits != 4 && bits != 8) || group_size < 8 || (group_size & (group_size - 1)) ||
-      K % group_size || K % 8 || units * 8 >= (int64_t(1) << 32))
-    return hipErrorInvalidValue;
-  const int gshift = __builtin_ctz((unsigned)group_size);
-  const unsigned blocks = (unsigned)((units + 255) / 256);
-  if (bits == 4)
-    dequant_fused_kernel<4><<<blocks, 256, 0, stream>>>(w, scales, biases, out, (uint32_t)units,
-                                                        gshift);
-  else
-    dequant_fused_kernel<8><<<blocks, 256, 0, stream>>>(w, scales, biases, out, (uint32_t)units,
-                                                        gshift);
-  return hipGetLastError();
 }
 
 }  // namespace fmxq

@@ -256,18 +256,47 @@ def test_qmvw_parts_and_walks(gpu, oracle, M, N, K, bias):
 @pytest.mark.parametrize("M,N,K,bits,group", [
     (768, 1024, 1024, 4, 64),    # the threshold M
     (1024, 1024, 1024, 4, 64),
-    (1500, 4104, 2048, 4, 32),   # ragged M, N not a multiple of the GEMM tiles
-    (1024, 2048, 4096, 4, 128),
-    (1100, 1032, 3072, 8, 64),
+    (1500, 4104, 2048, 4, 32),   # group 32: the prefill GEMM's 64-row tile instead
+    (1024, 2048, 4096, 4, 128),  # group 128: likewise
+    (1100, 1032, 3072, 8, 64),   # ragged M, N not a multiple of the 256-output tile
     (2048, 4096, 1024, 8, 32),
+    (1000, 4096, 14336, 4, 64),  # 128-row tiles, stream-K pieces of 112 steps
+    (2048, 4096, 14336, 8, 64),  # 256-row tiles, two pieces per tile
+    (1300, 14336, 4096, 4, 64),  # whole tiles, then stream-K pieces of uneven length
 ])
-def test_deq_gemm_shapes(gpu, oracle, M, N, K, bits, group):
-    """Bias-free products at M >= 768: W dequantized once with the prefill
-    kernel's single rounding, then the library bf16 GEMM (fp32 accumulation); the
-    per-element bound against the fp64 oracle holds as for the fused kernels."""
+def test_wide_gemm_shapes(gpu, oracle, M, N, K, bits, group):
+    """Bias-free products at M >= 768: the hand-written wide MFMA GEMM (group 64,
+    K a multiple of 256) with its stream-K split of the K range, or the prefill
+    GEMM for the other group sizes; per-element bound against the fp64 oracle."""
     rows = np.unique(np.array([0, 1, M // 3, M // 2, M - 2, M - 1]))
     _qmm_case(gpu, oracle, M, N, K, bits, group, seed=9700 + M + N + K + bits + group,
               rows_checked=rows)
+
+
+@pytest.mark.parametrize("M,N,K,bits", [(1000, 4096, 14336, 4), (2048, 4096, 14336, 8),
+                                        (2048, 14336, 4096, 4)])
+def test_wide_gemm_repeated_calls(gpu, M, N, K, bits):
+    """Six calls in a row on every row and output, against a torch fp32 product of
+    the dequantized weights (fmxq dequantize is bit-exact against the oracle).  A
+    slip in the pipelined waits shows up as a 32-row slab of one step's x read
+    stale in some calls only, so one call is not enough.  Gross-error bound:
+    2e-2 of the rms output plus 1e-2 of the element (bf16 output rounding and fp32
+    order differences stay 5x below it; a stale 64-deep step of x is far above)."""
+    from fastmlx_amd import ops
+
+    announce(f"wide GEMM repeated calls M={M} N={N} K={K} bits={bits}")
+    rng = np.random.default_rng(M + N + bits)
+    w, s, b = make_quant(rng, (N,), K, bits, 64)
+    x = make_x(rng, M, K)
+    dx, dw, ds, db = (to_dev(t, gpu) for t in (x, w, s, b))
+    wd = ops.dequantize(dw, ds, db, 64, bits).view(torch.bfloat16).float()
+    ref = dx.view(torch.bfloat16).float() @ wd.t()
+    rms = float(ref.pow(2).mean().sqrt())
+    bound = 0.02 * rms + 0.01 * ref.abs()
+    for call in range(6):
+        y = ops.quantized_matmul(dx, dw, ds, db, True, 64, bits).view(torch.bfloat16).float()
+        bad = int(((y - ref).abs() > bound).sum())
+        assert bad == 0, f"call {call}: {bad} of {y.numel()} outputs off the fp32 product"
 
 
 def test_qmvs_bias(gpu, oracle):
@@ -349,7 +378,7 @@ def test_graph_replay_matches_eager(gpu):
 
     rng = np.random.default_rng(77)
     # M=1 / 4 GEMVs, qmvs (M=16, narrow), qmvw with K parts and its fixup (M=32),
-    # the prefill GEMM (M=96) and the dequantize-then-GEMM path (M=1024, 2048).
+    # the prefill GEMM (M=96) and the wide GEMM (M=1024, 2048).
     shapes = [(1, 4096, 4096), (4, 1024, 4096), (16, 2048, 2048), (32, 4096, 4096),
               (96, 512, 1024), (1024, 1024, 1024), (2048, 4096, 1024)]
     tensors = []
