@@ -421,7 +421,7 @@ def moe_points(torch, ops, gen, dev, cpu):
 PROBES = {
     # name: (M, N, K, bits) dense products over rotating weight copies
     "qmv_down": (1, 4096, 14336, 4), "qmv_up": (1, 14336, 4096, 4),
-    "qmv_c0": (1, 2048, 2048, 4),
+    "qmv_c0": (1, 2048, 2048, 4), "tied_head": (1, 128256, 4096, 4),
     "qmvx4_up": (4, 14336, 4096, 4), "qmvx8_up": (8, 14336, 4096, 4),
     "skinny16_up": (16, 14336, 4096, 4), "skinny32_up": (32, 14336, 4096, 4),
     "skinny16_down": (16, 4096, 14336, 4), "skinny32_down": (32, 4096, 14336, 4),
@@ -604,6 +604,12 @@ def main():
         c0 = [gen_quant(torch, 2048, 2048, 4, gen, dev) for _ in range(128)]
         extra["c0_qmv_2048x2048_M1"] = dense_point(torch, ops, c0, 1, 2048, 2048, 4, gen, dev)
         del c0
+        # the tied lm_head (llama.go:433-437): qlinear on the 128256 x 4096 embedding
+        # triple, the largest single decode product; two copies (2 x 279 MB) so
+        # every launch streams from HBM
+        head = [gen_quant(torch, 128256, 4096, 4, gen, dev) for _ in range(2)]
+        extra["tied_head_128256x4096_M1"] = dense_point(torch, ops, head, 1, 128256, 4096, 4, gen, dev)
+        del head
         nd = extra["qmv_4096x14336_M1"]
         by_dn = qmm_bytes(1, 4096, 14336, 4, GROUP)
         # The same kernel on taller matrices of the same 14336-deep shape: the

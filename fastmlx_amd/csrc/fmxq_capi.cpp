@@ -70,7 +70,18 @@ struct SplitWs {
 };
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, SplitWs> g_ws;
+
+// Device buffers replaced by larger ones.  A graph captured earlier may still
+// hold them, so they are kept alive (growth is monotonic, at most doubling the
+// footprint) rather than freed.  The list has its own lock: the split-K and the
+// SwitchGLU scratch grow under different locks.
+std::mutex g_retired_mu;
 std::vector<void*> g_retired;
+void retire(void* p) {
+  if (!p) return;
+  std::lock_guard<std::mutex> lk(g_retired_mu);
+  g_retired.push_back(p);
+}
 
 int split_workspace(hipStream_t s, const fmxq::QmmPlan& plan, float** ws, uint32_t** cnt) {
   int dev = 0;
@@ -98,10 +109,8 @@ int split_workspace(hipStream_t s, const fmxq::QmmPlan& plan, float** ws, uint32
     if (int rc = hip_status(hipMemset(nws, 0, nf * sizeof(float)), "split-K workspace: clear")) return rc;
     if (int rc = hip_status(hipMemset(ncnt, 0, nc * sizeof(uint32_t)), "split-K counters: clear"))
       return rc;
-    // A graph captured earlier may still hold the old buffers, so they are kept
-    // alive (growth is monotonic, at most doubling the footprint) rather than freed.
-    if (w.ws) g_retired.push_back(w.ws);
-    if (w.counters) g_retired.push_back(w.counters);
+    retire(w.ws);
+    retire(w.counters);
     w.ws = nws;
     w.ws_floats = nf;
     w.counters = ncnt;
@@ -128,7 +137,7 @@ int prefill_workspace(hipStream_t s, int64_t floats, float** out) {
     float* p = nullptr;
     if (int rc = hip_status(hipMalloc(&p, floats * sizeof(float)), "prefill workspace: hipMalloc"))
       return rc;
-    if (w.pf) g_retired.push_back(w.pf);
+    retire(w.pf);
     w.pf = p;
     w.pf_floats = floats;
   }
@@ -178,7 +187,7 @@ int stream_arena(hipStream_t s, size_t bytes, void** out, const char* op, int sl
                   "once outside capture first", op, bytes);
     void* p = nullptr;
     if (int rc = hip_status(hipMalloc(&p, bytes), "switch_glu scratch: hipMalloc")) return rc;
-    if (a.first) g_retired.push_back(a.first);
+    retire(a.first);
     a = {p, bytes};
   }
   *out = a.first;
@@ -505,17 +514,23 @@ int fmxq_gather_qmm(const uint16_t* x, const uint32_t* w, const uint16_t* scales
 }
 
 int fmxq_device_error(void* stream) {
-  uint32_t* flag = nullptr;
-  if (int rc = device_flag(static_cast<hipStream_t>(stream), &flag)) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  uint32_t* own = nullptr;
+  uint32_t* graph = nullptr;
+  if (int rc = fmxq::device_flags_to_check(s, &own, &graph)) return rc;
   if (int rc = hip_status(hipStreamSynchronize(s), "device_error: synchronize")) return rc;
   uint32_t v = 0;
-  if (int rc = hip_status(hipMemcpy(&v, flag, sizeof(v), hipMemcpyDeviceToHost),
-                          "device_error: read flag"))
-    return rc;
+  for (uint32_t* flag : {own, graph}) {
+    uint32_t w = 0;
+    if (int rc = hip_status(hipMemcpy(&w, flag, sizeof(w), hipMemcpyDeviceToHost),
+                            "device_error: read flag"))
+      return rc;
+    if (w == 0) continue;
+    if (int rc = hip_status(hipMemset(flag, 0, sizeof(uint32_t)), "device_error: clear flag"))
+      return rc;
+    v |= w;
+  }
   if (v == 0) return FMXQ_OK;
-  if (int rc = hip_status(hipMemset(flag, 0, sizeof(uint32_t)), "device_error: clear flag"))
-    return rc;
   if (v & 2u)
     return fail(FMXQ_ERR_DEVICE,
                 "quantized_matmul: a block of the wide GEMM gave up waiting for another "

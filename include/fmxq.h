@@ -241,12 +241,19 @@ int fmxq_route_group_topk(const void* gates, int gates_bf16, const float* bias, 
                           float routed_scaling_factor, bool norm_topk_prob, uint32_t* inds,
                           void* weights, int weights_bf16, void* stream);
 
-/* Synchronizes `stream`, then reports (and clears) the device-side error flag
+/* Synchronizes `stream`, then reports (and clears) the device-side error flags
  * that gather kernels raise on an out-of-range index: returns FMXQ_OK or
- * FMXQ_ERR_INDEX.  The flag is the stream's own (kernels enqueued on `stream`
- * raise it; other streams' flags are neither read nor cleared).  Streams get
- * flag slots in order of first use, 64 per device; beyond 64 streams on one
- * device, slots are shared in turn. */
+ * FMXQ_ERR_INDEX (FMXQ_ERR_DEVICE if a wide-GEMM block gave up waiting).  Two
+ * flags are read:
+ *   - the stream's own, raised by kernels enqueued on `stream` outside graph
+ *     capture (other streams' own flags are neither read nor cleared).  Streams
+ *     get these in order of first use, 63 per device; beyond 63 streams on one
+ *     device they are shared in turn;
+ *   - the device's graph flag, raised by kernels that were captured into a
+ *     graph, wherever the graph is replayed (the replay stream is not known at
+ *     capture).  Every stream's query reads and clears it, so with graphs
+ *     replayed on several streams at once the report names the device, not the
+ *     stream. */
 int fmxq_device_error(void* stream);
 
 #ifdef __cplusplus

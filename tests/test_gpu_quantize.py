@@ -72,6 +72,33 @@ def test_quantize_full_size_and_round_trip(gpu, oracle, bits):
         assert np.array_equal(to_np(deq), oracle.dequantize(rq, rs, rb, 64, bits))
 
 
+def test_quantize_exact_ties_round_half_even(gpu, oracle):
+    """A 4-bit group with min 0 and max 15: delta = 1, the edge is the max, scale
+    = -1 and bias = 15, so q = rint(15 - w) and w = k + 0.5 lands exactly halfway.
+    The kernel (like the oracle) rounds halfway to even -- MLX's op-level
+    quantize rule.  Whether MLX's own device kernels round halfway away from zero
+    instead is not settled by anything in the reference (no quantize fixture), so
+    this rule is documented here, not pinned: w = 2.5 gives q = 12 (half-away
+    would give 13), w = 0.5 gives 14 (15), w = 1.5 gives 14 either way."""
+    from fastmlx_amd import ops
+    from synth import unpack
+
+    K = 64
+    w = np.full(K, 7.0, np.float32)
+    w[0], w[1] = 0.0, 15.0
+    w[2:8] = [0.5, 1.5, 2.5, 3.5, 12.5, 13.5]
+    w16 = oracle.f32_to_bf16(w[None, :])
+    announce("quantize exact halfway quotients")
+    wq, s, b = ops.quantize(to_dev(w16, gpu), 64, 4)
+    torch.cuda.synchronize()
+    assert oracle.bf16_to_f32(to_np(s))[0, 0] == -1.0
+    assert oracle.bf16_to_f32(to_np(b))[0, 0] == 15.0
+    q = unpack(to_np(wq, np.uint32), 4)[0]
+    half_even = [15, 0, 14, 14, 12, 12, 2, 2]
+    assert list(q[:8]) == half_even, list(q[:8])
+    assert np.array_equal(to_np(wq, np.uint32), oracle.quantize(w16, 64, 4)[0])
+
+
 def test_array_ops_match_numpy(gpu):
     """reshape / split / swapaxes / contiguous against numpy on several dtypes,
     including non-adjacent axes, negative axes and empty split parts."""

@@ -83,3 +83,41 @@ def test_noalloc_refuses_oversized_scratch(gpu):
     assert "scratch" in msg and "allocation-free" in msg, msg
     torch.cuda.synchronize()
     _case(gpu, lib, 4, E=16, T=4, k=4, D=256, I=512)
+
+
+def test_noalloc_first_call_inside_graph_capture(gpu):
+    """The allocation-free entry point's very first call on a fresh stream, made
+    inside graph capture: every allocating path (the per-stream scratch, the
+    workspaces) refuses to grow while a stream is captured, so a capture that
+    succeeds and replays to fmxq_switch_glu's output bit for bit shows that the
+    fixed buffer served the call.  Replayed twice, with an eager call of another
+    size in between."""
+    from fastmlx_amd import _lib
+
+    lib = _lib.load()
+    rng = np.random.default_rng(21)
+    E, T, k, D, I = 64, 6, 4, 512, 512
+    q = lambda n, kk: tuple(to_dev(t, gpu) for t in make_quant(rng, (E, n), kk))
+    gate, up, down = q(I, D), q(I, D), q(D, I)
+    x = to_dev(make_x(rng, T, D), gpu)
+    inds = to_dev(topk_uniform(rng, T, E, k).astype(np.uint32), gpu)
+    yg = torch.zeros(T, k, D, dtype=torch.bfloat16, device=gpu)
+    ya = torch.empty(T, k, D, dtype=torch.bfloat16, device=gpu)
+    fresh = torch.cuda.Stream()
+    fresh.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    announce("switch_glu_noalloc first call inside graph capture")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=fresh):
+        rc = _call(lib, "fmxq_switch_glu_noalloc", x, inds, gate, up, down, yg, T, k, E, D, I, 4,
+                   ctypes.c_void_p(fresh.cuda_stream))
+    assert rc == 0, lib.fmxq_last_error()
+    assert _call(lib, "fmxq_switch_glu", x, inds, gate, up, down, ya, T, k, E, D, I, 4) == 0
+    torch.cuda.synchronize()
+    want = to_np(ya)
+    for rep in range(2):
+        yg.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(to_np(yg), want), f"replay {rep} differs from fmxq_switch_glu"
+        _case(gpu, lib, 30 + rep, E=16, T=3, k=2, D=256, I=256)  # other contents in the buffer
