@@ -24,55 +24,21 @@
 
 #include "../../include/fmx.h"
 #include "../../include/fmxq.h"
+#include "fmx_shape.hpp"
 #include "fmxq_host.hpp"
 #include "fmxq_internal.hpp"
 
 using fmxq::check_quant;
 using fmxq::fail;
 using fmxq::hip_status;
+using fmx_shape::dtype_name;
+using fmx_shape::dtype_size;
+using fmx_shape::is_index_dtype;
+using fmx_shape::is_signed_dtype;
+using fmx_shape::prod;
+using fmx_shape::shape_str;
 
 namespace {
-
-size_t dtype_size(int d) {
-  switch (d) {
-    case FMX_BOOL: case FMX_UINT8: case FMX_INT8: return 1;
-    case FMX_UINT16: case FMX_INT16: case FMX_FLOAT16: case FMX_BFLOAT16: return 2;
-    case FMX_UINT32: case FMX_INT32: case FMX_FLOAT32: return 4;
-    case FMX_UINT64: case FMX_INT64: case FMX_COMPLEX64: case FMX_FLOAT64: return 8;
-    default: return 0;
-  }
-}
-
-bool is_index_dtype(int d) {
-  return d == FMX_UINT8 || d == FMX_UINT16 || d == FMX_UINT32 || d == FMX_UINT64 ||
-         d == FMX_INT8 || d == FMX_INT16 || d == FMX_INT32 || d == FMX_INT64;
-}
-
-bool is_signed_dtype(int d) {
-  return d == FMX_INT8 || d == FMX_INT16 || d == FMX_INT32 || d == FMX_INT64;
-}
-
-const char* dtype_name(int d) {
-  static const char* names[] = {"bool",    "uint8",   "uint16",   "uint32", "uint64",
-                                "int8",    "int16",   "int32",    "int64",  "float16",
-                                "float32", "bfloat16", "complex64", "float64"};
-  return (d >= 0 && d <= FMX_FLOAT64) ? names[d] : "invalid";
-}
-
-std::string shape_str(const std::vector<int64_t>& s) {
-  std::string r = "[";
-  for (size_t i = 0; i < s.size(); ++i) {
-    if (i) r += " ";
-    r += std::to_string(s[i]);
-  }
-  return r + "]";
-}
-
-int64_t prod(const std::vector<int64_t>& s, size_t from = 0, size_t to = SIZE_MAX) {
-  int64_t p = 1;
-  for (size_t i = from; i < std::min(to, s.size()); ++i) p *= s[i];
-  return p;
-}
 
 struct Stream {
   hipStream_t s = nullptr;
@@ -100,44 +66,19 @@ Array* arr(const fmx_array a) { return static_cast<Array*>(a.ctx); }
 
 // ---- device buffer cache ----
 
-std::mutex g_pool_mu;
-std::map<std::pair<int, hipStream_t>, std::multimap<size_t, void*>> g_pool;
-
-size_t round_bytes(size_t n) {
-  if (n <= 512) return 512;
-  if (n <= ((size_t)1 << 20)) return (n + 511) & ~(size_t)511;
-  size_t p = (size_t)1 << 20;
-  while (p * 2 <= n) p *= 2;
-  const size_t step = p / 8;  // at most 12.5% slack above 1 MiB
-  return (n + step - 1) / step * step;
-}
+fmx_shape::BufferCache g_cache;
 
 int pool_alloc(int dev, hipStream_t s, size_t n, void** out, size_t* cap) {
-  const size_t want = round_bytes(n);
-  {
-    std::lock_guard<std::mutex> lk(g_pool_mu);
-    auto& fl = g_pool[{dev, s}];
-    auto it = fl.find(want);
-    if (it != fl.end()) {
-      *out = it->second;
-      *cap = want;
-      fl.erase(it);
-      return FMXQ_OK;
-    }
+  const size_t want = fmx_shape::round_bytes(n);
+  if (g_cache.take(dev, s, want, out)) {
+    *cap = want;
+    return FMXQ_OK;
   }
   void* p = nullptr;
   hipError_t e = hipMalloc(&p, want);
   if (e != hipSuccess) {
     // Give cached buffers back to the device and try once more.
-    std::vector<void*> drop;
-    {
-      std::lock_guard<std::mutex> lk(g_pool_mu);
-      for (auto& kv : g_pool)
-        if (kv.first.first == dev)
-          for (auto& b : kv.second) drop.push_back(b.second);
-      for (auto& kv : g_pool)
-        if (kv.first.first == dev) kv.second.clear();
-    }
+    const std::vector<void*> drop = g_cache.drain(dev);
     if (!drop.empty()) {
       (void)hipDeviceSynchronize();
       for (void* b : drop) (void)hipFree(b);
@@ -165,8 +106,7 @@ int fence(hipStream_t waiter, hipStream_t signaller) {
 void release_storage(Array* a) {
   if (a->storage == Storage::kPooled && a->data) {
     for (hipStream_t r : a->readers) (void)fence(a->stream, r);
-    std::lock_guard<std::mutex> lk(g_pool_mu);
-    g_pool[{a->device, a->stream}].emplace(a->cap, a->data);
+    g_cache.put(a->device, a->stream, a->cap, a->data);
   } else if (a->storage == Storage::kMalloc && a->data) {
     (void)hipFree(a->data);
   }
@@ -236,13 +176,8 @@ int need_shape(const Array* a, const std::vector<int64_t>& want, const char* op,
   return FMXQ_OK;
 }
 
-// Packed width -> K for a valid bits value (bits is checked first).
 int unpacked_k(const Array* w, int bits, const char* op, int64_t* K) {
-  if (bits != 4 && bits != 8)
-    return fail(FMXQ_ERR_UNSUPPORTED, "%s: bits=%d not supported (4 or 8)", op, bits);
-  if (w->shape.empty()) return fail(FMXQ_ERR_SHAPE, "%s: w must have at least one axis", op);
-  *K = w->shape.back() * (32 / bits);
-  return FMXQ_OK;
+  return fmx_shape::unpacked_k(w->shape, bits, op, K);
 }
 
 // Everything an op needs once validation has passed.
@@ -282,8 +217,7 @@ void finish(Launch& L) {
     if (a->storage == Storage::kPooled && a->stream != L.s &&
         std::find(a->readers.begin(), a->readers.end(), L.s) == a->readers.end())
       a->readers.push_back(L.s);
-  std::lock_guard<std::mutex> lk(g_pool_mu);
-  for (auto& t : L.temps) g_pool[{L.dev, L.s}].emplace(t.second, t.first);
+  for (auto& t : L.temps) g_cache.put(L.dev, L.s, t.second, t.first);
   L.temps.clear();
 }
 
@@ -329,27 +263,22 @@ int index_vector(Launch& L, const Array* src, const std::vector<int64_t>& arange
                  const std::vector<int64_t>& bshape, const uint32_t** out) {
   const int64_t n = prod(bshape);
   const std::vector<int64_t>& sshape = src ? src->shape : arange_shape;
-  const size_t nd = bshape.size();
   // Already flat and of the right width: use in place.
-  if (src && (src->dtype == FMX_UINT32 || src->dtype == FMX_INT32) && sshape.size() <= nd &&
-      prod(sshape) == n) {
+  if (src && (src->dtype == FMX_UINT32 || src->dtype == FMX_INT32) &&
+      fmx_shape::same_elements(sshape, bshape)) {
     *out = static_cast<const uint32_t*>(src->data);
     return FMXQ_OK;
   }
-  if (nd > (size_t)fmxq::kMaxIndexDims)
-    return fail(FMXQ_ERR_UNSUPPORTED, "gather_qmm: index batch has %zu axes (max %d)", nd,
-                fmxq::kMaxIndexDims);
+  fmx_shape::BroadcastMap bm;
+  if (int rc = fmx_shape::broadcast_map(sshape, bshape, &bm, "gather_qmm")) return rc;
+  static_assert(fmx_shape::kMaxIndexDims == fmxq::kMaxIndexDims, "index axes");
   fmxq::IndexMap m{};
-  m.ndim = (int)nd;
+  m.ndim = bm.ndim;
   m.elem_bytes = src ? (int)dtype_size(src->dtype) : 4;
   m.is_signed = src ? is_signed_dtype(src->dtype) : false;
-  const size_t pad = nd - sshape.size();
-  int64_t stride = 1;
-  for (int d = (int)nd - 1; d >= 0; --d) {
-    m.shape[d] = bshape[d];
-    const int64_t sd = d >= (int)pad ? sshape[d - pad] : 1;
-    m.stride[d] = (sd == 1) ? 0 : stride;
-    stride *= sd;
+  for (int d = 0; d < bm.ndim; ++d) {
+    m.shape[d] = bm.shape[d];
+    m.stride[d] = bm.stride[d];
   }
   void* buf = nullptr;
   if (int rc = temp(L, (size_t)n * sizeof(uint32_t), &buf)) return rc;
@@ -358,21 +287,6 @@ int index_vector(Launch& L, const Array* src, const std::vector<int64_t>& arange
                           "gather_qmm: index broadcast"))
     return rc;
   *out = static_cast<const uint32_t*>(buf);
-  return FMXQ_OK;
-}
-
-int broadcast_shapes(const std::vector<int64_t>& a, const std::vector<int64_t>& b,
-                     std::vector<int64_t>* out) {
-  const size_t n = std::max(a.size(), b.size());
-  out->assign(n, 1);
-  for (size_t i = 0; i < n; ++i) {
-    const int64_t da = i < n - a.size() ? 1 : a[i - (n - a.size())];
-    const int64_t db = i < n - b.size() ? 1 : b[i - (n - b.size())];
-    if (da != db && da != 1 && db != 1)
-      return fail(FMXQ_ERR_SHAPE, "gather_qmm: index shapes %s and %s do not broadcast",
-                  shape_str(a).c_str(), shape_str(b).c_str());
-    (*out)[i] = da == 1 ? db : da;
-  }
   return FMXQ_OK;
 }
 
@@ -423,14 +337,7 @@ fmx_array make_handle(std::vector<int64_t> shape, fmx_dtype dtype) {
 }
 
 int read_shape(const int* shape, int dim, std::vector<int64_t>* out, const char* op) {
-  if (dim < 0 || (dim > 0 && !shape))
-    return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: bad shape pointer/rank", op);
-  out->clear();
-  for (int i = 0; i < dim; ++i) {
-    if (shape[i] < 0) return fail(FMXQ_ERR_SHAPE, "%s: negative dimension %d", op, shape[i]);
-    out->push_back(shape[i]);
-  }
-  return FMXQ_OK;
+  return fmx_shape::read_shape(shape, dim, out, op);
 }
 
 int qmm_op(fmx_array* res, const fmx_array x, const fmx_array w, const fmx_array scales,
@@ -449,25 +356,15 @@ int qmm_op(fmx_array* res, const fmx_array x, const fmx_array w, const fmx_array
   if (int rc = need_dtype(B, FMX_BFLOAT16, op, "biases")) return rc;
   if (Bias)
     if (int rc = need_dtype(Bias, FMX_BFLOAT16, op, "bias")) return rc;
-  if (X->shape.empty()) return fail(FMXQ_ERR_SHAPE, "%s: x must have at least one axis", op);
-  if (W->shape.size() != 2)
-    return fail(FMXQ_ERR_UNSUPPORTED, "%s: w must be [N, K*bits/32] (got %s)", op,
-                shape_str(W->shape).c_str());
-  int64_t K = 0;
-  if (int rc = unpacked_k(W, bits, op, &K)) return rc;
-  if (int rc = check_quant(group_size, bits, K, transpose, op)) return rc;
-  if (X->shape.back() != K)
-    return fail(FMXQ_ERR_SHAPE, "%s: x has K=%lld but w packs K=%lld", op,
-                (long long)X->shape.back(), (long long)K);
-  const int64_t N = W->shape[0];
-  const std::vector<int64_t> sshape{N, K / group_size};
-  if (int rc = need_shape(S, sshape, op, "scales")) return rc;
-  if (int rc = need_shape(B, sshape, op, "biases")) return rc;
+  fmx_shape::QmmGeom g;
+  if (int rc = fmx_shape::qmm_geom(X->shape, W->shape, transpose, group_size, bits, &g, op))
+    return rc;
+  const int64_t K = g.K, N = g.N, M = g.M;
+  if (int rc = need_shape(S, g.sshape, op, "scales")) return rc;
+  if (int rc = need_shape(B, g.sshape, op, "biases")) return rc;
   if (Bias)
     if (int rc = need_shape(Bias, {N}, op, "bias")) return rc;
-  std::vector<int64_t> oshape(X->shape.begin(), X->shape.end() - 1);
-  oshape.push_back(N);
-  const int64_t M = prod(X->shape, 0, X->shape.size() - 1);
+  const std::vector<int64_t>& oshape = g.oshape;
 
   Launch L;
   if (int rc = begin(L, s, {X, W, S, B, Bias})) return rc;
@@ -838,46 +735,17 @@ int fmx_gather_qmm(fmx_array* res, const fmx_array x, const fmx_array w,
   if (Ri && !is_index_dtype(Ri->dtype))
     return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: rhs_indices must be integral (got %s)", op,
                 dtype_name(Ri->dtype));
-  if (X->shape.size() < 2) return fail(FMXQ_ERR_SHAPE, "%s: x must be [..., M, K]", op);
-  if (W->shape.size() < 2) return fail(FMXQ_ERR_SHAPE, "%s: w must be [..., N, K*bits/32]", op);
-  int64_t K = 0;
-  if (int rc = unpacked_k(W, bits, op, &K)) return rc;
-  if (int rc = check_quant(group_size, bits, K, transpose, op)) return rc;
-  if (X->shape.back() != K)
-    return fail(FMXQ_ERR_SHAPE, "%s: x has K=%lld but w packs K=%lld", op,
-                (long long)X->shape.back(), (long long)K);
-  const size_t xnd = X->shape.size(), wnd = W->shape.size();
-  const int64_t Mx = X->shape[xnd - 2];
-  const int64_t N = W->shape[wnd - 2];
-  const std::vector<int64_t> xb(X->shape.begin(), X->shape.end() - 2);
-  const std::vector<int64_t> wb(W->shape.begin(), W->shape.end() - 2);
-  std::vector<int64_t> sshape = wb;
-  sshape.push_back(N);
-  sshape.push_back(K / group_size);
-  if (int rc = need_shape(S, sshape, op, "scales")) return rc;
-  if (int rc = need_shape(B, sshape, op, "biases")) return rc;
-  const std::vector<int64_t>& lb = Li ? Li->shape : xb;
-  const std::vector<int64_t>& rb = Ri ? Ri->shape : wb;
-  std::vector<int64_t> bshape;
-  if (int rc = broadcast_shapes(lb, rb, &bshape)) return rc;
-  const int64_t batch = prod(bshape), x_batch = prod(xb), E = prod(wb);
-  std::vector<int64_t> oshape = bshape;
-  oshape.push_back(Mx);
-  oshape.push_back(N);
-
-  // Implicit lhs: item i reads x item i / lhs_div when x's batch axes are the
-  // leading axes of the output batch (the expand_dims choreography of
-  // switchGLUCore, switch_glu.go:111-118); any other layout is materialized.
-  int64_t lhs_div = 0;
-  if (!Li) {
-    const size_t nd = bshape.size(), pad = nd - xb.size();
-    size_t j = 0;
-    while (j < nd && (j >= pad ? xb[j - pad] : 1) == bshape[j]) ++j;
-    bool flat = true;
-    for (size_t d = j; d < nd; ++d)
-      if ((d >= pad ? xb[d - pad] : 1) != 1) flat = false;
-    if (flat) lhs_div = std::max<int64_t>(prod(bshape, j), 1);
-  }
+  fmx_shape::GatherGeom g;
+  if (int rc = fmx_shape::gather_geom(X->shape, W->shape, &S->shape, &B->shape,
+                                      Li ? &Li->shape : nullptr, Ri ? &Ri->shape : nullptr,
+                                      transpose, group_size, bits, &g))
+    return rc;
+  const int64_t K = g.K, Mx = g.Mx, N = g.N, batch = g.batch, x_batch = g.x_batch, E = g.E;
+  const int64_t lhs_div = g.lhs_div;
+  const std::vector<int64_t>& xb = g.xb;
+  const std::vector<int64_t>& wb = g.wb;
+  const std::vector<int64_t>& bshape = g.bshape;
+  const std::vector<int64_t>& oshape = g.oshape;
 
   Launch L;
   if (int rc = begin(L, s, {X, W, S, B, Li, Ri})) return rc;
@@ -924,6 +792,7 @@ int fmx_dequantize(fmx_array* res, const fmx_array w, const fmx_array scales,
   if (int rc = need_shape(B, sshape, op, "biases")) return rc;
   std::vector<int64_t> oshape(W->shape.begin(), W->shape.end() - 1);
   oshape.push_back(K);
+  if (int rc = fmx_shape::check_elements(oshape, op)) return rc;
   const int64_t rows = prod(W->shape, 0, W->shape.size() - 1);
 
   Launch L;
@@ -965,6 +834,7 @@ int fmx_dequantize_rows(fmx_array* res, const fmx_array w, const fmx_array scale
   if (int rc = need_shape(B, sshape, op, "biases")) return rc;
   std::vector<int64_t> oshape = I->shape;
   oshape.push_back(K);
+  if (int rc = fmx_shape::check_elements(oshape, op)) return rc;
   const int64_t n = I->numel();
 
   Launch L;
@@ -1159,14 +1029,6 @@ int fmx_scale_neg8(fmx_array* res, const fmx_array scale, const fmx_stream s) {
 // copy; the values are the same as MLX's.
 
 namespace {
-int norm_axis(int axis, size_t ndim, const char* op, int* out) {
-  const int n = (int)ndim;
-  if (axis < -n || axis >= n)
-    return fail(FMXQ_ERR_SHAPE, "%s: axis %d out of range for %d dimensions", op, axis, n);
-  *out = axis < 0 ? axis + n : axis;
-  return FMXQ_OK;
-}
-
 int copy_op(fmx_array* res, Array* A, std::vector<int64_t> shape, const fmx_stream s,
             const char* op) {
   Launch L;
@@ -1237,30 +1099,8 @@ int fmx_reshape(fmx_array* res, const fmx_array a, const int* shape, size_t ndim
   if (ndim && !shape) return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: null shape", op);
   Array* A;
   if (int rc = need(a, op, "a", &A)) return rc;
-  std::vector<int64_t> out(ndim);
-  int infer = -1;
-  int64_t known = 1;
-  for (size_t i = 0; i < ndim; ++i) {
-    if (shape[i] == -1) {
-      if (infer >= 0) return fail(FMXQ_ERR_SHAPE, "%s: more than one -1 in the shape", op);
-      infer = (int)i;
-    } else if (shape[i] < 0) {
-      return fail(FMXQ_ERR_SHAPE, "%s: negative size %d", op, shape[i]);
-    } else {
-      out[i] = shape[i];
-      known *= shape[i];
-    }
-  }
-  const int64_t n = A->numel();
-  if (infer >= 0) {
-    if (known == 0 || n % known)
-      return fail(FMXQ_ERR_SHAPE, "%s: cannot infer -1 reshaping %s", op,
-                  shape_str(A->shape).c_str());
-    out[infer] = n / known;
-  } else if (known != n) {
-    return fail(FMXQ_ERR_SHAPE, "%s: %s has %lld elements, the new shape %lld", op,
-                shape_str(A->shape).c_str(), (long long)n, (long long)known);
-  }
+  std::vector<int64_t> out;
+  if (int rc = fmx_shape::reshape(A->shape, shape, ndim, &out, op)) return rc;
   return copy_op(res, A, std::move(out), s, op);
 }
 
@@ -1277,19 +1117,13 @@ int fmx_split(fmx_array* res, size_t n_res, const fmx_array a, const int* indice
                 op, n_res, num_indices, num_indices + 1);
   Array* A;
   if (int rc = need(a, op, "a", &A)) return rc;
-  int ax = 0;
-  if (int rc = norm_axis(axis, A->shape.size(), op, &ax)) return rc;
+  fmx_shape::SplitPlan sp;
+  if (int rc = fmx_shape::split(A->shape, indices, num_indices, axis, &sp, op)) return rc;
+  const int ax = sp.axis;
   const int64_t dim = A->shape[ax];
-  std::vector<int64_t> cut{0};
-  for (size_t i = 0; i < num_indices; ++i) {
-    if (indices[i] < cut.back() || indices[i] > dim)
-      return fail(FMXQ_ERR_SHAPE, "%s: index %d out of order or beyond axis size %lld", op,
-                  indices[i], (long long)dim);
-    cut.push_back(indices[i]);
-  }
-  cut.push_back(dim);
-  const int64_t outer = prod(A->shape, 0, ax);
-  const size_t inner = (size_t)prod(A->shape, ax + 1) * dtype_size(A->dtype);
+  const std::vector<int64_t>& cut = sp.cut;
+  const int64_t outer = sp.outer;
+  const size_t inner = (size_t)sp.inner * dtype_size(A->dtype);
   Launch L;
   if (int rc = begin(L, s, {A})) return rc;
   std::vector<Array*> parts(n_res, nullptr);
@@ -1319,12 +1153,10 @@ int fmx_swapaxes(fmx_array* res, const fmx_array a, int axis1, int axis2, const 
   if (!res) return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: null result", op);
   Array* A;
   if (int rc = need(a, op, "a", &A)) return rc;
-  int a1 = 0, a2 = 0;
-  if (int rc = norm_axis(axis1, A->shape.size(), op, &a1)) return rc;
-  if (int rc = norm_axis(axis2, A->shape.size(), op, &a2)) return rc;
-  if (a1 > a2) std::swap(a1, a2);
-  std::vector<int64_t> shape = A->shape;
-  std::swap(shape[a1], shape[a2]);
+  fmx_shape::SwapPlan sw;
+  if (int rc = fmx_shape::swapaxes(A->shape, axis1, axis2, &sw, op)) return rc;
+  const int a1 = sw.a1, a2 = sw.a2;
+  const std::vector<int64_t>& shape = sw.shape;
   if (a1 == a2) return copy_op(res, A, shape, s, op);
   const size_t es = dtype_size(A->dtype);
   if (es != 1 && es != 2 && es != 4 && es != 8)
@@ -1334,8 +1166,7 @@ int fmx_swapaxes(fmx_array* res, const fmx_array a, int axis1, int axis2, const 
   Array* r = nullptr;
   if (int rc = new_result(L, shape, A->dtype, &r)) return rc;
   int rc = hip_status(
-      fmxq::launch_swap_axes(A->data, r->data, prod(A->shape, 0, a1), A->shape[a1],
-                             prod(A->shape, a1 + 1, a2), A->shape[a2], prod(A->shape, a2 + 1),
+      fmxq::launch_swap_axes(A->data, r->data, sw.outer, sw.d1, sw.mid, sw.d2, sw.inner,
                              (int)es, L.s),
       op);
   finish(L);

@@ -30,20 +30,6 @@ int hip_status(hipError_t e, const char* what) {
   return fail(FMXQ_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
 }
 
-int check_quant(int group_size, int bits, int64_t K, bool transpose, const char* op) {
-  if (!transpose)
-    return fail(FMXQ_ERR_UNSUPPORTED, "%s: transpose=false is not supported (the reference "
-                "always passes true)", op);
-  if (bits != 4 && bits != 8)
-    return fail(FMXQ_ERR_UNSUPPORTED, "%s: bits=%d not supported (4 or 8)", op, bits);
-  if (group_size != 32 && group_size != 64 && group_size != 128)
-    return fail(FMXQ_ERR_UNSUPPORTED, "%s: group_size=%d not supported (32, 64 or 128)", op,
-                group_size);
-  if (K <= 0 || K % group_size != 0)
-    return fail(FMXQ_ERR_SHAPE, "%s: K=%lld must be a positive multiple of group_size=%d", op,
-                (long long)K, group_size);
-  return FMXQ_OK;
-}
 
 }  // namespace fmxq
 
