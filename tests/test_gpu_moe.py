@@ -666,6 +666,103 @@ def test_switch_glu_combine_few_slots_shapes(gpu, oracle, I, gated, E, T, k):
                          what=f"switch_glu_combine I={I}")
 
 
+# --- the one-token layer (gate/up, then down with the combine) ---
+
+def _combine_ref_check(oracle, got, x, inds, gate, up, down, wts, E, sh=None, sg=None,
+                       what="one-token layer"):
+    """got [1, D] against the oracle's routed experts (bad ids contribute zero) plus
+    an optional precomputed shared row sh (gated by sigmoid(sg))."""
+    safe = np.where(inds >= E, 0, inds)
+    sref = parity.SwitchRef(x, safe, gate, up, down, fused=False)
+    near = sref.refs[0].copy()
+    allow = parity.switch_bound(near, near, sref.hscale)
+    bad = inds >= E
+    near[bad] = 0.0
+    allow[bad] = 0.0
+    shared = None
+    if sh is not None:
+        shv = oracle.bf16_to_f32(sh).astype(np.float64)
+        if sg is not None:
+            r16 = lambda v: oracle.bf16_to_f32(oracle.f32_to_bf16(np.asarray(v, np.float32))).astype(np.float64)
+            gt = r16(1 / (1 + np.exp(-oracle.bf16_to_f32(sg).astype(np.float64))))
+            shv = r16(gt[:, None] * shv)
+        shared = (shv, 2.0 ** -8 * np.abs(shv))
+    parity.combine_check(got, near, allow, wts, shared=shared, what=what)
+
+
+@pytest.mark.parametrize("I,D,E,k,gated,bad", [
+    (512, 512, 9, 6, True, True),        # shallow rows: the segment walk
+    (1024, 1024, 9, 6, False, False),    # 32 lanes per down row
+    (2048, 4096, 12, 8, True, True),     # two chunks per lane on the gate/up rows
+    (4096, 2048, 9, 6, False, True),     # two chunks per lane on the down rows
+    (512, 7168, 20, 16, True, False),    # 16 slots, the most the unsorted path takes
+    (512, 10240, 16, 16, False, True),   # every expert hit
+])
+def test_switch_glu_combine_one_token(gpu, oracle, I, D, E, k, gated, bad):
+    """One token: the few-slot gate/up GEMV, then the down projection fused with the
+    weighted top-k sum, at hidden sizes from 512 to 10240 (one to five chunks a lane
+    on the gate/up rows), every down layout (16, 32 and 64 lanes per row, one or two
+    chunks per lane), up to 16 slots, a gated or plain shared row and a bad expert
+    id (its slot contributes zero, the flag is raised)."""
+    from fastmlx_amd import FmxqError, ops
+
+    rng = np.random.default_rng(I + D + E + k)
+    gate, up, down = _stack(rng, E, D, I)
+    x = make_x(rng, 1, D)
+    inds = topk_uniform(rng, 1, E, k)
+    if bad:
+        inds[0, k // 2] = E + 5
+    wts = oracle.f32_to_bf16(rng.dirichlet(np.ones(k), size=1).astype(np.float32))
+    sh = make_x(rng, 1, D)
+    sg = make_x(rng, 1) if gated else None
+    dev = lambda t: to_dev(t, gpu)
+    announce(f"switch_glu_combine one token I={I} D={D} E={E} k={k} bad={bad}")
+    out = ops.switch_glu_combine(dev(x), dev(inds.astype(np.uint32)), tuple(map(dev, gate)),
+                                 tuple(map(dev, up)), tuple(map(dev, down)), dev(wts), dev(sh),
+                                 None if sg is None else dev(sg))
+    torch.cuda.synchronize()
+    got = to_np(out)
+    if bad:
+        with pytest.raises(FmxqError):
+            ops.device_error()
+    else:
+        ops.device_error()
+    _combine_ref_check(oracle, got, x, inds, gate, up, down, wts, E, sh, sg,
+                       what=f"one token I={I} D={D}")
+
+
+def test_one_token_layer_back_to_back(gpu, oracle):
+    """One-token layers in a row on one stream, with different slot counts and
+    experts and no synchronization between them: each call's down/combine kernel
+    must read its own call's h rows from the stream's scratch.  Every output is
+    checked, and a second round of the same calls gives the same bits."""
+    from fastmlx_amd import ops
+
+    rng = np.random.default_rng(4242)
+    E, D, I = 24, 2048, 512
+    gate, up, down = _stack(rng, E, D, I)
+    dev = lambda t: to_dev(t, gpu)
+    dg, du, dd = tuple(map(dev, gate)), tuple(map(dev, up)), tuple(map(dev, down))
+    calls = []
+    for i, k in enumerate((10, 4, 16, 1, 10, 7)):
+        x = make_x(rng, 1, D)
+        inds = topk_uniform(rng, 1, E, k)
+        wts = oracle.f32_to_bf16(rng.dirichlet(np.ones(k), size=1).astype(np.float32))
+        calls.append((x, inds, wts, dev(x), dev(inds.astype(np.uint32)), dev(wts)))
+    announce("one-token layer: six calls back to back")
+    outs = [ops.switch_glu_combine(dx, di, dg, du, dd, dw) for _, _, _, dx, di, dw in calls]
+    torch.cuda.synchronize()
+    ops.device_error()
+    for (x, inds, wts, *_), out in zip(calls, outs):
+        _combine_ref_check(oracle, to_np(out), x, inds, gate, up, down, wts, E,
+                           what=f"back-to-back k={inds.shape[1]}")
+    # once more: the same calls repeated give the same bits
+    again = [ops.switch_glu_combine(dx, di, dg, du, dd, dw) for _, _, _, dx, di, dw in calls]
+    torch.cuda.synchronize()
+    for a, b in zip(outs, again):
+        assert np.array_equal(to_np(a), to_np(b))
+
+
 # --- moe_layer: routed experts, weighted sum and the shared expert in one call ---
 
 @pytest.mark.parametrize("M", [1, 3, 32, 256])
