@@ -425,6 +425,7 @@ PROBES = {
     "qmvx4_up": (4, 14336, 4096, 4), "qmvx8_up": (8, 14336, 4096, 4),
     "skinny16_up": (16, 14336, 4096, 4), "skinny32_up": (32, 14336, 4096, 4),
     "skinny16_down": (16, 4096, 14336, 4), "skinny32_down": (32, 4096, 14336, 4),
+    "skinny64_up": (64, 14336, 4096, 4), "skinny64_down": (64, 4096, 14336, 4),
     "qmm_up": (2048, 14336, 4096, 4), "qmm_down": (2048, 4096, 14336, 4),
     "qmm512_up": (512, 14336, 4096, 4), "qmm512_down": (512, 4096, 14336, 4),
 }

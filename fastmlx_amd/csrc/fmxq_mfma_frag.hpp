@@ -52,6 +52,27 @@ __device__ __forceinline__ bf16x8 wfrag(uint32_t w) {
   }
 }
 
+// One 4-bit word (q0..q7, least significant first) dequantized in natural order:
+// the bf16 pairs (w0, w1) (w2, w3) (w4, w5) (w6, w7) of w = bf16(fma(s, q, b)), the
+// exact s q + b rounded once.  The even nibbles are masked into bytes (q0 q2 q4 q6)
+// and the odd nibbles kept in place (16 q1 ..), so each value is one
+// v_cvt_f32_ubyteN; the odd ones take s16 = s / 16, which is exact, so
+// s16 * (16 q) = s * q and the fma is the same exact s q + b.  The empty asm hides
+// the masks' known bits, which would otherwise turn each byte pick into a
+// bit-field extract plus a conversion.
+__device__ __forceinline__ bf16x8 deq_frag4(uint32_t w, float s, float s16, float b) {
+  uint32_t e = w & 0x0F0F0F0Fu, o = w & 0xF0F0F0F0u;
+  asm("" : "+v"(e), "+v"(o));
+  const u32x4 r = {
+      pack_bf16x2(__builtin_fmaf(s, (float)(e & 0xffu), b), __builtin_fmaf(s16, (float)(o & 0xffu), b)),
+      pack_bf16x2(__builtin_fmaf(s, (float)((e >> 8) & 0xffu), b),
+                  __builtin_fmaf(s16, (float)((o >> 8) & 0xffu), b)),
+      pack_bf16x2(__builtin_fmaf(s, (float)((e >> 16) & 0xffu), b),
+                  __builtin_fmaf(s16, (float)((o >> 16) & 0xffu), b)),
+      pack_bf16x2(__builtin_fmaf(s, (float)(e >> 24), b), __builtin_fmaf(s16, (float)(o >> 24), b))};
+  return __builtin_bit_cast(bf16x8, r);
+}
+
 // Exponent-trick offset per value and the factor that turns the ones-MFMA sum of
 // the A operand back into sum x (int8 A carries every x value twice).
 template <int BITS>

@@ -34,6 +34,7 @@
 
 #include "fmxq_common.hpp"
 #include "fmxq_internal.hpp"
+#include "fmxq_mfma_frag.hpp"
 
 namespace fmxq {
 namespace {
@@ -54,25 +55,6 @@ __device__ __forceinline__ constexpr int wait_enc(int vm, int lgkm) {
   return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (lgkm << 8);
 }
 
-// One 4-bit word (q0..q7, least significant first) -> the bf16 pairs (w0, w1)
-// (w2, w3) (w4, w5) (w6, w7) of w = bf16(fma(s, q, b)).  The even nibbles are
-// masked into bytes (q0 q2 q4 q6) and the odd nibbles kept in place (16 q1 ..),
-// so each value is one v_cvt_f32_ubyteN; the odd ones take s / 16, which is
-// exact, so s16 * (16 q) = s * q and the fma is the same exact s q + b.  The
-// empty asm hides the masks' known bits, which would otherwise turn each byte
-// pick into a bit-field extract plus a conversion.
-__device__ __forceinline__ bf16x8 deq4(uint32_t w, float s, float s16, float b) {
-  uint32_t e = w & 0x0F0F0F0Fu, o = w & 0xF0F0F0F0u;
-  asm("" : "+v"(e), "+v"(o));
-  const u32x4 r = {
-      pack_bf16x2(__builtin_fmaf(s, (float)(e & 0xffu), b), __builtin_fmaf(s16, (float)(o & 0xffu), b)),
-      pack_bf16x2(__builtin_fmaf(s, (float)((e >> 8) & 0xffu), b),
-                  __builtin_fmaf(s16, (float)((o >> 8) & 0xffu), b)),
-      pack_bf16x2(__builtin_fmaf(s, (float)((e >> 16) & 0xffu), b),
-                  __builtin_fmaf(s16, (float)((o >> 16) & 0xffu), b)),
-      pack_bf16x2(__builtin_fmaf(s, (float)(e >> 24), b), __builtin_fmaf(s16, (float)(o >> 24), b))};
-  return __builtin_bit_cast(bf16x8, r);
-}
 // Two 8-bit words (e0..e7) -> 4 bf16 pairs of w = bf16(fma(s, q, b)).
 __device__ __forceinline__ bf16x8 deq8(uint32_t w0, uint32_t w1, float s, float b) {
   const u32x4 r = {pack_bf16x2(__builtin_fmaf(s, (float)(w0 & 0xffu), b),
@@ -264,7 +246,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(WideArgs wa) {
 #pragma unroll
       for (int j = 0; j < JT; ++j) {
         if constexpr (BITS == 4) {
-          af[j][s] = deq4(wq[set][j][0][s], sb.s[j], sb.s[j] * 0.0625f, sb.b[j]);
+          af[j][s] = deq_frag4(wq[set][j][0][s], sb.s[j], sb.s[j] * 0.0625f, sb.b[j]);
         } else {
           const u32x4 v = wq[set][j][s >> 1];
           af[j][s] = deq8(v[(s & 1) * 2], v[(s & 1) * 2 + 1], sb.s[j], sb.b[j]);

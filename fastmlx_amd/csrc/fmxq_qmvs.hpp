@@ -298,7 +298,13 @@ constexpr int kXStageRow = 512;
 // ahead, as in qmvs_slice) and runs the MFMAs.  Skipped DMA instructions change
 // no wait: the explicit wait counts only the weight loads issued after a step's
 // x.  Only acc[.][0, MTW) is touched.
-template <int MTW, int MT, int NTT, int NMAT, int WV, bool FOLD>
+//
+// DEQ (not with FOLD): the weights are dequantized instead, w = bf16(fma(s, q, b))
+// in natural order (deq_frag4), and the MFMAs accumulate x . w straight into acc
+// with x read in natural order: no Σx MFMAs, no per-group corrections and no x
+// permutation, for 22 VALU per packed word instead of 7.  The word's VALU is
+// shared by the MTW x tiles, so it pays from 2 tiles (17 to 64 x rows).
+template <int MTW, int MT, int NTT, int NMAT, int WV, bool FOLD, bool DEQ = false>
 __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8_t* stage,
                                                __amdgpu_buffer_rsrc_t xres,
                                                const uint32_t (&xo)[8 * MTW / WV], int wave,
@@ -478,6 +484,31 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
     f32x4 xr[MTW];
 #pragma unroll
     for (int j = 0; j < SU; ++j) {
+      if constexpr (DEQ) {
+        static_assert(!FOLD, "DEQ accumulates the dequantized product directly");
+        bf16x8 A[MTW][2];
+#pragma unroll
+        for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            A[mt][h] = __builtin_bit_cast(
+                bf16x8, *reinterpret_cast<const u32x4*>(xc + mt * 16 * kXStageRow + xa[j][h]));
+#pragma unroll
+        for (int p = 0; p < NMAT; ++p)
+#pragma unroll
+          for (int t = 0; t < NTT; ++t) {
+            const float s = (j & 1) ? bf16_hi(sv[p][t][j >> 1]) : bf16_lo(sv[p][t][j >> 1]);
+            const float b = (j & 1) ? bf16_hi(bv[p][t][j >> 1]) : bf16_lo(bv[p][t][j >> 1]);
+            const bf16x8 B0 = deq_frag4(wv[j][p][t][0], s, s * 0.0625f, b);
+            const bf16x8 B1 = deq_frag4(wv[j][p][t][1], s, s * 0.0625f, b);
+#pragma unroll
+            for (int mt = 0; mt < MTW; ++mt) {
+              acc[p][mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mt][0], B0, acc[p][mt][t], 0, 0, 0);
+              acc[p][mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mt][1], B1, acc[p][mt][t], 0, 0, 0);
+            }
+          }
+        continue;
+      }
       bf16x8 A[MTW][2];
 #pragma unroll
       for (int mt = 0; mt < MTW; ++mt) {
@@ -548,7 +579,8 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
 // step.  Steps d with s0 + d >= s1 load from clamped
 // addresses (weights from an offset past the buffer, which reads zeros without
 // a memory access) and are not computed.
-template <int MT, int NTT, int WV, int D>
+// DEQ: the weights dequantized and x in natural order, as in qmvs_walk_xlds.
+template <int MT, int NTT, int WV, int D, bool DEQ = false>
 __device__ __forceinline__ void qmvs_walk_xall(uint8_t* xs, uint8_t* stage, __amdgpu_buffer_rsrc_t xres,
                                                const uint32_t (&xo)[8 * MT / WV], int wave,
                                                const uint32_t* w, const uint16_t* sc,
@@ -663,6 +695,28 @@ __device__ __forceinline__ void qmvs_walk_xall(uint8_t* xs, uint8_t* stage, __am
       }
 #pragma unroll
     for (int j = 0; j < SU; ++j) {
+      if constexpr (DEQ) {
+        bf16x8 A[MT][2];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            A[mt][h] = __builtin_bit_cast(
+                bf16x8, *reinterpret_cast<const u32x4*>(xc + mt * 16 * kXStageRow + xa[j][h]));
+#pragma unroll
+        for (int t = 0; t < NTT; ++t) {
+          const float sf = (j & 1) ? bf16_hi(sv[t][j >> 1]) : bf16_lo(sv[t][j >> 1]);
+          const float bf = (j & 1) ? bf16_hi(bv[t][j >> 1]) : bf16_lo(bv[t][j >> 1]);
+          const bf16x8 B0 = deq_frag4(wv[j][t][0], sf, sf * 0.0625f, bf);
+          const bf16x8 B1 = deq_frag4(wv[j][t][1], sf, sf * 0.0625f, bf);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mt][0], B0, acc[mt][t], 0, 0, 0);
+            acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mt][1], B1, acc[mt][t], 0, 0, 0);
+          }
+        }
+        continue;
+      }
       bf16x8 A[MT][2];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {

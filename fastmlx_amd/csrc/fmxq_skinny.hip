@@ -364,6 +364,21 @@ hipError_t launch_qmvs(const QmmArgs& a, hipStream_t stream) {
 
 namespace {
 
+// The pipelined walk dequantizes the weights (qmvs_walk_xlds DEQ) from this many
+// 16-row x tiles: at M = 64, 30.3 -> 24.2 us on 14336x4096 and 29.3 -> 23.6 us on
+// 4096x14336; at M = 32 on 4096x14336 19.5 -> 17.9 us.
+#ifndef FMXQ_QMVW_DEQ_MIN_MT
+#define FMXQ_QMVW_DEQ_MIN_MT 2
+#endif
+constexpr int kQmvwDeqMinMT = FMXQ_QMVW_DEQ_MIN_MT;
+// The up-front walk likewise from 2 tiles (C1 stack at M = 24 / 32: 3.03 -> 2.99 ms,
+// 3.09 -> 3.01 ms); at one tile the exponent-trick form is quicker (M = 16 on
+// 14336x4096: 16.0 against 17.7 us dequantized).
+#ifndef FMXQ_QMVW_XALL_DEQ_MIN_MT
+#define FMXQ_QMVW_XALL_DEQ_MIN_MT 2
+#endif
+constexpr int kQmvwXallDeqMinMT = FMXQ_QMVW_XALL_DEQ_MIN_MT;
+
 template <int MT, int NTT, int WV, int D>
 __global__ __launch_bounds__(WV * 64) __attribute__((amdgpu_waves_per_eu(MT == 1 && NTT == 1 ? 3 : 2)))
 void qmvw_kernel(QmmArgs a) {
@@ -401,13 +416,15 @@ void qmvw_kernel(QmmArgs a) {
 #pragma unroll
     for (int t = 0; t < NTT; ++t) acc[0][mt][t] = f32x4{};
   if constexpr (D > 0) {
-    qmvs_walk_xall<MT, NTT, WV, D>(&xs[0][0], stage[wave], xres, xo, wave, a.w, a.scales, a.biases,
+    qmvs_walk_xall<MT, NTT, WV, D, (MT >= kQmvwXallDeqMinMT)>(&xs[0][0], stage[wave], xres, xo, wave,
+                                                              a.w, a.scales, a.biases,
                                    nb, a.N, a.K, s0, s1, acc[0]);
   } else {
     const uint32_t* const w[1] = {a.w};
     const uint16_t* const sc[1] = {a.scales};
     const uint16_t* const bi[1] = {a.biases};
-    qmvs_walk_xlds<MT, MT, NTT, 1, WV, false>(xs[0], xs[1], stage[wave], xres, xo, wave, a.M, w, sc, bi,
+    qmvs_walk_xlds<MT, MT, NTT, 1, WV, false, (MT >= kQmvwDeqMinMT)>(xs[0], xs[1], stage[wave], xres, xo,
+                                                                     wave, a.M, w, sc, bi,
                                        nb, a.N, a.K, s0, s1, acc);
   }
 
