@@ -166,8 +166,8 @@ hipError_t launch_gather_qmv(const GatherArgs& a, hipStream_t stream);
 // MoE pieces around gather_qmm (fmxq_moe.hip).  The sort orders the S slots by
 // expert id (ids >= E last); lhs_sorted[pos] = lhs ? lhs[s] : s / lhs_div for the
 // slot s moved to pos.  With seg non-null it also writes the segment table of the
-// sorted order ((start, len) pairs, each run of one id cut at multiples of
-// `window` slots) and the segment count to *nseg.
+// sorted order ((start, len) pairs, each run of one id cut every `window` slots
+// from its start) and the segment count to *nseg.
 hipError_t launch_sort_slots(const uint32_t* inds, int64_t S, int64_t lhs_div, int64_t E,
                              uint32_t* order, uint32_t* rhs_sorted, uint32_t* lhs_sorted,
                              hipStream_t stream, const uint32_t* lhs = nullptr,

@@ -47,17 +47,18 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* w
   return r;
 }
 
-// Pieces of the sorted range [off, off + c) cut at multiples of window.
-__device__ __forceinline__ uint32_t range_pieces(uint32_t off, uint32_t c, uint32_t window) {
-  return c ? (off + c - 1) / window - off / window + 1 : 0u;
+// Pieces of a c-slot run cut every `window` slots from its start.
+__device__ __forceinline__ uint32_t run_pieces(uint32_t c, uint32_t window) {
+  return (c + window - 1) / window;
 }
 
 // One block: counts per expert in LDS, exclusive scan, scatter.  Ids >= E go
 // to a final bucket (the gather kernels zero those rows and raise the flag).
 // Each thread owns a run of consecutive buckets for the scans.  With seg
 // non-null, before the scatter: the pieces of every bucket's range
-// [off, off + count) cut at multiples of `window`, as (start, len) pairs in
-// bucket order, and their number in *nseg.  With tiles non-null as well, the
+// [off, off + count) cut every `window` slots from off (so a run of c slots has
+// ceil(c / window) pieces wherever it starts), as (start, len) pairs in bucket
+// order, and their number in *nseg.  With tiles non-null as well, the
 // runs of an expert (id < E) with at least long_min slots are not cut into
 // window pieces but into tiles of tile_rows slots, written as (start, len) pairs
 // to tiles with their number in *ntile (the grouped GEMM's work list).
@@ -99,7 +100,7 @@ __global__ __launch_bounds__(1024) void sort_slots_kernel(const uint32_t* __rest
     uint32_t lp = 0, lt = 0;
     for (int64_t i = b0; i < b1; ++i) {
       if (is_long(i)) lt += (cnt[i] + tile_rows - 1) / tile_rows;
-      else lp += range_pieces(cur[i], cnt[i], (uint32_t)window);
+      else lp += run_pieces(cnt[i], (uint32_t)window);
     }
     uint32_t k = block_exclusive_scan(lp, wsum, &total);
     if (threadIdx.x == 0) *nseg = total;
@@ -117,12 +118,9 @@ __global__ __launch_bounds__(1024) void sort_slots_kernel(const uint32_t* __rest
         }
         continue;
       }
-      for (uint32_t p = cur[i]; p < end; ++k) {
-        const uint32_t wend = (p / window + 1) * window;
-        const uint32_t q = wend < end ? wend : end;
+      for (uint32_t p = cur[i]; p < end; p += (uint32_t)window, ++k) {
         seg[2 * k] = p;
-        seg[2 * k + 1] = q - p;
-        p = q;
+        seg[2 * k + 1] = end - p < (uint32_t)window ? end - p : (uint32_t)window;
       }
     }
     __syncthreads();  // the scatter below advances cur

@@ -3,9 +3,10 @@
 // mlx_gather_qmm, mlxgo/binding_cgo.go:645-673) once the routing slots are sorted
 // by expert.
 //
-// Slots sorted by expert id form runs; a segment is the part of one run inside
-// one aligned window of W slots (W = 16 MT), so a segment holds at most 16 MT
-// slots of one expert (a block of a 32-slot window whose segment has at most 16
+// Slots sorted by expert id form runs; a segment is a piece of one run, the run
+// cut every W slots from its start (W = 16 MT), so a segment holds at most 16 MT
+// slots of one expert and a run of c slots reads the expert's weights
+// ceil(c / W) times (a block of a 32-slot window whose segment has at most 16
 // slots walks one 16-row tile only).  sort_slots_kernel (fmxq_moe.hip) writes the segment table
 // while it sorts.  Grid: (column tiles, segment bound); blocks past the actual
 // segment count return at once.  A block of 4 waves = WC column groups x KS K
@@ -181,6 +182,16 @@ __global__ __launch_bounds__(256) void moe_qmvs_kernel(MoeArgs a) {
   store_segment<MT, NTT, NMAT>(a, start, len, bad_e, nb, acc);
 }
 
+#ifndef FMXQ_MOE_DEQ_MIN_MT
+#define FMXQ_MOE_DEQ_MIN_MT 2
+#endif
+// Walks of at least this many 16-row x tiles dequantize the weights (DEQ of
+// qmvs_walk_xlds) instead of folding the bias term: the 32-slot segments with
+// more than 16 slots.  Measured per layer: configuration 4 at M=256 1529-1541 ->
+// 1492 us, at M=32 581-583 -> 575-579 us; configuration 3 at M=512 254-259 ->
+// 249-252 us, at M=128 unchanged.
+constexpr int kMoeDeqMinMT = FMXQ_MOE_DEQ_MIN_MT;
+
 // Fixed-length (16 or 32 slot) x-in-LDS form of moe_qmvs_kernel for blocks whose
 // 4 waves walk the whole K range side by side (16 NTT columns each): the
 // segment's x rows go to LDS once per step for all four (qmvs_walk_xlds), so a
@@ -264,8 +275,9 @@ __global__ __launch_bounds__(WV * 64) __attribute__((amdgpu_waves_per_eu(MT == 1
         qmvs_walk_xall<MT, NTT, WV, 2>(&xs[0][0], stage[wave], xres, xo, wave, w[0], sc[0], bi[0],
                                        nb, a.N, a.K, 0, a.K / 256, acc[0]);
       else
-        qmvs_walk_xlds<MT, MT, NTT, NMAT, WV, true>(xs[0], xs[1], stage[wave], xres, xo, wave, len, w,
-                                              sc, bi, nb, a.N, a.K, 0, a.K / 256, acc);
+        qmvs_walk_xlds<MT, MT, NTT, NMAT, WV, !(MT >= kMoeDeqMinMT), (MT >= kMoeDeqMinMT)>(
+            xs[0], xs[1], stage[wave], xres, xo, wave, len, w, sc, bi, nb, a.N, a.K, 0,
+            a.K / 256, acc);
     }
   }
   store_segment<MT, NTT, NMAT>(a, start, len, bad_e, nb, acc);

@@ -237,7 +237,7 @@ def test_moe_combine_op_chain(gpu, oracle):
 
 @pytest.mark.parametrize("E,T,k", [
     (64, 5, 4),     # 20 slots over 64 experts: 16-slot windows, mostly one slot per segment
-    (4, 40, 2),     # 80 slots over 4 experts: 32-slot windows, runs crossing windows
+    (4, 40, 2),     # 80 slots over 4 experts: 32-slot windows, runs of several pieces
     (1, 37, 1),     # one expert: every segment a full window but the last
     (16, 64, 3),    # 192 slots, uniform
 ])
@@ -453,8 +453,9 @@ def test_gather_qmm_segments_short_and_long(gpu, oracle):
 
 
 @pytest.mark.parametrize("E,lens,K", [
-    # 600 slots over 8 experts (32-slot windows): runs of 1, odd lengths, runs that end
-    # just inside or just past a window; grid 32 column tiles x 28 segments
+    # 600 slots over 8 experts (32-slot windows): runs of 1, odd lengths, runs one
+    # slot short of or past a piece (31, 33), pieces of 17 to 32 slots (the walk that
+    # dequantizes the weights) and of 1 to 16; grid 32 column tiles x 28 segments
     (8, [1, 3, 17, 31, 33, 64, 151, 300], 1024),
     # 232 slots over 64 experts (16-slot windows), runs of 1 to 6; grid 16 x 80
     (64, None, 1024),
