@@ -804,6 +804,59 @@ extern "C" int fmxq_moe_layer(
                                                     flag, s, sw_down, ss_down, sb_down),
                       "moe_layer: down/combine");
   }
+  // Sorted batches below the grouped GEMM's floor: the shared expert joins the
+  // sort as expert id E with one slot per token (after the S routed slots), so its
+  // segments ride in the routed gate/up and down launches; the rows land in the
+  // arena's slot 1, routed then shared, and the combine reads both.
+  {
+    const int64_t Sa = S + T;
+    const int window = fmxq::moe_window(Sa, E + 1);
+    const int64_t max_seg = fmxq::moe_max_segments(Sa, E + 1, window);
+    if (!fmxq::moe_combine_unsorted(S, E) && grouped_max_tiles(S, E) == 0 &&
+        E + 1 <= kSortMaxExperts && max_seg <= kMaxSegmentsGrid &&
+        fmxq::moe_qmvs_supported(I, D, bits, group_size) &&
+        fmxq::moe_qmvs_supported(D, I, bits, group_size) && aligned16(s_gate) &&
+        aligned16(b_gate) && aligned16(s_up) && aligned16(b_up) && aligned16(s_down) &&
+        aligned16(b_down) && aligned16(ss_gate) && aligned16(sb_gate) && aligned16(ss_up) &&
+        aligned16(sb_up) && aligned16(ss_down) && aligned16(sb_down)) {
+      uint32_t* flag = nullptr;
+      if (int rc = device_flag(s, &flag)) return rc;
+      MoeScratch m;
+      if (int rc = moe_scratch(s, Sa, I, max_seg, &m, op)) return rc;
+      void* rows = nullptr;
+      if (int rc = stream_arena(s, align_up((size_t)Sa * D * sizeof(uint16_t)), &rows, op, 1))
+        return rc;
+      uint16_t* y = static_cast<uint16_t*>(rows);
+      if (int rc = hip_status(fmxq::launch_sort_slots(inds, S, topk, E, m.order, m.rhs, m.lhs, s,
+                                                      nullptr, m.seg, m.nseg, window, nullptr,
+                                                      nullptr, 0, 0, T),
+                              "moe_layer: sort"))
+        return rc;
+      fmxq::MoeArgs gu{x, m.lhs, {w_gate, w_up}, {s_gate, s_up}, {b_gate, b_up}, m.rhs, m.seg,
+                       m.nseg, m.h, nullptr, Sa, I, D, E, T, flag};
+      gu.sh_w[0] = sw_gate;
+      gu.sh_w[1] = sw_up;
+      gu.sh_s[0] = ss_gate;
+      gu.sh_s[1] = ss_up;
+      gu.sh_b[0] = sb_gate;
+      gu.sh_b[1] = sb_up;
+      gu.sh_seg = true;
+      if (int rc = hip_status(fmxq::launch_moe_qmvs(gu, 2, window, max_seg, s),
+                              "moe_layer: gate/up"))
+        return rc;
+      fmxq::MoeArgs dn{m.h, nullptr, {w_down, nullptr}, {s_down, nullptr}, {b_down, nullptr},
+                       m.rhs, m.seg, m.nseg, y, m.order, Sa, D, I, E, Sa, flag};
+      dn.sh_w[0] = sw_down;
+      dn.sh_s[0] = ss_down;
+      dn.sh_b[0] = sb_down;
+      dn.sh_seg = true;
+      if (int rc = hip_status(fmxq::launch_moe_qmvs(dn, 1, window, max_seg, s), "moe_layer: down"))
+        return rc;
+      return hip_status(fmxq::launch_moe_combine(y, weights, y + S * D, shared_gate, out, T, topk,
+                                                 D, s),
+                        "moe_layer: combine");
+    }
+  }
   // Otherwise the shared expert as a one-expert SwitchGLU over every token (its
   // rows in the arena's slot 2), then the routed part with those rows as the
   // shared term.  Its all-zero expert ids live in slot 3, which only ever holds

@@ -167,13 +167,15 @@ hipError_t launch_gather_qmv(const GatherArgs& a, hipStream_t stream);
 // expert id (ids >= E last); lhs_sorted[pos] = lhs ? lhs[s] : s / lhs_div for the
 // slot s moved to pos.  With seg non-null it also writes the segment table of the
 // sorted order ((start, len) pairs, each run of one id cut every `window` slots
-// from its start) and the segment count to *nseg.
+// from its start) and the segment count to *nseg.  With sh_T > 0, sh_T slots of a
+// shared expert (id E, x row t for slot S + t) follow the routed ones, and
+// out-of-range routed ids are stored as E + 1.
 hipError_t launch_sort_slots(const uint32_t* inds, int64_t S, int64_t lhs_div, int64_t E,
                              uint32_t* order, uint32_t* rhs_sorted, uint32_t* lhs_sorted,
                              hipStream_t stream, const uint32_t* lhs = nullptr,
                              uint32_t* seg = nullptr, uint32_t* nseg = nullptr, int window = 16,
                              uint32_t* tiles = nullptr, uint32_t* ntile = nullptr,
-                             int long_min = 0, int tile_rows = 0);
+                             int long_min = 0, int tile_rows = 0, int64_t sh_T = 0);
 hipError_t launch_silu_mul_tiles(const uint16_t* g, const uint16_t* u, uint16_t* h,
                                  const uint32_t* tiles, const uint32_t* ntile, int64_t max_tiles,
                                  int64_t tile_rows, int64_t n, hipStream_t stream);
@@ -242,6 +244,9 @@ struct MoeArgs {
   const uint16_t* sh_s[2] = {nullptr, nullptr};
   const uint16_t* sh_b[2] = {nullptr, nullptr};
   int64_t sh_T = 0;
+  // Segment-table form only: expert id E names the shared expert (sh_w / sh_s /
+  // sh_b), ids above E are out of range (launch_sort_slots with sh_T > 0).
+  bool sh_seg = false;
 };
 // Slot counts up to which the MoE products skip the sort: every slot is its own
 // segment (a sort saves weight reads only when slots share an expert).

@@ -62,8 +62,14 @@ __device__ __forceinline__ uint32_t run_pieces(uint32_t c, uint32_t window) {
 // runs of an expert (id < E) with at least long_min slots are not cut into
 // window pieces but into tiles of tile_rows slots, written as (start, len) pairs
 // to tiles with their number in *ntile (the grouped GEMM's work list).
+//
+// With sh_T > 0, sh_T shared-expert slots follow the S routed ones: slot S + t
+// has id E and x row t, and out-of-range routed ids go to bucket E + 1 and are
+// stored as E + 1 in rhs_sorted (so a walk tells the shared expert, id E, from a
+// bad id, above E).
 __global__ __launch_bounds__(1024) void sort_slots_kernel(const uint32_t* __restrict__ inds,
-                                                          int64_t S, int64_t lhs_div, int64_t E,
+                                                          int64_t S, int64_t sh_T,
+                                                          int64_t lhs_div, int64_t E,
                                                           uint32_t* __restrict__ order,
                                                           uint32_t* __restrict__ rhs_sorted,
                                                           uint32_t* __restrict__ lhs_sorted,
@@ -73,16 +79,20 @@ __global__ __launch_bounds__(1024) void sort_slots_kernel(const uint32_t* __rest
                                                           int window, uint32_t* __restrict__ tiles,
                                                           uint32_t* __restrict__ ntile,
                                                           uint32_t long_min, uint32_t tile_rows) {
-  extern __shared__ uint32_t cnt[];  // E + 1 counters, then E + 1 cursors
+  extern __shared__ uint32_t cnt[];  // nb counters, then nb cursors
   __shared__ uint32_t wsum[16], total;
-  const int64_t nb = E + 1;
+  const uint32_t bad = (uint32_t)E + (sh_T > 0 ? 1u : 0u);  // bucket of out-of-range ids
+  const int64_t nb = (int64_t)bad + 1;
+  const int64_t Sa = S + sh_T;
+  auto bucket = [&](int64_t s) -> uint32_t {
+    if (s >= S) return (uint32_t)E;
+    const uint32_t e = inds[s];
+    return e < (uint64_t)E ? e : bad;
+  };
   uint32_t* cur = cnt + nb;
   for (int64_t i = threadIdx.x; i < nb; i += blockDim.x) cnt[i] = 0;
   __syncthreads();
-  for (int64_t s = threadIdx.x; s < S; s += blockDim.x) {
-    const uint32_t e = inds[s];
-    atomicAdd(&cnt[e < (uint64_t)E ? e : E], 1u);
-  }
+  for (int64_t s = threadIdx.x; s < Sa; s += blockDim.x) atomicAdd(&cnt[bucket(s)], 1u);
   __syncthreads();
   const int64_t per = (nb + blockDim.x - 1) / blockDim.x;
   const int64_t b0 = threadIdx.x * per < nb ? threadIdx.x * per : nb;
@@ -125,12 +135,12 @@ __global__ __launch_bounds__(1024) void sort_slots_kernel(const uint32_t* __rest
     }
     __syncthreads();  // the scatter below advances cur
   }
-  for (int64_t s = threadIdx.x; s < S; s += blockDim.x) {
-    const uint32_t e = inds[s];
-    const uint32_t pos = atomicAdd(&cur[e < (uint64_t)E ? e : E], 1u);
+  for (int64_t s = threadIdx.x; s < Sa; s += blockDim.x) {
+    const uint32_t b = bucket(s);
+    const uint32_t pos = atomicAdd(&cur[b], 1u);
     order[pos] = (uint32_t)s;
-    rhs_sorted[pos] = e;
-    lhs_sorted[pos] = lhs ? lhs[s] : (uint32_t)(s / lhs_div);
+    rhs_sorted[pos] = sh_T > 0 ? b : inds[s];
+    lhs_sorted[pos] = s >= S ? (uint32_t)(s - S) : lhs ? lhs[s] : (uint32_t)(s / lhs_div);
   }
 }
 
@@ -223,11 +233,13 @@ hipError_t launch_sort_slots(const uint32_t* inds, int64_t S, int64_t lhs_div, i
                              uint32_t* order, uint32_t* rhs_sorted, uint32_t* lhs_sorted,
                              hipStream_t stream, const uint32_t* lhs, uint32_t* seg,
                              uint32_t* nseg, int window, uint32_t* tiles, uint32_t* ntile,
-                             int long_min, int tile_rows) {
+                             int long_min, int tile_rows, int64_t sh_T) {
   if (seg && (!nseg || window < 1)) return hipErrorInvalidValue;
   if (tiles && (!seg || !ntile || long_min < 1 || tile_rows < 1)) return hipErrorInvalidValue;
-  const size_t lds = (size_t)(E + 1) * 2 * sizeof(uint32_t);
-  sort_slots_kernel<<<1, 1024, lds, stream>>>(inds, S, lhs_div, E, order, rhs_sorted, lhs_sorted,
+  if (sh_T < 0) return hipErrorInvalidValue;
+  const size_t lds = (size_t)(E + 1 + (sh_T > 0 ? 1 : 0)) * 2 * sizeof(uint32_t);
+  sort_slots_kernel<<<1, 1024, lds, stream>>>(inds, S, sh_T, lhs_div, E, order, rhs_sorted,
+                                              lhs_sorted,
                                               lhs, seg, nseg, window, tiles, ntile,
                                               (uint32_t)long_min, (uint32_t)tile_rows);
   return hipGetLastError();

@@ -101,7 +101,8 @@ __global__ __launch_bounds__(256) void moe_qmvs_kernel(MoeArgs a) {
   const int64_t len = a.seg ? (int64_t)a.seg[2 * sg + 1] : 1;
   const uint32_t e = a.rhs[start];
   const int64_t nb = (int64_t)blockIdx.x * (16 * NTT * WC) + wc * (16 * NTT);
-  const bool bad_e = (int64_t)e >= a.E;
+  const bool sh = a.sh_seg && (int64_t)e == a.E;
+  const bool bad_e = (int64_t)e >= a.E && !sh;
 
   // x row of each of this lane's slots (row of the segment's first slot for lanes
   // past its end; a bad slot reads row 0 and is zeroed at the store).
@@ -129,9 +130,9 @@ __global__ __launch_bounds__(256) void moe_qmvs_kernel(MoeArgs a) {
     const uint16_t* bi[NMAT];
 #pragma unroll
     for (int p = 0; p < NMAT; ++p) {
-      w[p] = a.w[p] + (int64_t)e * a.N * wpr;
-      sc[p] = a.s[p] + (int64_t)e * a.N * gpr;
-      bi[p] = a.b[p] + (int64_t)e * a.N * gpr;
+      w[p] = sh ? a.sh_w[p] : a.w[p] + (int64_t)e * a.N * wpr;
+      sc[p] = sh ? a.sh_s[p] : a.s[p] + (int64_t)e * a.N * gpr;
+      bi[p] = sh ? a.sh_b[p] : a.b[p] + (int64_t)e * a.N * gpr;
     }
     const int64_t nst = a.K / (SU * 64);
     const int64_t st0 = ks * nst / KS, st1 = (ks + 1) * nst / KS;
@@ -212,7 +213,8 @@ __global__ __launch_bounds__(WV * 64) __attribute__((amdgpu_waves_per_eu(MT == 1
   const int64_t len = a.seg ? (int64_t)a.seg[2 * sg + 1] : 1;
   const uint32_t e = a.rhs[start];
   const int64_t nb = (int64_t)blockIdx.x * (16 * NTT * WV) + wave * (16 * NTT);
-  const bool bad_e = (int64_t)e >= a.E;
+  const bool sh = a.sh_seg && (int64_t)e == a.E;
+  const bool bad_e = (int64_t)e >= a.E && !sh;
 
   f32x4 acc[NMAT][MT][NTT];
 #pragma unroll
@@ -228,9 +230,9 @@ __global__ __launch_bounds__(WV * 64) __attribute__((amdgpu_waves_per_eu(MT == 1
     const uint16_t* bi[NMAT];
 #pragma unroll
     for (int p = 0; p < NMAT; ++p) {
-      w[p] = a.w[p] + (int64_t)e * a.N * wpr;
-      sc[p] = a.s[p] + (int64_t)e * a.N * gpr;
-      bi[p] = a.b[p] + (int64_t)e * a.N * gpr;
+      w[p] = sh ? a.sh_w[p] : a.w[p] + (int64_t)e * a.N * wpr;
+      sc[p] = sh ? a.sh_s[p] : a.s[p] + (int64_t)e * a.N * gpr;
+      bi[p] = sh ? a.sh_b[p] : a.b[p] + (int64_t)e * a.N * gpr;
     }
     // moe_xlds_supported keeps x_rows * K * 2 below 2^31.
     const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
@@ -740,10 +742,12 @@ hipError_t launch_moe_qmvs(const MoeArgs& a, int nmat, int window, int64_t max_s
   // us), without the GEMV grid's blocks for every other segment.
   MoeArgs b = a;
   const bool gemv = a.K >= 2048 && a.K <= 16384 && !a.seg;
-  // Shared-expert segments exist only in the GEMV form, without an output row map.
-  if (a.sh_T > 0 && (!gemv || a.yrow || !a.sh_w[0] || !a.sh_s[0] || !a.sh_b[0] ||
-                     (nmat == 2 && (!a.sh_w[1] || !a.sh_s[1] || !a.sh_b[1]))))
-    return hipErrorInvalidValue;
+  // Shared-expert segments exist in the GEMV form, without an output row map, and
+  // as id E of a segment table.
+  const bool sh_ops = a.sh_w[0] && a.sh_s[0] && a.sh_b[0] &&
+                      (nmat == 1 || (a.sh_w[1] && a.sh_s[1] && a.sh_b[1]));
+  if (a.sh_T > 0 && (!gemv || a.yrow || !sh_ops)) return hipErrorInvalidValue;
+  if (a.sh_seg && (!a.seg || a.sh_T > 0 || !sh_ops)) return hipErrorInvalidValue;
   if (gemv)
     return nmat == 2 ? launch_qmv1_nmat<2, 1>(a, a.S + a.sh_T, stream)
                      : launch_qmv1_nmat<1, 1>(a, a.S + a.sh_T, stream);

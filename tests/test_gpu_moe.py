@@ -771,9 +771,11 @@ def test_moe_layer_shared_expert_c4(gpu, oracle, M):
     """Configuration 4 with its shared expert computed inside the call
     (deepseekv3_forward.go:436-440: routed sum + mlp(x)), up to M=256, the largest
     token count the bench times.  One token runs the
-    shared expert as one more gate/up segment and one more down/combine wave; more
-    tokens run it as a one-expert SwitchGLU first.  Checked element by element
-    against the oracle's routed experts and shared MLP."""
+    shared expert as one more gate/up segment and one more down/combine wave; three
+    tokens (24 slots, few sharing an expert) run it as a one-expert SwitchGLU first;
+    sorted batches (32 and 256 tokens) sort it in as expert E, one slot per token,
+    inside the routed launches.  Checked element by element against the oracle's
+    routed experts and shared MLP."""
     from fastmlx_amd import ops
 
     (gate, up, down), dstack, shared, dshared = _layer_weights(gpu, "c4")
@@ -801,13 +803,16 @@ def test_moe_layer_shared_expert_c4(gpu, oracle, M):
 
 
 @pytest.mark.parametrize("T,E,D,k", [(1, 300, 2048, 10), (2, 300, 2048, 10),
-                                     (1, 64, 2048, 16), (1, 40, 512, 6)])
+                                     (1, 64, 2048, 16), (1, 40, 512, 6),
+                                     (24, 32, 2048, 6), (40, 16, 512, 4)])
 def test_moe_layer_gated_shared_expert(gpu, oracle, T, E, D, k):
     """A Qwen3-Next-style layer (qwen3next_forward.go:519-524): the shared expert's
     output scaled by sigmoid(shared_gate) before it is added.  One token with up
     to 15 slots and D >= 2048 runs fused; two tokens, 16 slots (a block would need
     17 waves) and D = 512 (below the GEMV form's depth) run the one-expert
-    SwitchGLU first."""
+    SwitchGLU first; 24 and 40 tokens over few experts sort the shared expert in
+    as expert E (16- and 32-slot segments; D = 512 walks its down projection with
+    every load issued up front)."""
     from fastmlx_amd import ops
 
     rng = np.random.default_rng(960 + T + k + D)
@@ -838,21 +843,28 @@ def test_moe_layer_gated_shared_expert(gpu, oracle, T, E, D, k):
                          what=f"moe_layer gated T={T}")
 
 
-def test_moe_layer_bad_expert_id(gpu, oracle):
-    """A bad routed id in the fused one-token form: its slot contributes zero, the
-    shared expert and the other slots still add up, and the flag is raised."""
+@pytest.mark.parametrize("T", [1, 20])
+def test_moe_layer_bad_expert_id(gpu, oracle, T):
+    """Bad routed ids: their slots contribute zero, the shared expert and the other
+    slots still add up, and the flag is raised.  One token runs the fused one-token
+    form; 20 tokens (120 slots over 40 experts) sort the shared expert in as
+    expert E, where a routed id of exactly E must still count as bad, not as the
+    shared expert."""
     from fastmlx_amd import FmxqError, ops
 
-    rng = np.random.default_rng(971)
+    rng = np.random.default_rng(971 + T)
     E, D, I, k = 40, 2048, 512, 6
     gate, up, down = _stack(rng, E, D, I)
     sh = _stack(rng, 1, D, I)
-    x = make_x(rng, 1, D)
-    inds = topk_uniform(rng, 1, E, k)
-    inds[0, 2] = E + 7
-    w16 = oracle.f32_to_bf16(rng.dirichlet(np.ones(k), size=1).astype(np.float32))
+    x = make_x(rng, T, D)
+    inds = topk_uniform(rng, T, E, k)
+    bad = [(0, 2, E + 7)] if T == 1 else [(0, 2, E + 7), (5, 1, E), (T - 1, 0, 2 ** 32 - 1)]
+    inds = inds.astype(np.int64)
+    for t, j, v in bad:
+        inds[t, j] = v
+    w16 = oracle.f32_to_bf16(rng.dirichlet(np.ones(k), size=T).astype(np.float32))
     dev = lambda t: to_dev(t, gpu)
-    announce("moe_layer bad id")
+    announce(f"moe_layer bad id T={T}")
     out = ops.moe_layer(dev(x), dev(inds.astype(np.uint32)), tuple(map(dev, gate)),
                         tuple(map(dev, up)), tuple(map(dev, down)), dev(w16),
                         tuple(tuple(map(dev, q)) for q in sh))
@@ -860,13 +872,14 @@ def test_moe_layer_bad_expert_id(gpu, oracle):
     got = to_np(out)
     with pytest.raises(FmxqError):
         ops.device_error()
-    safe = np.where(inds >= E, 0, inds)
+    safe = np.where(inds >= E, 0, inds).astype(np.int32)
     sref = parity.SwitchRef(x, safe, gate, up, down, fused=False)
     near = sref.refs[0].copy()
-    near[0, 2] = 0.0
     allow = parity.switch_bound(near, near, sref.hscale)
-    allow[0, 2] = 0.0
-    ssref = parity.SwitchRef(x, np.zeros((1, 1), dtype=np.int32), *sh, fused=False)
+    for t, j, _ in bad:
+        near[t, j] = 0.0
+        allow[t, j] = 0.0
+    ssref = parity.SwitchRef(x, np.zeros((T, 1), dtype=np.int32), *sh, fused=False)
     sv = ssref.refs[0]
     sa = parity.switch_bound(sv, sv, ssref.hscale)
     parity.combine_check(got, near, allow, w16, shared=(sv[:, 0], sa[:, 0]),
@@ -874,10 +887,11 @@ def test_moe_layer_bad_expert_id(gpu, oracle):
 
 
 def test_moe_layer_graph_replay(gpu, oracle):
-    """moe_layer under HIP graph capture: the one-token form and the several-token
-    form (whose shared expert ids come from a zero buffer filled once per buffer)
-    replay to the eager result every time, with eager calls of other sizes on the
-    same stream in between."""
+    """moe_layer under HIP graph capture: the one-token form, the few-slot form
+    (whose shared expert ids come from a zero buffer filled once per buffer) and
+    the sorted form (the shared expert sorted in as expert E) replay to the eager
+    result every time, with eager calls of other sizes on the same stream in
+    between."""
     from fastmlx_amd import ops
 
     (gate, up, down), dstack, shared, dshared = _layer_weights(gpu, "c4")
@@ -885,7 +899,7 @@ def test_moe_layer_graph_replay(gpu, oracle):
     E, D = gate[0].shape[0], down[0].shape[1]
     k = 8
     cases = []
-    for T in (1, 4):
+    for T in (1, 4, 40):
         inds = topk_zipf(rng, T, E, k)
         g = 1 / (1 + np.exp(-rng.standard_normal((T, k))))
         w16 = oracle.f32_to_bf16((g / g.sum(1, keepdims=True)).astype(np.float32))
