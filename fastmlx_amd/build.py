@@ -2,7 +2,8 @@
 
 ``python -m fastmlx_amd.build`` or ``fastmlx_amd.build.build()``.  Objects go to
 ``fastmlx_amd/_build/``; the shared library lands next to this file so it
-travels with the source tree.
+travels with the source tree.  ``--diag`` (``build_diag()``) also builds the
+time-line diagnostic program ``diag/qmv1_timeline``.
 """
 from __future__ import annotations
 
@@ -34,8 +35,8 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found; libfmxq.so cannot be built")
 
 
-def _compile(src: str, obj: str) -> None:
-    cmd = [_hipcc(), *HIP_FLAGS, "-c", src, "-o", obj]
+def _compile(src: str, obj: str, flags=None) -> None:
+    cmd = [_hipcc(), *(flags or HIP_FLAGS), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
@@ -44,6 +45,29 @@ def _compile(src: str, obj: str) -> None:
     msgs = [ln for ln in r.stderr.splitlines() if noise not in ln and ln.strip()]
     if msgs:
         print("\n".join(msgs), file=sys.stderr)
+
+
+DIAG = os.path.join(HERE, "diag")
+TIMELINE = os.path.join(DIAG, "qmv1_timeline")
+
+
+def build_diag(verbose: bool = True) -> str:
+    """The time-line diagnostic (diag/qmv1_timeline.hip): a program, not part of the
+    library, linked with its own build of fmxq_qmv.hip under FMXQ_QMV1_TIMELINE."""
+    os.makedirs(OUT_DIR, exist_ok=True)
+    flags = [*HIP_FLAGS, "-I", CSRC, "-DFMXQ_QMV1_TIMELINE"]
+    objs = []
+    for src in (os.path.join(DIAG, "qmv1_timeline.hip"), os.path.join(CSRC, "fmxq_qmv.hip")):
+        obj = os.path.join(OUT_DIR, "timeline_" + os.path.basename(src) + ".o")
+        _compile(src, obj, flags)
+        objs.append(obj)
+    r = subprocess.run([_hipcc(), f"--offload-arch={ARCH}", "-o", TIMELINE, *objs],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed: {TIMELINE}\n{r.stdout}\n{r.stderr}")
+    if verbose:
+        print(f"built {TIMELINE}")
+    return TIMELINE
 
 
 def build(verbose: bool = True) -> str:
@@ -67,3 +91,5 @@ def build(verbose: bool = True) -> str:
 
 if __name__ == "__main__":
     build()
+    if "--diag" in sys.argv[1:]:
+        build_diag()

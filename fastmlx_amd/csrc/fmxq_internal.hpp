@@ -39,6 +39,11 @@ struct QmmArgs {
   const uint32_t* g_yrow = nullptr;
   int64_t g_xrows = 0;
   uint32_t* g_flag = nullptr;
+#ifdef FMXQ_QMV1_TIMELINE
+  // Time-line diagnostic build only (fastmlx_amd/diag/qmv1_timeline.hip):
+  // qmv1_slice_kernel stores six words per wave here when non-null.
+  uint64_t* tl_stamps = nullptr;
+#endif
 };
 
 // Gathered product over `batch` items of Mx rows:

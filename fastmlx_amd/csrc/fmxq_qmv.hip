@@ -324,8 +324,26 @@ static hipError_t launch_qmv1(const QmmArgs& a, hipStream_t stream) {
 //     +7 of the slice) in a wave-private table [RW][32], no barrier;
 //   - a block is RG row groups x KS slices; the slices meet in LDS.
 // Arithmetic as in qmv1_kernel.
+//
+// With FMXQ_QMV1_TIMELINE (the diagnostic build of fastmlx_amd/diag only; the
+// library compiles none of it) each wave reads the 100 MHz s_memrealtime clock at
+// its start, once its weight loads are issued, after its first row's arithmetic
+// (so after its first weight bytes arrived), after its last row's, and at its end,
+// and lane 0 stores the five stamps and the wave's XCC and hardware ids to
+// a.tl_stamps[6 * wave] with vector stores.
+#ifdef FMXQ_QMV1_TIMELINE
+#define FMXQ_TL_STAMP(v) v = __builtin_amdgcn_s_memrealtime()
+#define FMXQ_TL_AFTER(v, r) asm volatile("" ::"v"(r))
+#else
+#define FMXQ_TL_STAMP(v) (void)0
+#define FMXQ_TL_AFTER(v, r) (void)0
+#endif
 template <int RW, int KS, int RG>
 __global__ __launch_bounds__(KS * RG * 64) void qmv1_slice_kernel(QmmArgs a) {
+#ifdef FMXQ_QMV1_TIMELINE
+  uint64_t tl[5] = {};
+#endif
+  FMXQ_TL_STAMP(tl[0]);
   constexpr int LV = __builtin_ctz(RW);
   // Two-slice (4096-deep) rows load the block's scales as contiguous runs into a
   // shared table; longer rows keep each wave's own pieces (measured no faster as
@@ -394,6 +412,7 @@ __global__ __launch_bounds__(KS * RG * 64) void qmv1_slice_kernel(QmmArgs a) {
     wv[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.w + (int64_t)n * wpr) + c);
   }
   __builtin_amdgcn_sched_barrier(0);
+  FMXQ_TL_STAMP(tl[1]);
   XChunk<4> xc;
   {
     float s = 0.f;
@@ -441,7 +460,13 @@ __global__ __launch_bounds__(KS * RG * 64) void qmv1_slice_kernel(QmmArgs a) {
     const float s = bf16_lo(sb);
     const float bo = __builtin_fmaf(-magic_offset<4>(), s, bf16_hi(sb));
     res[r] = __builtin_fmaf(s, chunk_dot<4>(wv[r], xc), bo * xc.sum);
+    if (r == 0) {
+      FMXQ_TL_AFTER(tl[2], res[0]);
+      FMXQ_TL_STAMP(tl[2]);
+    }
   }
+  FMXQ_TL_AFTER(tl[3], res[RW - 1]);
+  FMXQ_TL_STAMP(tl[3]);
   const float tot = wave_sum_multi<RW>(res, lane);
   const int idx = lane >> (6 - LV);
   const bool writer = (lane & ((64 >> LV) - 1)) == 0;
@@ -458,6 +483,17 @@ __global__ __launch_bounds__(KS * RG * 64) void qmv1_slice_kernel(QmmArgs a) {
   } else {
     if (writer && n < a.N) a.y[n] = finish_out(tot, a.bias, n);
   }
+#ifdef FMXQ_QMV1_TIMELINE
+  FMXQ_TL_STAMP(tl[4]);
+  if (a.tl_stamps && lane == 0) {
+    const uint32_t hw = __builtin_amdgcn_s_getreg((4 << 0) | (0 << 6) | (31 << 11));   // HW_ID
+    const uint32_t xcc = __builtin_amdgcn_s_getreg((20 << 0) | (0 << 6) | (3 << 11));  // XCC_ID
+    uint64_t* o = a.tl_stamps + 6 * ((int64_t)blockIdx.x * (KS * RG) + wave);
+#pragma unroll
+    for (int i = 0; i < 5; ++i) o[i] = tl[i];
+    o[5] = ((uint64_t)xcc << 32) | hw;
+  }
+#endif
 }
 
 template <int RW, int KS, int RG>
