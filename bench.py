@@ -659,8 +659,8 @@ def main():
         busy = profile_value(QMM_PMC, "mfma_busy")
         extra["qmm_M2048_mfma_busy_rocprof"] = busy
         # The qmm headline: the hand-written MFMA kernel that quantized_matmul runs
-        # at M >= 768 (dequantization in registers, no vendor GEMM, no workspace
-        # the size of W); both Config 2 orientations, int4 group 64.
+        # at prefill sizes (dequantization in registers, no vendor GEMM, no
+        # workspace the size of W); both Config 2 orientations, int4 group 64.
         qd = extra["c2_4bit_4096x14336_M2048"]
         extra["qmm_M2048"] = {
             "kernel": "fmxq::qmm_wide_kernel<4,8,256> (hand-written HIP, bf16 MFMA 32x32x16)",

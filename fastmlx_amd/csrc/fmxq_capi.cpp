@@ -291,7 +291,7 @@ int qmm_common(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
   hipStream_t s = static_cast<hipStream_t>(stream);
   // Prefill sizes: the wide GEMM (256 x 256 tiles, weights dequantized in
   // registers, stream-K over the tiles past the last whole wave of blocks).
-  if (M >= fmxq::kWideMinM && fmxq::qmm_wide_supported(a)) {
+  if (fmxq::qmm_use_wide(M, N, K) && fmxq::qmm_wide_supported(a)) {
     int cus = 0;
     if (int rc = device_cus(&cus)) return rc;
     const fmxq::WidePlan wp = fmxq::qmm_wide_plan(M, N, K, cus);

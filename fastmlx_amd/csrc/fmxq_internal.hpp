@@ -146,7 +146,19 @@ hipError_t launch_qmm_prefill(const QmmArgs& a, hipStream_t stream);
 // their tile leave fp32 partials in ws (ws_floats, one bm x 256 slot per block)
 // and bump tile_count (tiles counters, zero between calls; the kernel clears
 // them again).
-constexpr int64_t kWideMinM = 768;
+// quantized_matmul takes the wide GEMM (where qmm_wide_supported) from
+// kWideMinM rows of x, and from kWideMinMWide rows for outputs at least twice
+// the depth (N >= 2K: the gate/up shapes).  Measured against the prefill GEMM
+// (4-bit / 8-bit, us): 14336x4096 at M = 128 48-50 / 51-53 -> 36-38 / 38.5, at
+// M = 256 58-62 / 58 -> 46-50 / 56, at M = 512 77-79 / 82 -> 63-67 / 73;
+// 4096x14336 at M = 384 91 / 93 -> 70 / 86, at M = 512 93-94 / 96 -> 77.5 / 85,
+// at M = 640 153 / 157 -> 110 / 132.  Below M = 384 the deep shape stays on the
+// prefill GEMM (M = 256: 54 against 54-62 us).
+constexpr int64_t kWideMinM = 384;
+constexpr int64_t kWideMinMWide = 128;
+inline bool qmm_use_wide(int64_t M, int64_t N, int64_t K) {
+  return M >= kWideMinM || (M >= kWideMinMWide && N >= 2 * K);
+}
 constexpr int kWideMinPiece = 16;
 struct WidePlan {
   int bm, tm, nk, dp, sk_len, blocks;

@@ -1,5 +1,6 @@
 // fmxq_qmm_wide.hip -- MFMA GEMM with the dequantization in registers, for
-// quantized_matmul at prefill sizes (M >= kWideMinM rows of x).
+// quantized_matmul at prefill sizes (qmm_use_wide: M >= 384 rows of x, or
+// M >= 128 for outputs at least twice the depth).
 //
 // Replaces the GEMM of mlx_quantized_matmul (mlxgo/binding_cgo.go:636-643) for
 // x [M, K] with M = batch * seq rows: prefill through compute/models/quant.go:91-101
@@ -484,11 +485,26 @@ WidePlan qmm_wide_plan(int64_t M, int64_t N, int64_t K, int cus) {
   // into more pieces.
   const int64_t tn = (N + kT - 1) / kT;
   p.bm = 2 * ((M + 255) / 256) * tn >= cus ? 256 : 128;
+
   p.tm = (int)((M + p.bm - 1) / p.bm);
   const int64_t tiles = (int64_t)p.tm * tn;
   p.nk = (int)(K / kS);
   p.blocks = cus;
   p.dp = (int)(tiles / cus);
+  // Tiles filling at least 7/8 of the CUs but not all of them: one whole tile
+  // per block, no stream-K.  Pieces of tiles * nk / cus steps would cut nearly
+  // every tile in two, each cut costing a partial's round trip and a wait
+  // (14336x4096 at M = 512, 224 tiles on 256 CUs: 4-bit 73-77 -> 63-67 us, 8-bit
+  // 92-95 -> 73 us).
+  if (p.dp == 0 && tiles * 8 >= (int64_t)cus * 7) {
+    p.dp = 1;
+    p.blocks = (int)tiles;
+    p.sk_iters = 0;
+    p.sk_len = 0;
+    p.tiles = tiles;
+    p.ws_floats = 0;
+    return p;
+  }
   const int64_t rest = tiles % cus;
   p.sk_iters = rest * p.nk;
   p.sk_len = 0;

@@ -171,7 +171,8 @@ def test_qmm_prefill_tiles(gpu, oracle, M, N, K, bits, group):
     (300, 512, 2048, 4, 64, True),     # 8 tiles -> 4 K parts each (fixup adds the bias)
     (130, 700, 4096, 8, 32, False),    # 8-bit, group 32, ragged M and N, parts only
     (1000, 2048, 8192, 4, 128, False), # 64 tiles x 4 parts
-    (512, 16640, 1024, 4, 64, True),   # 260 tiles: 256 whole, the last 4 in 2 parts each
+    (512, 16640, 1024, 4, 32, True),   # 260 tiles: 256 whole, the last 4 in 2 parts each
+                                       # (group 32 keeps M = 512 off the wide GEMM)
 ])
 def test_qmm_prefill_k_split(gpu, oracle, M, N, K, bits, group, bias):
     """Prefill tiles of a part-full last wave are computed in K parts summed by a
@@ -254,7 +255,12 @@ def test_qmvw_parts_and_walks(gpu, oracle, M, N, K, bias):
 
 
 @pytest.mark.parametrize("M,N,K,bits,group", [
-    (768, 1024, 1024, 4, 64),    # the threshold M
+    (384, 1024, 1024, 4, 64),    # the threshold M
+    (383, 1024, 1024, 4, 64),    # one row below it: the prefill GEMM
+    (128, 8192, 4096, 4, 64),    # outputs twice the depth: the wide GEMM from M = 128
+    (127, 8192, 4096, 8, 64),    # one row below: the prefill GEMM
+    (512, 14336, 4096, 8, 64),   # 224 tiles on 256 CUs: one whole tile per block
+    (768, 1024, 1024, 4, 64),
     (1024, 1024, 1024, 4, 64),
     (1500, 4104, 2048, 4, 32),   # group 32: the prefill GEMM's 64-row tile instead
     (1024, 2048, 4096, 4, 128),  # group 128: likewise
@@ -265,9 +271,11 @@ def test_qmvw_parts_and_walks(gpu, oracle, M, N, K, bias):
     (1300, 14336, 4096, 4, 64),  # whole tiles, then stream-K pieces of uneven length
 ])
 def test_wide_gemm_shapes(gpu, oracle, M, N, K, bits, group):
-    """Bias-free products at M >= 768: the hand-written wide MFMA GEMM (group 64,
-    K a multiple of 256) with its stream-K split of the K range, or the prefill
-    GEMM for the other group sizes; per-element bound against the fp64 oracle."""
+    """Prefill-sized products (M >= 384, or M >= 128 where N >= 2K): the
+    hand-written wide MFMA GEMM (group 64, K a multiple of 256) with its stream-K
+    split of the K range or one whole tile per block, or the prefill GEMM for the
+    other group sizes and just below the thresholds; per-element bound against the
+    fp64 oracle."""
     rows = np.unique(np.array([0, 1, M // 3, M // 2, M - 2, M - 1]))
     _qmm_case(gpu, oracle, M, N, K, bits, group, seed=9700 + M + N + K + bits + group,
               rows_checked=rows)
