@@ -162,8 +162,10 @@ int fmxq_switch_glu_combine(const uint16_t* x, const uint32_t* inds, const uint3
  * ([1, I, D*bits/32], [1, D, I*bits/32], ...), with the routed experts' I.  The
  * shared expert's op chain and roundings are those of a one-expert SwitchGLU.
  * For one token (decode) the shared expert runs inside the routed kernels (one
- * more gate/up segment, one more wave per down/combine block; top_k <= 15);
- * otherwise it runs as fmxq_switch_glu on every token, then
+ * more gate/up segment, one more wave per down/combine block; top_k <= 15).
+ * Batches whose routed slots are sorted (below 4096 slots) sort it in as one
+ * more expert with one slot per token, so it runs inside the routed gate/up and
+ * down launches.  Otherwise it runs as fmxq_switch_glu on every token, then
  * fmxq_switch_glu_combine adds its rows.  Extends fmxq_switch_glu_combine; the
  * reference computes the shared expert with its own qlinear calls. */
 int fmxq_moe_layer(const uint16_t* x, const uint32_t* inds, const uint32_t* w_gate,
