@@ -250,11 +250,16 @@ int moe_scratch(hipStream_t s, int64_t S, int64_t h_cols, int64_t max_seg, MoeSc
 // kGroupedTileRows slots); shorter runs stay on the segment kernels.  Only batches
 // of kGroupedMinSlots or more use it: a grouped block walks all of K, so a few
 // tiles (one 256-slot run: 2 tiles x N/256 blocks) leave the chip idle where the
-// window walk spreads the same run over many blocks.
+// window walk spreads the same run over many blocks.  Batches averaging fewer
+// than kGroupedMinAvgRun slots per expert skip it too: the gate, up and down
+// passes and the silu pass are launched whatever the routing, and with runs that
+// short they rarely find a tile (configuration 3 at M = 512, 10 slots per expert:
+// 252-256 -> 248-250 us per layer).
 constexpr int64_t kGroupedMinRun = 256;
 constexpr int64_t kGroupedMinSlots = 4096;
+constexpr int64_t kGroupedMinAvgRun = 16;
 int64_t grouped_max_tiles(int64_t S, int64_t E) {
-  if (S < kGroupedMinSlots) return 0;
+  if (S < kGroupedMinSlots || S < kGroupedMinAvgRun * E) return 0;
   const int64_t runs = S / kGroupedMinRun < E ? S / kGroupedMinRun : E;
   const int64_t bound = runs == 0 ? 0 : runs + S / fmxq::kGroupedTileRows + 1;
   return bound <= kMaxSegmentsGrid ? bound : 0;  // the work list runs along the grid's y axis

@@ -20,7 +20,9 @@
 #include "../../include/fmxq.h"
 #include "fmxq_host.hpp"
 
-constexpr int kFlagSlots = 64;
+// 16 KiB per device: enough streams that a process sharing a word between two
+// of them is not a practical case.
+constexpr int kFlagSlots = 4096;
 static __device__ __align__(256) uint32_t index_flag[kFlagSlots];
 static __device__ __align__(256) unsigned char scratch[FMXQ_NOALLOC_SCRATCH_BYTES];
 

@@ -249,8 +249,9 @@ int fmxq_route_group_topk(const void* gates, int gates_bf16, const float* bias, 
  * flags are read:
  *   - the stream's own, raised by kernels enqueued on `stream` outside graph
  *     capture (other streams' own flags are neither read nor cleared).  Streams
- *     get these in order of first use, 63 per device; beyond 63 streams on one
- *     device they are shared in turn;
+ *     get these in order of first use, 4095 per device; beyond 4095 streams on
+ *     one device they are shared in turn (two streams sharing a word then see
+ *     each other's errors);
  *   - the device's graph flag, raised by kernels that were captured into a
  *     graph, wherever the graph is replayed (the replay stream is not known at
  *     capture).  Every stream's query reads and clears it, so with graphs
