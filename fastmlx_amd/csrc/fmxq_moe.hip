@@ -67,6 +67,12 @@ __device__ __forceinline__ uint32_t run_pieces(uint32_t c, uint32_t window) {
 // has id E and x row t, and out-of-range routed ids go to bucket E + 1 and are
 // stored as E + 1 in rhs_sorted (so a walk tells the shared expert, id E, from a
 // bad id, above E).
+//
+// STAGED (S + sh_T <= kSortStageSlots): the scatter writes the three sorted
+// arrays to LDS and the block then copies them out in order: one block's
+// scattered 4-byte stores are one cache line each, the copy is coalesced.
+constexpr int64_t kSortStageSlots = 8192;
+template <bool STAGED>
 __global__ __launch_bounds__(1024) void sort_slots_kernel(const uint32_t* __restrict__ inds,
                                                           int64_t S, int64_t sh_T,
                                                           int64_t lhs_div, int64_t E,
@@ -80,6 +86,7 @@ __global__ __launch_bounds__(1024) void sort_slots_kernel(const uint32_t* __rest
                                                           uint32_t* __restrict__ ntile,
                                                           uint32_t long_min, uint32_t tile_rows) {
   extern __shared__ uint32_t cnt[];  // nb counters, then nb cursors
+  __shared__ uint32_t stg[STAGED ? 3 * kSortStageSlots : 1];
   __shared__ uint32_t wsum[16], total;
   const uint32_t bad = (uint32_t)E + (sh_T > 0 ? 1u : 0u);  // bucket of out-of-range ids
   const int64_t nb = (int64_t)bad + 1;
@@ -135,12 +142,22 @@ __global__ __launch_bounds__(1024) void sort_slots_kernel(const uint32_t* __rest
     }
     __syncthreads();  // the scatter below advances cur
   }
+  uint32_t* so = STAGED ? stg : order;
+  uint32_t* sr = STAGED ? stg + kSortStageSlots : rhs_sorted;
+  uint32_t* sl = STAGED ? stg + 2 * kSortStageSlots : lhs_sorted;
   for (int64_t s = threadIdx.x; s < Sa; s += blockDim.x) {
     const uint32_t b = bucket(s);
     const uint32_t pos = atomicAdd(&cur[b], 1u);
-    order[pos] = (uint32_t)s;
-    rhs_sorted[pos] = sh_T > 0 ? b : inds[s];
-    lhs_sorted[pos] = s >= S ? (uint32_t)(s - S) : lhs ? lhs[s] : (uint32_t)(s / lhs_div);
+    so[pos] = (uint32_t)s;
+    sr[pos] = sh_T > 0 ? b : inds[s];
+    sl[pos] = s >= S ? (uint32_t)(s - S) : lhs ? lhs[s] : (uint32_t)(s / lhs_div);
+  }
+  if constexpr (!STAGED) return;
+  __syncthreads();
+  for (int64_t i = threadIdx.x; i < Sa; i += blockDim.x) {
+    order[i] = so[i];
+    rhs_sorted[i] = sr[i];
+    lhs_sorted[i] = sl[i];
   }
 }
 
@@ -238,10 +255,18 @@ hipError_t launch_sort_slots(const uint32_t* inds, int64_t S, int64_t lhs_div, i
   if (tiles && (!seg || !ntile || long_min < 1 || tile_rows < 1)) return hipErrorInvalidValue;
   if (sh_T < 0) return hipErrorInvalidValue;
   const size_t lds = (size_t)(E + 1 + (sh_T > 0 ? 1 : 0)) * 2 * sizeof(uint32_t);
-  sort_slots_kernel<<<1, 1024, lds, stream>>>(inds, S, sh_T, lhs_div, E, order, rhs_sorted,
-                                              lhs_sorted,
-                                              lhs, seg, nseg, window, tiles, ntile,
-                                              (uint32_t)long_min, (uint32_t)tile_rows);
+  // The staged form holds 96 KiB (and a few words) of static LDS; its counters
+  // stay within 56 KiB so the block's total stays below the CU's 160 KiB.
+  if (S + sh_T <= kSortStageSlots && lds <= 56 * 1024)
+    sort_slots_kernel<true><<<1, 1024, lds, stream>>>(inds, S, sh_T, lhs_div, E, order,
+                                                      rhs_sorted, lhs_sorted, lhs, seg, nseg,
+                                                      window, tiles, ntile, (uint32_t)long_min,
+                                                      (uint32_t)tile_rows);
+  else
+    sort_slots_kernel<false><<<1, 1024, lds, stream>>>(inds, S, sh_T, lhs_div, E, order,
+                                                       rhs_sorted, lhs_sorted, lhs, seg, nseg,
+                                                       window, tiles, ntile, (uint32_t)long_min,
+                                                       (uint32_t)tile_rows);
   return hipGetLastError();
 }
 

@@ -516,6 +516,7 @@ def test_switch_glu_many_slots_per_expert_long_rows(gpu, oracle):
     (2, 2100, 2, 256, 256),    # two runs of 2100 slots: 16 full tiles and a partial each
     (3, 2100, 2, 256, 512),    # three runs of ~1400
     (24, 1024, 4, 256, 256),   # Zipf: runs of 838 .. 281 grouped, 239 and below on the walk
+    (2, 8200, 2, 256, 256),    # 16400 slots: more than the sort's LDS staging holds
 ])
 def test_switch_glu_long_runs(gpu, oracle, E, T, k, D, I):
     rng = np.random.default_rng(E * 7 + T + k + D)
