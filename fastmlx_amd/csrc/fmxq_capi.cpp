@@ -310,10 +310,19 @@ int qmm_common(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
     }
     return hip_status(fmxq::launch_qmm_wide(a, wp, flag, s), op);
   }
-  // 9 <= M <= 64 (int4 group 64): qmvw, x shared through LDS and K split over
-  // blocks; at M <= 16 only for wide outputs or long rows, where it beats qmvs.
-  if (M > 8 && M <= fmxq::kQmvwMaxM && (M > 16 || N >= 8192 || K >= 8192) &&
-      fmxq::qmvw_supported(a)) {
+  // qmvw, x shared through LDS and K split over blocks.  int4 group 64 at
+  // 9 <= M <= 64, at M <= 16 only for wide outputs or long rows, where it beats
+  // qmvs.  int8 group 64 (dequantizing walk) from M = 9 on every shape, and from
+  // M = 2 / 3 / 8 on long rows / wide / 4096-row outputs, where it beats the dot2
+  // GEMV (us, dot2 -> walk: 4096x14336 M = 2 21.1 -> 17.1, M = 5 33.4 -> 17.6;
+  // 14336x4096 M = 3 21.0 -> 18.2, M = 5 24.4 -> 18.5 (M = 2 15.4 against 18.1
+  // stays); 4096x4096 M = 8 13.0 -> 9.3 (M = 5 9.4 against 9.3 stays); narrower
+  // outputs keep the GEMV up to M = 8: 1024x4096 M = 8 5.8 against 6.9) and the
+  // prefill GEMM's 64-row tile (M = 9-16 on 4096x4096 16.5-17.3 -> 9.4-9.6).
+  const bool walk4 = bits == 4 && M > 8 && (M > 16 || N >= 8192 || K >= 8192);
+  const bool walk8 = bits == 8 && (M >= 9 || (M >= 2 && K >= 8192) || (M >= 3 && N >= 8192) ||
+                                   (M >= 8 && N >= 4096));
+  if ((walk4 || walk8) && M <= fmxq::kQmvwMaxM && fmxq::qmvw_supported(a)) {
     int cus = 0;
     if (int rc = device_cus(&cus)) return rc;
     const fmxq::QmvwPlan qp = fmxq::qmvw_plan(a, cus);

@@ -102,7 +102,7 @@ bool qmvs_supported(const QmmArgs& a);
 hipError_t launch_qmvs(const QmmArgs& a, hipStream_t stream);
 bool qmv_mfma_supported(const QmmArgs& a);
 hipError_t launch_qmv_mfma(const QmmArgs& a, hipStream_t stream);
-// int4 group-64 product for M <= kQmvwMaxM with x shared through LDS by the waves
+// int4 / int8 group-64 product for M <= kQmvwMaxM with x shared through LDS by the waves
 // of a block and K split over blocks (fmxq_skinny.hip, qmvw_kernel).
 constexpr int kQmvwMaxM = 64;
 struct QmvwPlan {

@@ -73,6 +73,21 @@ __device__ __forceinline__ bf16x8 deq_frag4(uint32_t w, float s, float s16, floa
   return __builtin_bit_cast(bf16x8, r);
 }
 
+// Two 8-bit words (q0..q7, least significant byte of w0 first) dequantized in
+// natural order: the bf16 pairs of w = bf16(fma(s, q, b)), the exact s q + b
+// rounded once; each byte is one v_cvt_f32_ubyteN.
+__device__ __forceinline__ bf16x8 deq_frag8(uint32_t w0, uint32_t w1, float s, float b) {
+  const u32x4 r = {pack_bf16x2(__builtin_fmaf(s, (float)(w0 & 0xffu), b),
+                               __builtin_fmaf(s, (float)((w0 >> 8) & 0xffu), b)),
+                   pack_bf16x2(__builtin_fmaf(s, (float)((w0 >> 16) & 0xffu), b),
+                               __builtin_fmaf(s, (float)(w0 >> 24), b)),
+                   pack_bf16x2(__builtin_fmaf(s, (float)(w1 & 0xffu), b),
+                               __builtin_fmaf(s, (float)((w1 >> 8) & 0xffu), b)),
+                   pack_bf16x2(__builtin_fmaf(s, (float)((w1 >> 16) & 0xffu), b),
+                               __builtin_fmaf(s, (float)(w1 >> 24), b))};
+  return __builtin_bit_cast(bf16x8, r);
+}
+
 // Exponent-trick offset per value and the factor that turns the ones-MFMA sum of
 // the A operand back into sum x (int8 A carries every x value twice).
 template <int BITS>

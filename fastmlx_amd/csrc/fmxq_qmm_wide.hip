@@ -56,19 +56,6 @@ __device__ __forceinline__ constexpr int wait_enc(int vm, int lgkm) {
   return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (lgkm << 8);
 }
 
-// Two 8-bit words (e0..e7) -> 4 bf16 pairs of w = bf16(fma(s, q, b)).
-__device__ __forceinline__ bf16x8 deq8(uint32_t w0, uint32_t w1, float s, float b) {
-  const u32x4 r = {pack_bf16x2(__builtin_fmaf(s, (float)(w0 & 0xffu), b),
-                               __builtin_fmaf(s, (float)((w0 >> 8) & 0xffu), b)),
-                   pack_bf16x2(__builtin_fmaf(s, (float)((w0 >> 16) & 0xffu), b),
-                               __builtin_fmaf(s, (float)(w0 >> 24), b)),
-                   pack_bf16x2(__builtin_fmaf(s, (float)(w1 & 0xffu), b),
-                               __builtin_fmaf(s, (float)((w1 >> 8) & 0xffu), b)),
-                   pack_bf16x2(__builtin_fmaf(s, (float)((w1 >> 16) & 0xffu), b),
-                               __builtin_fmaf(s, (float)(w1 >> 24), b))};
-  return __builtin_bit_cast(bf16x8, r);
-}
-
 template <int BITS, int WAVES, int BM>
 struct WideCfg {
   static constexpr int T = WAVES * 64;           // threads
@@ -250,7 +237,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void qmm_wide_kernel(WideArgs wa) {
           af[j][s] = deq_frag4(wq[set][j][0][s], sb.s[j], sb.s[j] * 0.0625f, sb.b[j]);
         } else {
           const u32x4 v = wq[set][j][s >> 1];
-          af[j][s] = deq8(v[(s & 1) * 2], v[(s & 1) * 2 + 1], sb.s[j], sb.b[j]);
+          af[j][s] = deq_frag8(v[(s & 1) * 2], v[(s & 1) * 2 + 1], sb.s[j], sb.b[j]);
         }
       }
     };

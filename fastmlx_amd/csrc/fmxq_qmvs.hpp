@@ -77,10 +77,10 @@ __device__ __forceinline__ f32x4 qmvs_bias4(float xs, float bo, f32x4 acc) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(xs, bo, acc, 0, 0, 0);
 }
 
-template <int NTT, int SU>
+template <int NTT, int SU, int BITS = 4>
 struct QmvsGeom {
   static constexpr int ROWS = 16 * NTT;
-  static constexpr int RB = SU * 32;           // bytes of one row per step
+  static constexpr int RB = SU * 8 * BITS;     // bytes of one row per step
   static constexpr int LPR = RB / 16;          // lanes per row in one load instruction
   static constexpr int NI = ROWS * RB / 1024;  // load instructions per step
   static constexpr int SPL = (64 / ROWS == 2) ? SU : SU / 2;  // groups per scale load
@@ -116,7 +116,7 @@ __device__ __forceinline__ void qmvs_slice(uint8_t* stage, const uint32_t* const
     int64_t n = nb + r;
     n = n < N ? n : N - 1;
     wq[i] = (uint32_t)((n * wpr + (lane % LPR) * 4) * 4);
-    wo[i] = r * RB + (qmvs_pos<SU>(lane % LPR, r) << 4);
+    wo[i] = r * RB + (qmvs_pos<RB / 32>(lane % LPR, r) << 4);
   }
   __amdgpu_buffer_rsrc_t wres[NMAT];
 #pragma unroll
@@ -304,7 +304,12 @@ constexpr int kXStageRow = 512;
 // with x read in natural order: no Σx MFMAs, no per-group corrections and no x
 // permutation, for 22 VALU per packed word instead of 7.  The word's VALU is
 // shared by the MTW x tiles, so it pays from 2 tiles (17 to 64 x rows).
-template <int MTW, int MT, int NTT, int NMAT, int WV, bool FOLD, bool DEQ = false>
+//
+// BITS = 8 (with DEQ only): 256-byte row slices per step (16-chunk stage rows), and
+// lane (c, q) reads chunk 4 j + q of its row's unit j, the 16 values that its two
+// MFMAs of the unit take (words 0-1 and 2-3, deq_frag8); the x fragments are those
+// of the int4 walk.
+template <int MTW, int MT, int NTT, int NMAT, int WV, bool FOLD, bool DEQ = false, int BITS = 4>
 __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8_t* stage,
                                                __amdgpu_buffer_rsrc_t xres,
                                                const uint32_t (&xo)[8 * MTW / WV], int wave,
@@ -315,15 +320,17 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
                                                int64_t N, int64_t K, int64_t s0, int64_t s1,
                                                f32x4 (&acc)[NMAT][MT][NTT]) {
   constexpr int SU = 4;
-  using G = QmvsGeom<NTT, SU>;
+  using G = QmvsGeom<NTT, SU, BITS>;
   constexpr int NI = G::NI, LPR = G::LPR, RB = G::RB, ROWS = G::ROWS, SPL = G::SPL;
   constexpr int AX = 8 * MTW / WV;
   static_assert(MTW <= MT, "walked tiles");
   static_assert(AX >= 1 && AX * WV == 8 * MTW, "x DMA split over the block's waves");
+  static_assert(BITS == 4 || (BITS == 8 && DEQ), "int8 weights are dequantized");
+  using wv_t = std::conditional_t<BITS == 8, u32x4, u32x2>;
   typedef uint32_t sbv_t __attribute__((ext_vector_type(SPL / 2)));
   const int lane = threadIdx.x & 63;
   const int c16 = lane & 15, q = lane >> 4;
-  const int64_t wpr = K / 8, gpr = K / 64;
+  const int64_t wpr = K * BITS / 32, gpr = K / 64;
 
   // Weights through buffer resources as in qmvs_slice: steps past s1 load zeros
   // without a memory access.
@@ -335,7 +342,7 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
     int64_t n = nb + r;
     n = n < N ? n : N - 1;
     wq[i] = (uint32_t)((n * wpr + (lane % LPR) * 4) * 4);
-    wo[i] = r * RB + (qmvs_pos<SU>(lane % LPR, r) << 4);
+    wo[i] = r * RB + (qmvs_pos<RB / 32>(lane % LPR, r) << 4);
   }
   __amdgpu_buffer_rsrc_t wres[NMAT];
 #pragma unroll
@@ -347,7 +354,8 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
 #pragma unroll
     for (int j = 0; j < SU; ++j) {
       const int r = 16 * t + c16;
-      wr[t][j] = r * RB + (qmvs_pos<SU>(2 * j + (q >> 1), r) << 4) + (q & 1) * 8;
+      wr[t][j] = BITS == 8 ? r * RB + (qmvs_pos<RB / 32>(4 * j + q, r) << 4)
+                           : r * RB + (qmvs_pos<RB / 32>(2 * j + (q >> 1), r) << 4) + (q & 1) * 8;
     }
   // Scale/bias loads.  16-row tiles (NTT = 1): one 8-byte load per lane covers two
   // steps (lane -> row l % 16, kind (l / 16) & 1 (scales, biases), step l / 32 of
@@ -387,7 +395,7 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
       for (int i = 0; i < NI; ++i)
         wbuf[d][p][i] = __builtin_bit_cast(
             u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                       wres[p], past ? (int)0x80000000u : (int)(wq[i] + (uint32_t)st * SU * 32), 0,
+                       wres[p], past ? (int)0x80000000u : (int)(wq[i] + (uint32_t)st * RB), 0,
                        2 /* nt */));
       if constexpr (!PAIR) sbuf[d][p] = *reinterpret_cast<const sbv_t*>(sbrow[p] + st * SU);
     }
@@ -437,14 +445,14 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
 #pragma unroll
       for (int i = 0; i < NI; ++i)
         *reinterpret_cast<u32x4*>(stage + p * G::STAGE + wo[i]) = wbuf[e][p][i];
-    u32x2 wv[SU][NMAT][NTT];
+    wv_t wv[SU][NMAT][NTT];
 #pragma unroll
     for (int j = 0; j < SU; ++j)
 #pragma unroll
       for (int p = 0; p < NMAT; ++p)
 #pragma unroll
         for (int t = 0; t < NTT; ++t)
-          wv[j][p][t] = *reinterpret_cast<const u32x2*>(stage + p * G::STAGE + wr[t][j]);
+          wv[j][p][t] = *reinterpret_cast<const wv_t*>(stage + p * G::STAGE + wr[t][j]);
     uint32_t sv[NMAT][NTT][SU / 2], bv[NMAT][NTT][SU / 2];
     if constexpr (PAIR) {
       if constexpr (e == 0) {
@@ -499,8 +507,14 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
           for (int t = 0; t < NTT; ++t) {
             const float s = (j & 1) ? bf16_hi(sv[p][t][j >> 1]) : bf16_lo(sv[p][t][j >> 1]);
             const float b = (j & 1) ? bf16_hi(bv[p][t][j >> 1]) : bf16_lo(bv[p][t][j >> 1]);
-            const bf16x8 B0 = deq_frag4(wv[j][p][t][0], s, s * 0.0625f, b);
-            const bf16x8 B1 = deq_frag4(wv[j][p][t][1], s, s * 0.0625f, b);
+            bf16x8 B0, B1;
+            if constexpr (BITS == 8) {
+              B0 = deq_frag8(wv[j][p][t][0], wv[j][p][t][1], s, b);
+              B1 = deq_frag8(wv[j][p][t][2], wv[j][p][t][3], s, b);
+            } else {
+              B0 = deq_frag4(wv[j][p][t][0], s, s * 0.0625f, b);
+              B1 = deq_frag4(wv[j][p][t][1], s, s * 0.0625f, b);
+            }
 #pragma unroll
             for (int mt = 0; mt < MTW; ++mt) {
               acc[p][mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mt][0], B0, acc[p][mt][t], 0, 0, 0);
@@ -579,24 +593,27 @@ __device__ __forceinline__ void qmvs_walk_xlds(uint8_t* xs0, uint8_t* xs1, uint8
 // step.  Steps d with s0 + d >= s1 load from clamped
 // addresses (weights from an offset past the buffer, which reads zeros without
 // a memory access) and are not computed.
-// DEQ: the weights dequantized and x in natural order, as in qmvs_walk_xlds.
-template <int MT, int NTT, int WV, int D, bool DEQ = false>
+// DEQ: the weights dequantized and x in natural order, as in qmvs_walk_xlds, and
+// BITS = 8 with it as there.
+template <int MT, int NTT, int WV, int D, bool DEQ = false, int BITS = 4>
 __device__ __forceinline__ void qmvs_walk_xall(uint8_t* xs, uint8_t* stage, __amdgpu_buffer_rsrc_t xres,
                                                const uint32_t (&xo)[8 * MT / WV], int wave,
                                                const uint32_t* w, const uint16_t* sc,
                                                const uint16_t* bi, int64_t nb, int64_t N, int64_t K,
                                                int64_t s0, int64_t s1, f32x4 (&acc)[MT][NTT]) {
   constexpr int SU = 4;
-  using G = QmvsGeom<NTT, SU>;
+  using G = QmvsGeom<NTT, SU, BITS>;
   constexpr int NI = G::NI, LPR = G::LPR, RB = G::RB, ROWS = G::ROWS, SPL = G::SPL;
   constexpr int AX = 8 * MT / WV;
   constexpr int XSLOT = 16 * MT * kXStageRow;
   static_assert(AX >= 1 && AX * WV == 8 * MT, "x DMA split over the block's waves");
   static_assert(D >= 1 && D * NI < 64, "vmcnt range");
+  static_assert(BITS == 4 || (BITS == 8 && DEQ), "int8 weights are dequantized");
+  using wv_t = std::conditional_t<BITS == 8, u32x4, u32x2>;
   typedef uint32_t sbv_t __attribute__((ext_vector_type(SPL / 2)));
   const int lane = threadIdx.x & 63;
   const int c16 = lane & 15, q = lane >> 4;
-  const int64_t wpr = K / 8, gpr = K / 64;
+  const int64_t wpr = K * BITS / 32, gpr = K / 64;
   if (s1 <= s0) return;
 
   uint32_t wq[NI];
@@ -607,7 +624,7 @@ __device__ __forceinline__ void qmvs_walk_xall(uint8_t* xs, uint8_t* stage, __am
     int64_t n = nb + r;
     n = n < N ? n : N - 1;
     wq[i] = (uint32_t)((n * wpr + (lane % LPR) * 4) * 4);
-    wo[i] = r * RB + (qmvs_pos<SU>(lane % LPR, r) << 4);
+    wo[i] = r * RB + (qmvs_pos<RB / 32>(lane % LPR, r) << 4);
   }
   const __amdgpu_buffer_rsrc_t wres =
       __builtin_amdgcn_make_buffer_rsrc((void*)w, (short)0, (int)(N * wpr * 4), 0x00020000);
@@ -617,7 +634,8 @@ __device__ __forceinline__ void qmvs_walk_xall(uint8_t* xs, uint8_t* stage, __am
 #pragma unroll
     for (int j = 0; j < SU; ++j) {
       const int r = 16 * t + c16;
-      wr[t][j] = r * RB + (qmvs_pos<SU>(2 * j + (q >> 1), r) << 4) + (q & 1) * 8;
+      wr[t][j] = BITS == 8 ? r * RB + (qmvs_pos<RB / 32>(4 * j + q, r) << 4)
+                           : r * RB + (qmvs_pos<RB / 32>(2 * j + (q >> 1), r) << 4) + (q & 1) * 8;
     }
   // Scale/bias words as in qmvs_slice: lane -> row l % ROWS, kind (l / ROWS) & 1,
   // and for 16-row tiles which half of the step's groups (l / ROWS / 2).
@@ -660,7 +678,7 @@ __device__ __forceinline__ void qmvs_walk_xall(uint8_t* xs, uint8_t* stage, __am
     for (int i = 0; i < NI; ++i)
       wbuf[d][i] = __builtin_bit_cast(
           u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                     wres, past ? (int)0x80000000u : (int)(wq[i] + (uint32_t)st * SU * 32), 0,
+                     wres, past ? (int)0x80000000u : (int)(wq[i] + (uint32_t)st * RB), 0,
                      2 /* nt */));
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -676,12 +694,12 @@ __device__ __forceinline__ void qmvs_walk_xall(uint8_t* xs, uint8_t* stage, __am
 #pragma unroll
     for (int i = 0; i < NI; ++i)
       *reinterpret_cast<u32x4*>(stage + wo[i]) = wbuf[d][i];
-    u32x2 wv[SU][NTT];
+    wv_t wv[SU][NTT];
 #pragma unroll
     for (int j = 0; j < SU; ++j)
 #pragma unroll
       for (int t = 0; t < NTT; ++t)
-        wv[j][t] = *reinterpret_cast<const u32x2*>(stage + wr[t][j]);
+        wv[j][t] = *reinterpret_cast<const wv_t*>(stage + wr[t][j]);
     uint32_t sv[NTT][SU / 2], bv[NTT][SU / 2];
 #pragma unroll
     for (int t = 0; t < NTT; ++t)
@@ -707,8 +725,14 @@ __device__ __forceinline__ void qmvs_walk_xall(uint8_t* xs, uint8_t* stage, __am
         for (int t = 0; t < NTT; ++t) {
           const float sf = (j & 1) ? bf16_hi(sv[t][j >> 1]) : bf16_lo(sv[t][j >> 1]);
           const float bf = (j & 1) ? bf16_hi(bv[t][j >> 1]) : bf16_lo(bv[t][j >> 1]);
-          const bf16x8 B0 = deq_frag4(wv[j][t][0], sf, sf * 0.0625f, bf);
-          const bf16x8 B1 = deq_frag4(wv[j][t][1], sf, sf * 0.0625f, bf);
+          bf16x8 B0, B1;
+          if constexpr (BITS == 8) {
+            B0 = deq_frag8(wv[j][t][0], wv[j][t][1], sf, bf);
+            B1 = deq_frag8(wv[j][t][2], wv[j][t][3], sf, bf);
+          } else {
+            B0 = deq_frag4(wv[j][t][0], sf, sf * 0.0625f, bf);
+            B1 = deq_frag4(wv[j][t][1], sf, sf * 0.0625f, bf);
+          }
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
             acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[mt][0], B0, acc[mt][t], 0, 0, 0);

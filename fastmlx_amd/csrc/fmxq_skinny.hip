@@ -379,10 +379,14 @@ constexpr int kQmvwDeqMinMT = FMXQ_QMVW_DEQ_MIN_MT;
 #endif
 constexpr int kQmvwXallDeqMinMT = FMXQ_QMVW_XALL_DEQ_MIN_MT;
 
-template <int MT, int NTT, int WV, int D>
+// int8 weights (BITS = 8) always take the dequantizing walks (there is no
+// exponent-trick form for 8-bit values).
+template <int MT, int NTT, int WV, int D, int BITS = 4>
 __global__ __launch_bounds__(WV * 64) __attribute__((amdgpu_waves_per_eu(MT == 1 && NTT == 1 ? 3 : 2)))
 void qmvw_kernel(QmmArgs a) {
-  using G = QmvsGeom<NTT, 4>;
+  using G = QmvsGeom<NTT, 4, BITS>;
+  constexpr bool kDeqXlds = BITS == 8 || MT >= kQmvwDeqMinMT;
+  constexpr bool kDeqXall = BITS == 8 || MT >= kQmvwXallDeqMinMT;
   constexpr int AX = 8 * MT / WV;
   constexpr int XSLOTS = D > 0 ? D : 2;
   __shared__ __attribute__((aligned(1024))) uint8_t xs[XSLOTS][16 * MT * kXStageRow];
@@ -416,14 +420,14 @@ void qmvw_kernel(QmmArgs a) {
 #pragma unroll
     for (int t = 0; t < NTT; ++t) acc[0][mt][t] = f32x4{};
   if constexpr (D > 0) {
-    qmvs_walk_xall<MT, NTT, WV, D, (MT >= kQmvwXallDeqMinMT)>(&xs[0][0], stage[wave], xres, xo, wave,
+    qmvs_walk_xall<MT, NTT, WV, D, kDeqXall, BITS>(&xs[0][0], stage[wave], xres, xo, wave,
                                                               a.w, a.scales, a.biases,
                                    nb, a.N, a.K, s0, s1, acc[0]);
   } else {
     const uint32_t* const w[1] = {a.w};
     const uint16_t* const sc[1] = {a.scales};
     const uint16_t* const bi[1] = {a.biases};
-    qmvs_walk_xlds<MT, MT, NTT, 1, WV, false, (MT >= kQmvwDeqMinMT)>(xs[0], xs[1], stage[wave], xres, xo,
+    qmvs_walk_xlds<MT, MT, NTT, 1, WV, false, kDeqXlds, BITS>(xs[0], xs[1], stage[wave], xres, xo,
                                                                      wave, a.M, w, sc, bi,
                                        nb, a.N, a.K, s0, s1, acc);
   }
@@ -491,7 +495,13 @@ template <int MT, int NTT, int WV, int D>
 hipError_t launch_qmvw_cfg(const QmmArgs& a, hipStream_t stream) {
   const int parts = a.splits > 1 ? a.splits : 1;
   const dim3 grid((unsigned)((a.N + 16 * NTT * WV - 1) / (16 * NTT * WV)), (unsigned)parts);
-  qmvw_kernel<MT, NTT, WV, D><<<grid, WV * 64, 0, stream>>>(a);
+  if (a.bits == 8) {
+    // int8: 16-row W tiles, pipelined walk only (qmvw_plan)
+    if constexpr (NTT == 1 && D == 0) qmvw_kernel<MT, 1, WV, 0, 8><<<grid, WV * 64, 0, stream>>>(a);
+    else return hipErrorInvalidValue;
+  } else {
+    qmvw_kernel<MT, NTT, WV, D><<<grid, WV * 64, 0, stream>>>(a);
+  }
   if (parts > 1) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -524,8 +534,8 @@ bool qmvw_supported(const QmmArgs& a) {
   auto al = [](const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0; };
   // K a multiple of 256 (whole steps; 8-byte scale loads stay aligned).  Weights
   // and x go through buffer resources: their byte sizes must stay below 2^31.
-  return a.bits == 4 && a.group_size == 64 && a.M >= 1 && a.M <= kQmvwMaxM && a.K % 256 == 0 &&
-         a.N * (a.K / 2) < (int64_t(1) << 31) &&
+  return (a.bits == 4 || a.bits == 8) && a.group_size == 64 && a.M >= 1 && a.M <= kQmvwMaxM &&
+         a.K % 256 == 0 && a.N * (a.K * a.bits / 8) < (int64_t(1) << 31) &&
          ((a.M - 1) * a.ldx + a.K) * 2 < (int64_t(1) << 31) && a.ldx % 8 == 0 &&
          al(a.x, 16) && al(a.w, 16) && al(a.scales, 8) && al(a.biases, 8);
 }
@@ -563,6 +573,12 @@ QmvwPlan qmvw_plan(const QmmArgs& a, int cus) {
     parts = 8;
     p.d = 2;
   }
+  if (a.bits == 8) {
+    // int8: 16-row W tiles and the pipelined walk (the up-front one would hold
+    // twice the weight registers).
+    p.ntt = 1;
+    p.d = 0;
+  }
   const int64_t rows = 16 * p.ntt * p.wv;
   const int64_t rblocks = (a.N + rows - 1) / rows;
   const int64_t enough = (2 * (int64_t)cus + rblocks - 1) / rblocks;
@@ -581,7 +597,8 @@ hipError_t launch_qmvw(const QmmArgs& a, const QmvwPlan& p, hipStream_t stream) 
     return hipErrorInvalidValue;
   // The upfront walk holds at most d steps: every part must fit.
   if (p.wv != 4 || (p.mt == 4 && p.ntt != 1) ||
-      (p.d > 0 && ((a.K / 256 + p.parts - 1) / p.parts > p.d || (p.mt == 4 && p.d > 2))))
+      (p.d > 0 && ((a.K / 256 + p.parts - 1) / p.parts > p.d || (p.mt == 4 && p.d > 2))) ||
+      (a.bits == 8 && (p.ntt != 1 || p.d != 0)))
     return hipErrorInvalidValue;
   if (p.mt == 1) return launch_qmvw_mt<1>(a, p.ntt, p.d, stream);
   if (p.mt == 2) return launch_qmvw_mt<2>(a, p.ntt, p.d, stream);

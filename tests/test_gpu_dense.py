@@ -128,18 +128,19 @@ def test_qmm_mfma_shapes(gpu, oracle, M, bits):
 @pytest.mark.parametrize("N,K", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (1024, 16384)])
 def test_int8_small_m_shapes(gpu, oracle, M, N, K):
     """int8 at 1 <= M <= 8: the register GEMV (at M >= 5 only M of its 8 x-row
-    slots built) for M <= 6 and up to 4096 output rows, the prefill GEMM's 64-row
-    tile for M = 7, 8 beyond; rows of 14336 and 16384 values take the register
-    GEMV's eight-slice, two-chunk form at M = 1 to 5 and the tile at M = 6 to 8."""
+    slots built) on the narrower outputs and at M = 1 (rows of 14336 and 16384
+    values in its eight-slice, two-chunk form), and the dequantizing skinny walk on
+    long rows from M = 2, on 14336 outputs from M = 3 and on 4096 outputs at M = 8."""
     _qmm_case(gpu, oracle, M, N, K, 8, 64, seed=14000 + M + N // 1024)
 
 
-@pytest.mark.parametrize("M,N,K,bits", [(6, 1024, 14336, 4), (7, 1000, 8192, 4),
-                                         (5, 2048, 8192, 8), (6, 3000, 4096, 8)])
-def test_register_gemv_partial_rows(gpu, oracle, M, N, K, bits):
+@pytest.mark.parametrize("M,N,K,bits,group", [(6, 1024, 14336, 4, 64), (7, 1000, 8192, 4, 64),
+                                               (5, 2048, 9216, 8, 32), (6, 3000, 4096, 8, 64)])
+def test_register_gemv_partial_rows(gpu, oracle, M, N, K, bits, group):
     """The register GEMV with 5..7 of its 8 x-row slots built, on the 8-slice form
-    of long rows and on ragged row counts."""
-    _qmm_case(gpu, oracle, M, N, K, bits, 64, seed=15000 + M * 7 + N + K + bits)
+    of long rows and on ragged row counts (int8 long rows in group 32, which the
+    int8 skinny walk does not take)."""
+    _qmm_case(gpu, oracle, M, N, K, bits, group, seed=15000 + M * 7 + N + K + bits)
 
 
 def test_qmm_ragged_n(gpu, oracle):
@@ -250,6 +251,34 @@ def test_qmvw_parts_and_walks(gpu, oracle, M, N, K, bias):
     dx, dw, ds, db = (to_dev(t, gpu) for t in (x, w, s, b))
     r1 = to_np(ops.quantized_matmul(dx, dw, ds, db, True, 64, 4))
     r2 = to_np(ops.quantized_matmul(dx, dw, ds, db, True, 64, 4))
+    torch.cuda.synchronize()
+    assert np.array_equal(r1, r2)
+
+
+@pytest.mark.parametrize("M", [9, 16, 17, 32, 33, 64])
+@pytest.mark.parametrize("N,K,bias", [
+    (8200, 1024, False),  # wide: parts of one step, ragged N
+    (4100, 2048, True),   # 4 parts of two steps, ragged last row block, bias in the fixup
+    (2050, 8192, False),  # long rows: 8 parts of four steps, N % 4 != 0 (scalar fixup)
+    (4096, 7936, False),  # 31 steps: uneven parts, an odd step count
+    (130, 256, True),     # one step: a single part stores bf16 directly
+])
+def test_qmvw_int8(gpu, oracle, M, N, K, bias):
+    """The int8 group-64 skinny walk (qmvw with BITS = 8, weights dequantized to
+    bf16 in 256-byte row slices per step), on every x-tile count and part plan it
+    takes, including shapes whose M <= 16 rows stay off it; two calls in a row
+    agree exactly."""
+    rows = np.unique(np.array([0, 1, M // 2, M - 2, M - 1]))
+    _qmm_case(gpu, oracle, M, N, K, 8, 64, seed=9600 + M * 5 + N + K, rows_checked=rows,
+              bias=bias)
+    from fastmlx_amd import ops
+
+    rng = np.random.default_rng(2)
+    w, s, b = make_quant(rng, (N,), K, 8, 64)
+    x = make_x(rng, M, K)
+    dx, dw, ds, db = (to_dev(t, gpu) for t in (x, w, s, b))
+    r1 = to_np(ops.quantized_matmul(dx, dw, ds, db, True, 64, 8))
+    r2 = to_np(ops.quantized_matmul(dx, dw, ds, db, True, 64, 8))
     torch.cuda.synchronize()
     assert np.array_equal(r1, r2)
 
