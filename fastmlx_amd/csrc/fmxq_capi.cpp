@@ -332,10 +332,13 @@ int qmm_common(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
     }
     return hip_status(fmxq::launch_qmvw(a, qp, s), op);
   }
-  // M <= 4: dot2 GEMV.  Other M <= 32: qmvs, except that narrow outputs (N < 2048)
+  // M <= 2: dot2 GEMV.  M = 3, 4: qmvs on outputs of 4096 rows or more (C1 stack,
+  // 224 products, whose 1024-row k and v stay on the dot2 GEMV: M = 3 2.11 ->
+  // 1.92 ms, M = 4 2.12 -> 1.97 ms; at M = 2 it lost, 1.56 -> 1.86 ms), the dot2
+  // GEMV otherwise.  Other M <= 32: qmvs, except that narrow outputs (N < 2048)
   // at M <= 8 stay on the dot2 GEMV, which is quicker there.
-  const bool skinny = M > fmxq::kQmvMaxM && M <= fmxq::kSkinnyMaxM && fmxq::qmvs_supported(a) &&
-                      !(M <= 8 && N < 2048 && fmxq::qmv_supported(a));
+  const bool skinny = (M > fmxq::kQmvMaxM || (M >= 3 && N >= 4096)) && M <= fmxq::kSkinnyMaxM &&
+                      fmxq::qmvs_supported(a) && !(M <= 8 && N < 2048 && fmxq::qmv_supported(a));
   if (skinny) return hip_status(fmxq::launch_qmvs(a, s), op);
   // 5 <= M <= 32 shapes qmvs does not take (int8, other group sizes) run on the
   // prefill GEMM's 64-row tile; M <= 4 stays on the dot2 GEMV, and so do int8

@@ -88,7 +88,8 @@ struct IndexMap {
 hipError_t launch_broadcast_index(const void* src, const IndexMap& m, uint32_t* out, int64_t n,
                                   hipStream_t stream);
 
-// Bandwidth-bound decode GEMV without MFMA: every M <= kQmvMaxM, and M <= 8
+// Bandwidth-bound decode GEMV without MFMA: every M <= kQmvMaxM (int4 group 64
+// at M = 3, 4 with 4096 or more outputs takes the MFMA walk instead), and M <= 8
 // where the x rows fit in registers (qmv_supported).
 constexpr int kQmvMaxM = 4;
 bool qmv_supported(const QmmArgs& a);

@@ -196,7 +196,7 @@ def test_skinny_mfma_rows_and_groups(gpu, oracle, M, bits, group, K):
     _qmm_case(gpu, oracle, M, 333, K, bits, group, seed=900 + M * 3 + bits + group)
 
 
-@pytest.mark.parametrize("M", [5, 8, 9, 16, 17, 32])
+@pytest.mark.parametrize("M", [3, 4, 5, 8, 9, 16, 17, 32])
 @pytest.mark.parametrize("N,K", [
     (8200, 1024),   # 32-row blocks (N >= 8192), ragged N, one 4-unit step per wave
     (2100, 8192),   # 16-row blocks with 8-unit steps, ragged N
@@ -206,7 +206,8 @@ def test_skinny_mfma_rows_and_groups(gpu, oracle, M, bits, group, K):
 ])
 def test_qmvs_blocks_and_steps(gpu, oracle, M, N, K):
     """The int4 group-64 skinny GEMV (qmvs): both block heights, both step sizes,
-    slices with no steps or an odd number of them, one and two 16-row x tiles."""
+    slices with no steps or an odd number of them, one and two 16-row x tiles;
+    M = 3 and 4 take it on 4096 or more outputs (the dot2 GEMV below that)."""
     _qmm_case(gpu, oracle, M, N, K, 4, 64, seed=9100 + M * 7 + N + K)
 
 
