@@ -203,8 +203,14 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
        i += (int64_t)gridDim.x * 256) {
     const int64_t t = i / pairs, d = (i - t * pairs) * 2;
     float a0 = 0.f, a1 = 0.f;
-    // Up to 16 expert rows are requested before any is summed (the sum still runs
-    // in j order).
+    // The shared term's loads go first, then up to 16 expert rows are requested
+    // before any is summed (the sum still runs in j order).
+    uint32_t sv = 0;
+    uint16_t sgb = 0;
+    if (shared) {
+      sv = *reinterpret_cast<const uint32_t*>(shared + t * D + d);
+      if (sgate) sgb = sgate[t];
+    }
     for (int64_t j0 = 0; j0 < topk; j0 += 16) {
       uint32_t v[16];
       uint16_t wb[16];
@@ -226,10 +232,9 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
     a0 = r16(a0);
     a1 = r16(a1);
     if (shared) {
-      const uint32_t sv = *reinterpret_cast<const uint32_t*>(shared + t * D + d);
       float s0 = bf16_lo(sv), s1 = bf16_hi(sv);
       if (sgate) {
-        const float gt = r16(1.f / (1.f + __expf(-bf16_bits_to_f32(sgate[t]))));
+        const float gt = r16(1.f / (1.f + __expf(-bf16_bits_to_f32(sgb))));
         s0 = r16(gt * s0);
         s1 = r16(gt * s1);
       }
