@@ -579,6 +579,13 @@ QmvwPlan qmvw_plan(const QmmArgs& a, int cus) {
     p.ntt = 1;
     p.d = 0;
   }
+  // 64-row x tiles on the pipelined walk: 8-wave blocks of 128 weight rows, so
+  // each x step DMA'd into LDS serves twice the weights (33-64 rows, against 4
+  // waves: 14336x4096 M = 33 / 48 / 64 22.3 / 23.3 / 24.0 -> 20.6 / 22.3 / 24.4
+  // us, 4096x14336 21.5 / 22.2 / 23.5 -> 19.9 / 21.8 / 23.0 us; int8 M = 64
+  // 26.5 / 26.2 -> 25.8 / 25.4 us).  16- and 32-row tiles stay at 4 waves (int8
+  // at M = 17-24 on 14336x4096 lost 12% with 8).
+  if (p.mt == 4 && p.ntt == 1 && p.d == 0) p.wv = 8;
   const int64_t rows = 16 * p.ntt * p.wv;
   const int64_t rblocks = (a.N + rows - 1) / rows;
   const int64_t enough = (2 * (int64_t)cus + rblocks - 1) / rblocks;
@@ -596,14 +603,15 @@ hipError_t launch_qmvw(const QmmArgs& a, const QmvwPlan& p, hipStream_t stream) 
       (p.parts > 1 && (!a.ws || a.splits != p.parts)))
     return hipErrorInvalidValue;
   // The upfront walk holds at most d steps: every part must fit.
-  if (p.wv != 4 || (p.mt == 4 && p.ntt != 1) ||
+  if ((p.wv != 4 && !(p.wv == 8 && p.mt == 4 && p.d == 0)) || (p.mt == 4 && p.ntt != 1) ||
       (p.d > 0 && ((a.K / 256 + p.parts - 1) / p.parts > p.d || (p.mt == 4 && p.d > 2))) ||
       (a.bits == 8 && (p.ntt != 1 || p.d != 0)))
     return hipErrorInvalidValue;
   if (p.mt == 1) return launch_qmvw_mt<1>(a, p.ntt, p.d, stream);
   if (p.mt == 2) return launch_qmvw_mt<2>(a, p.ntt, p.d, stream);
   // 64-row x tiles use 16-row W tiles only (32-row ones would spill), and at most
-  // two up-front steps (LDS).
+  // two up-front steps (LDS); the pipelined walk runs 8-wave blocks.
+  if (p.wv == 8) return launch_qmvw_cfg<4, 1, 8, 0>(a, stream);
   return launch_qmvw_mt<4>(a, 1, p.d, stream);
 }
 
