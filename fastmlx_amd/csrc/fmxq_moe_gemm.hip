@@ -296,8 +296,10 @@ template <int MT, int NTT, int NMAT>
 static hipError_t launch_wc(const MoeArgs& a, int wc, int64_t max_seg, hipStream_t stream) {
   const int64_t cols = 16 * NTT * wc;
   dim3 grid((unsigned)((a.N + cols - 1) / cols), (unsigned)max_seg);
-  // Four waves per block: an 8-wave block (128 columns per x fetch, one block
-  // per CU) measured slower (configuration 4 at M=256: 1871 -> 1971 us).
+  // Four waves per block: an 8-wave block (128 columns per x fetch, two blocks
+  // per CU) measured slower (configuration 4 at M=256: 1871 -> 1971 us, and again
+  // with the dequantizing walk: 1463-1478 -> 1553-1604 us; at M=32 with one-tile
+  // segments too: 556-561 -> 620 us), unlike the dense walk's 64-row tiles.
   if (wc == 4 && moe_xlds_supported(a)) moe_qmvw_kernel<MT, NTT, NMAT, 4><<<grid, 256, 0, stream>>>(a);
   else if (wc == 1) moe_qmvs_kernel<MT, NTT, 1, NMAT><<<grid, 256, 0, stream>>>(a);
   else if (wc == 2) moe_qmvs_kernel<MT, NTT, 2, NMAT><<<grid, 256, 0, stream>>>(a);
