@@ -41,8 +41,9 @@
 //
 // qmvw_kernel (int4, group 64, 9 <= M <= 64 where it wins: M > 16, or wide
 // outputs / long rows at M <= 16):
-//   - the same 16x16x32 tile walk, but the WV = 4 waves of a block own 4 W tiles
-//     side by side over one K part and share the block's x rows, which the block
+//   - the same 16x16x32 tile walk, but the WV waves of a block (4; 8 for 64-row
+//     x tiles on the pipelined walk) own WV W tiles side by side over one K part
+//     and share the block's x rows, which the block
 //     DMAs into LDS (buffer_load ... lds) once per step: qmvs reads x once per
 //     wave, and at M = 16 that is twice the weight bytes through the texture
 //     units (isolating the two streams on MI355X: x, not the weights, set the
