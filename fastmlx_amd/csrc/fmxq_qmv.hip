@@ -505,9 +505,9 @@ static hipError_t launch_qmv1_slice_cfg(const QmmArgs& a, hipStream_t stream) {
 
 // Shapes where the slice kernel beats qmv1_kernel (graphs of launches over
 // distinct weight copies): 14336-deep rows (8.2 -> 7.7 us for 4096 x 14336) and
-// K = 4096 up to 16384 rows (4.2 -> 3.9 us for 4096 x 4096; 8.1 -> 7.8 us for
-// 14336 x 4096 once the scales load as block runs).  28672 x 4096 measures the
-// same on both and stays on qmv1_kernel.
+// K = 4096 at every height (4.2 -> 3.9 us for 4096 x 4096; 8.1 -> 7.8 us for
+// 14336 x 4096 once the scales load as block runs; 28672 x 4096 12.4-12.8 ->
+// 12.1 us; the 128256 x 4096 tied head 47.7-48.4 -> 43.7-44.4 us, 85% of HBM).
 static hipError_t launch_qmv1_slice(const QmmArgs& a, hipStream_t stream) {
   if (a.M != 1 || a.bits != 4 || a.group_size != 64 || a.K % 2048 != 0 ||
       a.N >= (int64_t(1) << 31))
@@ -522,7 +522,6 @@ static hipError_t launch_qmv1_slice(const QmmArgs& a, hipStream_t stream) {
     case 7: return launch_qmv1_slice_cfg<8, 7, 1>(a, stream);
     case 8: return launch_qmv1_slice_cfg<8, 8, 1>(a, stream);
     case 2:
-      if (a.N > 16384) return hipErrorNotSupported;
       return a.N >= 2048 ? launch_qmv1_slice_cfg<8, 2, 2>(a, stream)
                          : launch_qmv1_slice_cfg<2, 2, 2>(a, stream);
     default: return hipErrorNotSupported;
