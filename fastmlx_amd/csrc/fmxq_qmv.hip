@@ -503,8 +503,8 @@ static hipError_t launch_qmv1_slice_cfg(const QmmArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// Shapes where the slice kernel beats qmv1_kernel (graphs of launches over
-// distinct weight copies): 14336-deep rows (8.2 -> 7.7 us for 4096 x 14336) and
+// Shapes where the slice kernel beats qmv1_kernel or the qmvx GEMV (graphs of
+// launches over distinct weight copies): 2048-deep rows (below), 14336-deep rows (8.2 -> 7.7 us for 4096 x 14336) and
 // K = 4096 at every height (4.2 -> 3.9 us for 4096 x 4096; 8.1 -> 7.8 us for
 // 14336 x 4096 once the scales load as block runs; 28672 x 4096 12.4-12.8 ->
 // 12.1 us; the 128256 x 4096 tied head 47.7-48.4 -> 43.7-44.4 us, 85% of HBM).
@@ -516,6 +516,11 @@ static hipError_t launch_qmv1_slice(const QmmArgs& a, hipStream_t stream) {
       (reinterpret_cast<uintptr_t>(a.x) & 15u) || (reinterpret_cast<uintptr_t>(a.w) & 15u))
     return hipErrorNotSupported;
   switch (a.K / 2048) {
+    // One slice (2048-deep rows): 2 rows per wave, 4 waves per block, no cross-slice
+    // sum (against the qmvx GEMV: 2048 x 2048 2.89 -> 2.60 us, 512 x 2048 2.54 ->
+    // 2.25 us, 8192 x 2048 4.20 -> 4.07 us; 1 or 4 rows per wave, or 2 waves per
+    // block, measured in between).
+    case 1: return launch_qmv1_slice_cfg<2, 1, 4>(a, stream);
     case 4: return launch_qmv1_slice_cfg<8, 4, 1>(a, stream);
     case 5: return launch_qmv1_slice_cfg<8, 5, 1>(a, stream);
     case 6: return launch_qmv1_slice_cfg<8, 6, 1>(a, stream);
