@@ -527,6 +527,11 @@ static hipError_t launch_qmv1_slice(const QmmArgs& a, hipStream_t stream) {
     case 7: return launch_qmv1_slice_cfg<8, 7, 1>(a, stream);
     case 8: return launch_qmv1_slice_cfg<8, 8, 1>(a, stream);
     case 2:
+      // 4 rows per wave from 8192 to 32767 outputs (14336 x 4096 7.64-7.98 ->
+      // 7.45-7.49 us, the C1 stack at M = 1 1.178 -> 1.165 ms); 8 below and above
+      // (4096 x 4096 3.80 against 4.01 us, the 128256-row head 44.0-44.4 against
+      // 45.1 us).
+      if (a.N >= 8192 && a.N < 32768) return launch_qmv1_slice_cfg<4, 2, 2>(a, stream);
       return a.N >= 2048 ? launch_qmv1_slice_cfg<8, 2, 2>(a, stream)
                          : launch_qmv1_slice_cfg<2, 2, 2>(a, stream);
     default: return hipErrorNotSupported;

@@ -219,6 +219,8 @@ def test_qmvs_blocks_and_steps(gpu, oracle, M, N, K):
     (2056, 4096, True),    # two slices x two 8-row groups per block, ragged
     (1001, 4096, False),   # two slices x two 2-row groups per block
     (28680, 4096, False),  # two slices on a tall matrix (rows past 16384), ragged
+    (8196, 4096, True),    # two slices of 4-row waves (8192 to 32767 outputs), ragged
+    (32776, 4096, False),  # two slices of 8-row waves again past 32767 outputs
     (2050, 2048, True),    # one slice (2048-deep rows), ragged rows, bias epilogue
     (77, 2048, False),     # one slice, fewer rows than one block's eight
     (520, 6144, False),    # three slices: not taken by the slice kernel
