@@ -636,7 +636,7 @@ def main():
         traffic = profile_value(ROOF_PMC, "traffic_bytes_per_launch")
         roof = {"bound": "hbm", "achieved": nd["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": nd["frac_hbm"], "traffic": None if traffic is None else int(traffic),
-                "kernel": "fmxq::qmv1_slice_kernel<8,7,1> (4-bit 4096x14336, M=1: the "
+                "kernel": "fmxq::qmv1_slice_kernel<16,7,1> (4-bit 4096x14336, M=1: the "
                           "north-star decode GEMV, the C1 down projection)",
                 "bytes_per_launch": by_dn, "us_per_launch": nd["us"],
                 "timing": "HIP events around a graph of %d back-to-back launches cycling over "

@@ -38,9 +38,9 @@
 
 int main(int argc, char** argv) {
   const int64_t N = argc > 1 ? std::atol(argv[1]) : 4096, K = argc > 2 ? std::atol(argv[2]) : 14336;
-  // qmv1_slice_kernel<8, 7, 1>: 8 rows x 7 slices of 2048 values per block (K = 14336);
+  // qmv1_slice_kernel<16, 7, 1>: 16 rows x 7 slices of 2048 values per block (K = 14336);
   // the launcher picks it for these shapes, and the stamp buffer is sized for it.
-  constexpr int RW = 8, KS = 7;
+  constexpr int RW = 16, KS = 7;
   if (K != 2048 * KS || N < 1 || N > (int64_t(1) << 20)) {
     std::printf("K must be %d and N in 1..2^20\n", 2048 * KS);
     return 1;
