@@ -524,10 +524,13 @@ static hipError_t launch_qmv1_slice(const QmmArgs& a, hipStream_t stream) {
     case 4: return launch_qmv1_slice_cfg<8, 4, 1>(a, stream);
     case 5: return launch_qmv1_slice_cfg<8, 5, 1>(a, stream);
     case 6: return launch_qmv1_slice_cfg<8, 6, 1>(a, stream);
-    // 14336-deep rows: 16 rows per wave, one 7-slice block per 16 rows (4096 x
-    // 14336 7.89-8.01 -> 7.64-7.68 us, 16384 x 14336 23.1-23.7 -> 22.4-22.5 us;
-    // 4 rows 8.0-8.1, 4 rows in two row groups 9.1-9.2 us).
-    case 7: return launch_qmv1_slice_cfg<16, 7, 1>(a, stream);
+    // 14336-deep rows: 16 rows per wave, one 7-slice block per 16 rows, up to 16384
+    // outputs (4096 x 14336 7.89-8.01 -> 7.64-7.68 us, 16384 x 14336 23.1-23.7 ->
+    // 22.3-22.6 us; 4 rows 8.0-8.1, 4 rows in two row groups 9.1-9.2 us); 8 rows
+    // on taller matrices (32768 x 14336: 41.8-41.9 against 42.9-43.2 us).
+    case 7:
+      if (a.N > 16384) return launch_qmv1_slice_cfg<8, 7, 1>(a, stream);
+      return launch_qmv1_slice_cfg<16, 7, 1>(a, stream);
     case 8: return launch_qmv1_slice_cfg<8, 8, 1>(a, stream);
     case 2:
       // 4 rows per wave from 8192 to 32767 outputs (14336 x 4096 7.64-7.98 ->

@@ -215,7 +215,8 @@ def test_qmvs_blocks_and_steps(gpu, oracle, M, N, K):
     (1001, 8192, False),   # four 2048-deep slices, rows not a multiple of the 8-row wave
     (77, 16384, True),     # eight slices (the largest block), bias epilogue
     (77, 32768, False),    # sixteen slices: not taken by the slice kernel
-    (264, 14336, False),   # the down-projection depth
+    (264, 14336, False),   # the down-projection depth (16-row waves)
+    (16392, 14336, True),  # past 16384 outputs: 8-row waves, ragged, bias epilogue
     (2056, 4096, True),    # two slices x two 8-row groups per block, ragged
     (1001, 4096, False),   # two slices x two 2-row groups per block
     (28680, 4096, False),  # two slices on a tall matrix (rows past 16384), ragged
