@@ -52,6 +52,11 @@ LLAMA_PROJ = [  # name, N (out), K (in): llama.go:403-428
     ("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
     ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336),
 ]
+# The same layer with the projections that read one x stored as one matrix (q|k|v,
+# gate|up): the same weight bytes in 4 launches instead of 7.  Not the reference's
+# call pattern (llama.go calls each projection); a labelled comparison only.
+FUSED_PROJ = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gateup", 28672, 4096),
+              ("down", 4096, 14336)]
 GROUP = 64
 PROFILES = os.path.join(ROOT, "profiles")
 ROOF_PMC = os.path.join(PROFILES, "qmv1_down_4096x14336_M1_traffic.md")
@@ -596,6 +601,30 @@ def main():
             extra[f"stack_M{M}_GBps"] = round(stack_bytes(M, L, bits) / (msM * 1e-3) / 1e9, 1)
             extra[f"stack_M{M}_ms"] = round(msM, 4)
             extra[f"stack_M{M}_frac_hbm"] = round(extra[f"stack_M{M}_GBps"] / HBM_PEAK_GBS, 4)
+
+        # labelled comparison: the stack at M = 1 with q|k|v and gate|up fused
+        fused = [{name: gen_quant(torch, N, K, bits, gen, dev) for name, N, K in FUSED_PROJ}
+                 for _ in range(L)]
+        xf = {K: torch.randn(1, K, device=dev, generator=gen).to(torch.bfloat16)
+              for K in (4096, 14336)}
+        of = {name: torch.empty(1, N, device=dev, dtype=torch.bfloat16)
+              for name, N, _ in FUSED_PROJ}
+
+        def fused_step():
+            for layer in fused:
+                for name, N, K in FUSED_PROJ:
+                    w, s, b = layer[name]
+                    ops.quantized_matmul(xf[K], w, s, b, True, GROUP, bits, out=of[name])
+        msf = time_graph(torch, capture(torch, fused_step), args.steps, args.warmup)
+        byf = L * sum(qmm_bytes(1, N, K, bits, GROUP) for _, N, K in FUSED_PROJ)
+        extra["stack_M1_fused_qkv_gateup"] = {
+            "ms": round(msf, 4), "GBps": round(byf / (msf * 1e-3) / 1e9, 1),
+            "frac_hbm": round(byf / (msf * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "launches_per_step": 4 * L,
+            "note": "q|k|v and gate|up weights stored as one matrix each (4 launches a layer "
+                    "instead of 7); not the reference's call pattern, a comparison of the "
+                    "launch count only"}
+        del fused
 
         ups = [layer[n] for layer in stack for n in ("gate", "up")]
         downs = [layer["down"] for layer in stack]
