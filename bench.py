@@ -52,11 +52,6 @@ LLAMA_PROJ = [  # name, N (out), K (in): llama.go:403-428
     ("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
     ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336),
 ]
-# The same layer with the projections that read one x stored as one matrix (q|k|v,
-# gate|up): the same weight bytes in 4 launches instead of 7.  Not the reference's
-# call pattern (llama.go calls each projection); a labelled comparison only.
-FUSED_PROJ = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gateup", 28672, 4096),
-              ("down", 4096, 14336)]
 GROUP = 64
 PROFILES = os.path.join(ROOT, "profiles")
 ROOF_PMC = os.path.join(PROFILES, "qmv1_down_4096x14336_M1_traffic.md")
@@ -602,29 +597,29 @@ def main():
             extra[f"stack_M{M}_ms"] = round(msM, 4)
             extra[f"stack_M{M}_frac_hbm"] = round(extra[f"stack_M{M}_GBps"] / HBM_PEAK_GBS, 4)
 
-        # labelled comparison: the stack at M = 1 with q|k|v and gate|up fused
-        fused = [{name: gen_quant(torch, N, K, bits, gen, dev) for name, N, K in FUSED_PROJ}
-                 for _ in range(L)]
-        xf = {K: torch.randn(1, K, device=dev, generator=gen).to(torch.bfloat16)
-              for K in (4096, 14336)}
-        of = {name: torch.empty(1, N, device=dev, dtype=torch.bfloat16)
-              for name, N, _ in FUSED_PROJ}
+        # labelled comparison: the same stack at M = 1 with q|k|v and gate|up each in one
+        # fmxq_quantized_matmul_group call (4 launches a layer instead of 7, same weights)
+        x4 = xs1[4096]
+        yq = {name: torch.empty(1, N, device=dev, dtype=torch.bfloat16)
+              for name, N, _ in LLAMA_PROJ}
 
-        def fused_step():
-            for layer in fused:
-                for name, N, K in FUSED_PROJ:
-                    w, s, b = layer[name]
-                    ops.quantized_matmul(xf[K], w, s, b, True, GROUP, bits, out=of[name])
-        msf = time_graph(torch, capture(torch, fused_step), args.steps, args.warmup)
-        byf = L * sum(qmm_bytes(1, N, K, bits, GROUP) for _, N, K in FUSED_PROJ)
-        extra["stack_M1_fused_qkv_gateup"] = {
-            "ms": round(msf, 4), "GBps": round(byf / (msf * 1e-3) / 1e9, 1),
-            "frac_hbm": round(byf / (msf * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        def grouped_step():
+            for layer in stack:
+                ops.quantized_matmul_group(x4, [layer["q"], layer["k"], layer["v"]], GROUP, bits,
+                                           outs=[yq["q"], yq["k"], yq["v"]])
+                ops.quantized_matmul(x4, *layer["o"], True, GROUP, bits, out=yq["o"])
+                ops.quantized_matmul_group(x4, [layer["gate"], layer["up"]], GROUP, bits,
+                                           outs=[yq["gate"], yq["up"]])
+                ops.quantized_matmul(xs1[14336], *layer["down"], True, GROUP, bits,
+                                     out=yq["down"])
+        msg = time_graph(torch, capture(torch, grouped_step), args.steps, args.warmup)
+        extra["stack_M1_grouped_qkv_gateup"] = {
+            "ms": round(msg, 4), "GBps": round(total_bytes / (msg * 1e-3) / 1e9, 1),
+            "frac_hbm": round(total_bytes / (msg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "launches_per_step": 4 * L,
-            "note": "q|k|v and gate|up weights stored as one matrix each (4 launches a layer "
-                    "instead of 7); not the reference's call pattern, a comparison of the "
-                    "launch count only"}
-        del fused
+            "note": "q|k|v and gate|up each through one fmxq_quantized_matmul_group call on "
+                    "the same separate weights (4 launches a layer instead of 7); not the "
+                    "reference's call pattern, a comparison of the launch count only"}
 
         ups = [layer[n] for layer in stack for n in ("gate", "up")]
         downs = [layer["down"] for layer in stack]

@@ -27,6 +27,8 @@ FMXQ_SYMBOLS = {
     "fmxq_quantized_matmul": (_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _bool, _int, _int, _p]),
     "fmxq_quantized_matmul_bias": (_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _bool, _int,
                                           _int, _p]),
+    "fmxq_quantized_matmul_group": (_int, [_p, _int, _p, _p, _p, _p, _p, _i64, _i64, _bool, _int,
+                                           _int, _p]),
     "fmxq_gather_qmm": (_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
                                _i64, _bool, _int, _int, _bool, _p]),
     "fmxq_device_error": (_int, [_p]),

@@ -435,6 +435,42 @@ int fmxq_quantized_matmul(const uint16_t* x, const uint32_t* w, const uint16_t* 
                     stream, "quantized_matmul");
 }
 
+int fmxq_quantized_matmul_group(const uint16_t* x, int n, const uint32_t* const* w,
+                                const uint16_t* const* scales, const uint16_t* const* biases,
+                                uint16_t* const* y, const int64_t* N, int64_t M, int64_t K,
+                                bool transpose, int group_size, int bits, void* stream) {
+  const char* op = "quantized_matmul_group";
+  if (n < 1 || n > fmxq::kSliceGroupMax)
+    return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: n=%d outside 1..%d", op, n, fmxq::kSliceGroupMax);
+  if (!w || !scales || !biases || !y || !N)
+    return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: null operand array", op);
+  if (int rc = check_quant(group_size, bits, K, transpose, op)) return rc;
+  if (M < 0) return fail(FMXQ_ERR_SHAPE, "%s: negative size M=%lld", op, (long long)M);
+  fmxq::QmmArgs mats[fmxq::kSliceGroupMax];
+  for (int i = 0; i < n; ++i) {
+    if (N[i] < 0)
+      return fail(FMXQ_ERR_SHAPE, "%s: negative size N[%d]=%lld", op, i, (long long)N[i]);
+    if (M > 0 && N[i] > 0) {
+      if (!x || !w[i] || !scales[i] || !biases[i] || !y[i])
+        return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: null operand of product %d", op, i);
+      if (!aligned16(x) || !aligned16(w[i]))
+        return fail(FMXQ_ERR_INVALID_ARGUMENT, "%s: x and w[%d] must be 16-byte aligned", op, i);
+    }
+    mats[i] = fmxq::QmmArgs{x, w[i], scales[i], biases[i], nullptr, y[i], M, N[i], K, K, N[i],
+                            group_size, bits};
+  }
+  if (M == 0) return FMXQ_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const hipError_t e = fmxq::launch_qmv1_slice_group(mats, n, s);
+  if (e != hipErrorNotSupported) return hip_status(e, op);
+  // Shapes the grouped launch does not take: one product at a time.
+  for (int i = 0; i < n; ++i)
+    if (int rc = qmm_common(x, w[i], scales[i], biases[i], nullptr, y[i], M, N[i], K, transpose,
+                            group_size, bits, stream, op))
+      return rc;
+  return FMXQ_OK;
+}
+
 int fmxq_quantized_matmul_bias(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
                                const uint16_t* biases, const uint16_t* bias, uint16_t* y,
                                int64_t M, int64_t N, int64_t K, bool transpose,

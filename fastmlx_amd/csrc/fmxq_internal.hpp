@@ -94,6 +94,9 @@ hipError_t launch_broadcast_index(const void* src, const IndexMap& m, uint32_t* 
 constexpr int kQmvMaxM = 4;
 bool qmv_supported(const QmmArgs& a);
 hipError_t launch_qmv(const QmmArgs& a, hipStream_t stream);
+// At most this many products of one x row in one grouped launch.
+constexpr int kSliceGroupMax = 4;
+hipError_t launch_qmv1_slice_group(const QmmArgs* mats, int n, hipStream_t stream);
 
 // MFMA GEMV for 5 <= M <= 32 (fmxq_skinny.hip): qmvs for int4 group 64 with K a
 // multiple of 256 and aligned operands, qmv_mfma for the other int4 (group_size

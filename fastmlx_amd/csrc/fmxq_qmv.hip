@@ -338,8 +338,10 @@ static hipError_t launch_qmv1(const QmmArgs& a, hipStream_t stream) {
 #define FMXQ_TL_STAMP(v) (void)0
 #define FMXQ_TL_AFTER(v, r) (void)0
 #endif
+// The kernel body for block bx of the product a (bx is blockIdx.x, or the block's
+// index within its matrix in the grouped launch below).
 template <int RW, int KS, int RG>
-__global__ __launch_bounds__(KS * RG * 64) void qmv1_slice_kernel(QmmArgs a) {
+__device__ __forceinline__ void qmv1_slice_body(const QmmArgs& a, int64_t bx) {
 #ifdef FMXQ_QMV1_TIMELINE
   uint64_t tl[5] = {};
 #endif
@@ -360,7 +362,7 @@ __global__ __launch_bounds__(KS * RG * 64) void qmv1_slice_kernel(QmmArgs a) {
   const int rg = wave / KS, ks = wave % KS;
   const int c = ks * 64 + lane;
   const int64_t wpr = a.K / 8, gpr = a.K / 64;
-  const int64_t nbase = ((int64_t)blockIdx.x * RG + rg) * RW;
+  const int64_t nbase = (bx * RG + rg) * RW;
   // Row indices in 32 bits (launch_qmv1_slice keeps N below 2^31), wave-uniform
   // for the weight rows: the clamp and the row offsets then stay on the scalar
   // unit (gfx9 has no 64-bit signed scalar compare, so an int64 clamp would move
@@ -383,7 +385,7 @@ __global__ __launch_bounds__(KS * RG * 64) void qmv1_slice_kernel(QmmArgs a) {
   if constexpr (BS) {
     if (tid < NPC) {
       const int n =
-          min(__builtin_amdgcn_readfirstlane((int)((int64_t)blockIdx.x * RG * RW)) + prow, nlast);
+          min(__builtin_amdgcn_readfirstlane((int)(bx * RG * RW)) + prow, nlast);
       const int64_t off = (int64_t)n * gpr + ppc * 8;
       ps[0] = *reinterpret_cast<const u32x4*>(a.scales + off);
       pb[0] = *reinterpret_cast<const u32x4*>(a.biases + off);
@@ -488,12 +490,36 @@ __global__ __launch_bounds__(KS * RG * 64) void qmv1_slice_kernel(QmmArgs a) {
   if (a.tl_stamps && lane == 0) {
     const uint32_t hw = __builtin_amdgcn_s_getreg((4 << 0) | (0 << 6) | (31 << 11));   // HW_ID
     const uint32_t xcc = __builtin_amdgcn_s_getreg((20 << 0) | (0 << 6) | (3 << 11));  // XCC_ID
-    uint64_t* o = a.tl_stamps + 6 * ((int64_t)blockIdx.x * (KS * RG) + wave);
+    uint64_t* o = a.tl_stamps + 6 * (bx * (KS * RG) + wave);
 #pragma unroll
     for (int i = 0; i < 5; ++i) o[i] = tl[i];
     o[5] = ((uint64_t)xcc << 32) | hw;
   }
 #endif
+}
+
+template <int RW, int KS, int RG>
+__global__ __launch_bounds__(KS * RG * 64) void qmv1_slice_kernel(QmmArgs a) {
+  qmv1_slice_body<RW, KS, RG>(a, blockIdx.x);
+}
+
+// Several products of one x row in one launch (fmxq_quantized_matmul_group): block
+// b belongs to matrix i when first[i] <= b < first[i + 1], and runs that matrix's
+// block b - first[i].  The matrix index is uniform over the block.
+struct SliceGroup {
+  QmmArgs m[kSliceGroupMax];
+  int64_t first[kSliceGroupMax + 1];
+  int n;
+};
+template <int RW, int KS, int RG>
+__global__ __launch_bounds__(KS * RG * 64) void qmv1_slice_group_kernel(SliceGroup g) {
+  const int64_t b = blockIdx.x;
+  int i = 0;
+#pragma unroll
+  for (int j = 1; j < kSliceGroupMax; ++j)
+    if (j < g.n && b >= g.first[j]) i = j;
+  i = __builtin_amdgcn_readfirstlane(i);
+  qmv1_slice_body<RW, KS, RG>(g.m[i], b - g.first[i]);
 }
 
 template <int RW, int KS, int RG>
@@ -508,40 +534,57 @@ static hipError_t launch_qmv1_slice_cfg(const QmmArgs& a, hipStream_t stream) {
 // K = 4096 at every height (4.2 -> 3.9 us for 4096 x 4096; 8.1 -> 7.8 us for
 // 14336 x 4096 once the scales load as block runs; 28672 x 4096 12.4-12.8 ->
 // 12.1 us; the 128256 x 4096 tied head 47.7-48.4 -> 43.7-44.4 us, 85% of HBM).
-static hipError_t launch_qmv1_slice(const QmmArgs& a, hipStream_t stream) {
-  if (a.M != 1 || a.bits != 4 || a.group_size != 64 || a.K % 2048 != 0 ||
-      a.N >= (int64_t(1) << 31))
-    return hipErrorNotSupported;
-  if ((reinterpret_cast<uintptr_t>(a.scales) & 15u) || (reinterpret_cast<uintptr_t>(a.biases) & 15u) ||
-      (reinterpret_cast<uintptr_t>(a.x) & 15u) || (reinterpret_cast<uintptr_t>(a.w) & 15u))
-    return hipErrorNotSupported;
-  switch (a.K / 2048) {
+// The slice kernel's shape for rows of depth K and N outputs: launch(RW, KS, RG)
+// with the three as integral constants, or hipErrorNotSupported.
+template <class L>
+static hipError_t with_slice_shape(int64_t K, int64_t N, L&& launch) {
+  using std::integral_constant;
+  auto go = [&](auto rw, auto ks, auto rg) { return launch(rw, ks, rg); };
+  switch (K / 2048) {
     // One slice (2048-deep rows): 2 rows per wave, 4 waves per block, no cross-slice
     // sum (against the qmvx GEMV: 2048 x 2048 2.89 -> 2.60 us, 512 x 2048 2.54 ->
     // 2.25 us, 8192 x 2048 4.20 -> 4.07 us; 1 or 4 rows per wave, or 2 waves per
     // block, measured in between).
-    case 1: return launch_qmv1_slice_cfg<2, 1, 4>(a, stream);
-    case 4: return launch_qmv1_slice_cfg<8, 4, 1>(a, stream);
-    case 5: return launch_qmv1_slice_cfg<8, 5, 1>(a, stream);
-    case 6: return launch_qmv1_slice_cfg<8, 6, 1>(a, stream);
+    case 1: return go(integral_constant<int, 2>{}, integral_constant<int, 1>{}, integral_constant<int, 4>{});
+    case 4: return go(integral_constant<int, 8>{}, integral_constant<int, 4>{}, integral_constant<int, 1>{});
+    case 5: return go(integral_constant<int, 8>{}, integral_constant<int, 5>{}, integral_constant<int, 1>{});
+    case 6: return go(integral_constant<int, 8>{}, integral_constant<int, 6>{}, integral_constant<int, 1>{});
     // 14336-deep rows: 16 rows per wave, one 7-slice block per 16 rows, up to 16384
     // outputs (4096 x 14336 7.89-8.01 -> 7.64-7.68 us, 16384 x 14336 23.1-23.7 ->
     // 22.3-22.6 us; 4 rows 8.0-8.1, 4 rows in two row groups 9.1-9.2 us); 8 rows
     // on taller matrices (32768 x 14336: 41.8-41.9 against 42.9-43.2 us).
     case 7:
-      if (a.N > 16384) return launch_qmv1_slice_cfg<8, 7, 1>(a, stream);
-      return launch_qmv1_slice_cfg<16, 7, 1>(a, stream);
-    case 8: return launch_qmv1_slice_cfg<8, 8, 1>(a, stream);
+      if (N > 16384)
+        return go(integral_constant<int, 8>{}, integral_constant<int, 7>{}, integral_constant<int, 1>{});
+      return go(integral_constant<int, 16>{}, integral_constant<int, 7>{}, integral_constant<int, 1>{});
+    case 8: return go(integral_constant<int, 8>{}, integral_constant<int, 8>{}, integral_constant<int, 1>{});
     case 2:
       // 4 rows per wave from 8192 to 32767 outputs (14336 x 4096 7.64-7.98 ->
       // 7.45-7.49 us, the C1 stack at M = 1 1.178 -> 1.165 ms); 8 below and above
       // (4096 x 4096 3.80 against 4.01 us, the 128256-row head 44.0-44.4 against
       // 45.1 us).
-      if (a.N >= 8192 && a.N < 32768) return launch_qmv1_slice_cfg<4, 2, 2>(a, stream);
-      return a.N >= 2048 ? launch_qmv1_slice_cfg<8, 2, 2>(a, stream)
-                         : launch_qmv1_slice_cfg<2, 2, 2>(a, stream);
+      if (N >= 8192 && N < 32768)
+        return go(integral_constant<int, 4>{}, integral_constant<int, 2>{}, integral_constant<int, 2>{});
+      if (N >= 2048)
+        return go(integral_constant<int, 8>{}, integral_constant<int, 2>{}, integral_constant<int, 2>{});
+      return go(integral_constant<int, 2>{}, integral_constant<int, 2>{}, integral_constant<int, 2>{});
     default: return hipErrorNotSupported;
   }
+}
+
+static bool slice_supported(const QmmArgs& a) {
+  return a.M == 1 && a.bits == 4 && a.group_size == 64 && a.K % 2048 == 0 &&
+         a.N < (int64_t(1) << 31) && !(reinterpret_cast<uintptr_t>(a.scales) & 15u) &&
+         !(reinterpret_cast<uintptr_t>(a.biases) & 15u) && !(reinterpret_cast<uintptr_t>(a.x) & 15u) &&
+         !(reinterpret_cast<uintptr_t>(a.w) & 15u);
+}
+
+static hipError_t launch_qmv1_slice(const QmmArgs& a, hipStream_t stream) {
+  if (!slice_supported(a)) return hipErrorNotSupported;
+  return with_slice_shape(a.K, a.N, [&](auto rw, auto ks, auto rg) {
+    return launch_qmv1_slice_cfg<decltype(rw)::value, decltype(ks)::value, decltype(rg)::value>(
+        a, stream);
+  });
 }
 
 struct QmvxShape {
@@ -815,6 +858,39 @@ static hipError_t launch_qmv_bits(const QmmArgs& a, hipStream_t stream) {
 
 bool qmv_supported(const QmmArgs& a) {
   return a.M <= kQmvMaxM || qmvx_supported(a, a.bits);
+}
+
+// Several products of one x row in one launch: every matrix M = 1, int4 group 64,
+// the same K and x, the slice kernel's alignment; the shape is the one a single
+// matrix of all their rows would take (q | k | v of 4096 + 1024 + 1024 rows: 8 rows
+// per wave; gate | up of 2 x 14336: 4).  hipErrorNotSupported otherwise.
+hipError_t launch_qmv1_slice_group(const QmmArgs* mats, int n, hipStream_t stream) {
+  if (n < 1 || n > kSliceGroupMax) return hipErrorNotSupported;
+  SliceGroup g{};
+  g.n = n;
+  int64_t total = 0;
+  for (int i = 0; i < n; ++i) {
+    const QmmArgs& a = mats[i];
+    if (!slice_supported(a) || a.K != mats[0].K || a.x != mats[0].x || a.N < 0)
+      return hipErrorNotSupported;
+    g.m[i] = a;
+    total += a.N;
+  }
+  if (total >= (int64_t(1) << 31)) return hipErrorNotSupported;
+  if (total == 0) return hipSuccess;
+  return with_slice_shape(mats[0].K, total, [&](auto rw, auto ks, auto rg) -> hipError_t {
+    constexpr int RW = decltype(rw)::value, KS = decltype(ks)::value, RG = decltype(rg)::value;
+    constexpr int64_t rows = RW * RG;
+    int64_t b = 0;
+    for (int i = 0; i < n; ++i) {
+      g.first[i] = b;
+      b += (g.m[i].N + rows - 1) / rows;
+    }
+    for (int i = n; i <= kSliceGroupMax; ++i) g.first[i] = b;
+    if (b == 0) return hipSuccess;
+    qmv1_slice_group_kernel<RW, KS, RG><<<(unsigned)b, KS * RG * 64, 0, stream>>>(g);
+    return hipGetLastError();
+  });
 }
 
 hipError_t launch_qmv(const QmmArgs& a, hipStream_t stream) {

@@ -88,6 +88,32 @@ def quantized_matmul(x, w, scales, biases, transpose: bool = True, group_size: i
     return out
 
 
+def quantized_matmul_group(x, mats, group_size: int = 64, bits: int = 4, outs=None):
+    """Several products of the same x [..., K]: mats is a list of (w, scales, biases)
+    triples (1 to 4), the result a list of y [..., N_i] bf16 (one launch where the
+    shapes allow, fmxq_quantized_matmul_group)."""
+    import ctypes
+
+    K = x.shape[-1]
+    M = x.numel() // max(K, 1)
+    n = len(mats)
+    for w, _, _ in mats:
+        if w.shape[-1] * 32 // bits != K:
+            raise ValueError(f"x has K={K} but w packs {w.shape[-1] * 32 // bits} values per row")
+    if outs is None:
+        outs = [torch.empty(*x.shape[:-1], w.shape[0], dtype=torch.bfloat16, device=x.device)
+                for w, _, _ in mats]
+    P = ctypes.c_void_p * n
+    ws = P(*[_dev(w, "w", _U32_LIKE) for w, _, _ in mats])
+    ss = P(*[_dev(s, "scales", _BF16_LIKE) for _, s, _ in mats])
+    bs = P(*[_dev(b, "biases", _BF16_LIKE) for _, _, b in mats])
+    ys = P(*[_dev(y, "out", _BF16_LIKE) for y in outs])
+    Ns = (ctypes.c_int64 * n)(*[w.shape[0] for w, _, _ in mats])
+    check(load().fmxq_quantized_matmul_group(_dev(x, "x", _BF16_LIKE), n, ws, ss, bs, ys, Ns, M, K,
+                                             True, group_size, bits, _stream(x)))
+    return outs
+
+
 def gather_qmm(x, w, scales, biases, rhs_indices, lhs_indices=None, lhs_div: int = 1,
                transpose: bool = True, group_size: int = 64, bits: int = 4,
                sorted_indices: bool = False, out=None):

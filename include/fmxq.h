@@ -88,6 +88,19 @@ int fmxq_quantized_matmul(const uint16_t* x, const uint32_t* w, const uint16_t* 
                           const uint16_t* biases, uint16_t* y, int64_t M, int64_t N,
                           int64_t K, bool transpose, int group_size, int bits, void* stream);
 
+/* No counterpart in the reference: n quantized_matmul products that read the same
+ * x, for the projections a model computes from one activation (q, k and v; gate
+ * and up), in one launch where the shapes allow (M = 1, int4 group 64, K a multiple
+ * of 2048, 16-byte aligned operands) and one launch each otherwise.  Product i is
+ * y[i] [M, N[i]] = x [M, K] . deq(w[i], scales[i], biases[i])^T with the operands of
+ * fmxq_quantized_matmul; 1 <= n <= 4.  The values agree with fmxq_quantized_matmul's
+ * to the same tolerance, not bit for bit: a grouped launch picks its wave shape from
+ * the group's total rows, which can change the order of a row's sum. */
+int fmxq_quantized_matmul_group(const uint16_t* x, int n, const uint32_t* const* w,
+                                const uint16_t* const* scales, const uint16_t* const* biases,
+                                uint16_t* const* y, const int64_t* N, int64_t M, int64_t K,
+                                bool transpose, int group_size, int bits, void* stream);
+
 /* qlinearBias (compute/models/quant.go:105-111): quantized_matmul followed by a
  * broadcast add of the additive bias [N] (bf16), fused into the epilogue with
  * the op chain's rounding: bf16(bf16(x . deq(W)^T) + bias).  bias may be NULL. */

@@ -473,3 +473,56 @@ def test_zero_sizes_enqueue_nothing(gpu):
     lib = _lib.load()
     assert lib.fmxq_quantized_matmul(None, None, None, None, None, 0, 16, 64, True, 64, 4,
                                      None) == 0
+
+
+@pytest.mark.parametrize("M,Ns,K,bits,group", [
+    (1, (4096, 1024, 1024), 4096, 4, 64),   # q | k | v of the C1 stack: one grouped launch
+    (1, (14336, 14336), 4096, 4, 64),       # gate | up: one launch, 4-row waves by the total
+    (1, (4096,), 14336, 4, 64),             # one product, 14336-deep rows
+    (1, (1030, 0, 77, 2050), 2048, 4, 64),  # four products, an empty one, ragged rows, 1 slice
+    (2, (1024, 512), 4096, 4, 64),          # M = 2: one launch per product
+    (1, (1024, 2048), 4096, 8, 64),         # int8: one launch per product
+    (1, (1024, 520), 6144, 4, 64),          # three slices: one launch per product
+])
+def test_quantized_matmul_group(gpu, oracle, M, Ns, K, bits, group):
+    """fmxq_quantized_matmul_group: every product checked element by element against
+    the fp64 oracle and by the 2e-2 metric, and against fmxq_quantized_matmul of the
+    same product (equal where both run the same wave shape, within the tolerance
+    otherwise)."""
+    import parity
+    from fastmlx_amd import ops
+
+    rng = np.random.default_rng(7000 + M + K + sum(Ns))
+    x = make_x(rng, M, K)
+    mats = [make_quant(rng, (N,), K, bits, group) for N in Ns]
+    announce(f"quantized_matmul_group M={M} Ns={Ns} K={K} bits={bits}")
+    dx = to_dev(x, gpu)
+    dm = [tuple(to_dev(t, gpu) for t in m) for m in mats]
+    ys = ops.quantized_matmul_group(dx, dm, group, bits)
+    singles = [ops.quantized_matmul(dx, *m, True, group, bits) for m in dm]
+    torch.cuda.synchronize()
+    for i, (N, (w, s, b)) in enumerate(zip(Ns, mats)):
+        got = to_np(ys[i])
+        assert got.shape == (M, N)
+        if N == 0:
+            continue
+        ref = parity.DenseRef(np.ascontiguousarray(x), w, s, b, group, bits)
+        parity.check_dense(got, ref, what=f"group product {i}: M={M} N={N} K={K}")
+        e = rel_err(oracle.bf16_to_f32(got), ref.mlx)
+        assert e < 2e-2, e
+        one = oracle.bf16_to_f32(to_np(singles[i]))
+        assert rel_err(oracle.bf16_to_f32(got), one) < 2e-2
+
+
+def test_quantized_matmul_group_validation(gpu):
+    """Refusals before any launch: n outside 1..4, and K / w disagreeing."""
+    from fastmlx_amd import ops
+
+    rng = np.random.default_rng(3)
+    x = to_dev(make_x(rng, 1, 2048), gpu)
+    m = tuple(to_dev(t, gpu) for t in make_quant(rng, (64,), 2048, 4, 64))
+    with pytest.raises(Exception):
+        ops.quantized_matmul_group(x, [m] * 5)
+    m4 = tuple(to_dev(t, gpu) for t in make_quant(rng, (64,), 4096, 4, 64))
+    with pytest.raises(ValueError):
+        ops.quantized_matmul_group(x, [m, m4])
