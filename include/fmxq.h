@@ -11,7 +11,10 @@
  *   fmxq_gather_qmm        <- mlx_gather_qmm        (mlxgo/binding_cgo.go:645-673)
  *   fmxq_dequantize        <- mlx_dequantize        (mlxgo/binding_cgo.go:675-682)
  *   fmxq_quantize          <- mlx_quantize          (mlxgo/binding_cgo.go:684-697)
- * The array-handle layer with mlx-c's exact argument lists is in fmx.h.
+ * The array-handle layer with mlx-c's exact argument lists is in fmx.h.  The other
+ * entries (SwitchGLU and the MoE layer, the routers, the grouped product and the
+ * allocation-free SwitchGLU) fuse what the reference's callers compose from those
+ * calls, or have no counterpart; each declaration says which.
  *
  * Data layout (MLX affine quantization):
  *   x       [M, K] bf16 (uint16 bit patterns), row-major
