@@ -526,3 +526,42 @@ def test_quantized_matmul_group_validation(gpu):
     m4 = tuple(to_dev(t, gpu) for t in make_quant(rng, (64,), 4096, 4, 64))
     with pytest.raises(ValueError):
         ops.quantized_matmul_group(x, [m, m4])
+
+
+def test_quantized_matmul_group_graph_replay(gpu):
+    """The grouped launch (its matrix table travels in the kernel arguments) captured
+    in a HIP graph: every replay, with eager calls between them, equals the eager
+    result bit for bit."""
+    from fastmlx_amd import ops
+
+    rng = np.random.default_rng(11)
+    x = to_dev(make_x(rng, 1, 4096), gpu)
+    mats = [tuple(to_dev(t, gpu) for t in make_quant(rng, (N,), 4096, 4, 64))
+            for N in (4096, 1024, 1024)]
+    outs = [torch.empty(1, w.shape[0], dtype=torch.bfloat16, device=gpu) for w, _, _ in mats]
+
+    def step():
+        ops.quantized_matmul_group(x, mats, 64, 4, outs=outs)
+
+    announce("graph capture of quantized_matmul_group")
+    step()
+    torch.cuda.synchronize()
+    eager = [to_np(y).copy() for y in outs]
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=side):
+        step()
+    for rep in range(3):
+        for y in outs:
+            y.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for y, e in zip(outs, eager):
+            assert np.array_equal(to_np(y), e), f"replay {rep} differs from eager"
+        step()
+        torch.cuda.synchronize()
